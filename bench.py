@@ -1,0 +1,272 @@
+"""Benchmark of the quantized-inference hot path on one MI355X.
+
+Headline line (value): W8A8 prefill GEMM, M=2048 K=4096 N=14336, int8 x int8 ->
+int32 -> fp32 per-channel/per-row dequant epilogue, inputs resident in HBM, in
+TOPS (2*M*N*K int ops per step). The same JSON line carries the roofline of that
+kernel, the CPU baseline (the oracle's AVX-512 VNNI igemm path on a bounded row
+sample) and the other configurations as `components`: decode GEMV (GB/s, weight
+buffers rotated past the 256 MB MALL), ternary GEMM (TOPS) and the RotorQuant
+K+V round trip (GB/s).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "rust-neural-network_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "W8A8 GEMM TOPS (% int8 MFMA peak); GEMV & RotorQuant GB/s (% HBM peak)"
+PEAK_INT8_TOPS = 5033.0   # MI355X dense int8 MFMA (datasheet, no sparsity)
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed(fn, steps, warmup):
+    """Average ms per call of fn() over `steps` calls after `warmup` calls,
+    measured with events on the current stream (the stream the C ABI launches
+    on), bracketed by device synchronisation."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def gen_f32(shape, seed, dev, scale=1.0):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+    return x * scale if scale != 1.0 else x
+
+
+def traffic_for(name):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f).get(name)
+        return None if t is None else t.get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+# ---------------------------------------------------------------- prefill
+def bench_prefill(H, W, dev, steps, warmup):
+    import torch
+    c = W.PREFILL
+    m, k, n = c["m"], c["k"], c["n"]
+    w = gen_f32((n, k), 1, dev, 0.02)
+    wq, sw = H.quant_rows_i8(w)
+    del w
+    x = gen_f32((m, k), 2, dev)
+    aq, sa = H.quant_rows_i8(x)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    fn = lambda: H.w8a8_linear(aq, sa, wq, sw, y=y)  # noqa: E731
+    ms = timed(fn, steps, warmup)
+    ops = 2.0 * m * n * k
+    tops = ops / (ms * 1e-3) / 1e12
+    state = dict(aq=aq, sa=sa, wq=wq, sw=sw, m=m, k=k, n=n)
+    return ms, tops, state
+
+
+# ---------------------------------------------------------------- GEMV
+def bench_gemv(H, W, dev, steps):
+    import torch
+    out = {}
+    for (m, k, n) in W.GEMV_SHAPES:
+        wbytes = k * n
+        copies = max(2, -(-640 * 2**20 // wbytes))  # > 2.5x the 256 MB MALL
+        ws, sws = [], []
+        for i in range(copies):
+            wq, sw = H.quant_rows_i8(gen_f32((n, k), 100 + i, dev, 0.02))
+            ws.append(wq)
+            sws.append(sw)
+        x = gen_f32((m, k), 7, dev)
+        mask = torch.rand((m, k), generator=torch.Generator(device=dev).manual_seed(8),
+                          device=dev) < 0.01
+        x = torch.where(mask, x * 20.0, x)
+        aq, sa = H.quant_rows_i8(x)
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        it = [0]
+
+        def fn():
+            i = it[0] % copies
+            it[0] += 1
+            H.w8a8_linear(aq, sa, ws[i], sws[i], y=y)
+
+        iters = max(steps, 200)
+        ms = timed(fn, iters, 20)
+        nbytes = k * n + 4 * n + m * k + 4 * m + 4 * m * n
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"m{m}_k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+                                  "weight_copies": copies}
+        del ws, sws
+        torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------- ternary
+def bench_ternary(H, W, dev, steps):
+    import torch
+    c = W.TERNARY
+    m, k, n = c["m"], c["k"], c["n"]
+    packed, scales = H.ternary_quantize(gen_f32((n, k), 3, dev), H.TERNARY_ABSMEAN)
+    aq, sa = H.quant_rows_i8(gen_f32((m, k), 4, dev))
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    ms = timed(lambda: H.ternary_gemm(aq, sa, packed, scales, n, y=y), max(steps, 100), 10)
+    ops = 2.0 * m * n * k
+    tops = ops / (ms * 1e-3) / 1e12
+    nbytes = n * k // 4 + 4 * n + m * k + 4 * m + 4 * m * n
+    return {"us": round(ms * 1e3, 3), "TOPS": round(tops, 1),
+            "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4), "ops": ops, "bytes": nbytes}
+
+
+# ---------------------------------------------------------------- RotorQuant
+def bench_rotorquant(H, W, dev, steps):
+    import torch
+    c = W.ROTORQUANT
+    shape = (c["batch"], c["heads"], c["seq"], c["head_dim"])
+    dim, bits = c["head_dim"], c["bits"]
+    ng = (dim + 2) // 3
+    kv, outs, rots = [], [], []
+    for which, seed in (("K", 11), ("V", 12)):
+        x = gen_f32(shape, seed, dev)
+        ch = torch.as_tensor(W.kv_outlier_channels(dim, seed), device=dev)
+        x[..., ch] *= 10.0
+        kv.append(x)
+        outs.append(torch.empty_like(x))
+        rots.append(torch.from_numpy(W.rotors(ng, seed)).to(dev))
+
+    def step():
+        for x, y, r in zip(kv, outs, rots):
+            H.rotorquant_quantize(x, r, bits, y=y)
+
+    ms = timed(step, max(steps // 2, 10), 3)
+    nbytes = sum(2 * x.numel() * 4 for x in kv)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_step": nbytes,
+            "launches_per_step": 2}
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(state, sample_rows=256, repeats=3):
+    """The reference CPU path for the prefill GEMM on the first `sample_rows`
+    rows: igemm (src/int8.rs:285-314: VNNI, B repacked per call, 4-row blocks
+    over threads) on a_u8 = a_s8 + 128 and B = W^T, then the zero-point
+    correction and the per-row/per-channel dequant epilogue."""
+    import numpy as np
+
+    import oracle as O
+    k, n = state["k"], state["n"]
+    aq = state["aq"][:sample_rows].cpu().numpy()
+    sa = state["sa"][:sample_rows].cpu().numpy()
+    wq = state["wq"].cpu().numpy()
+    sw = state["sw"].cpu().numpy()
+    b_kn = np.ascontiguousarray(wq.T)                   # weight layout prep, not timed
+    colsum128 = 128 * b_kn.astype(np.int64).sum(axis=0).astype(np.int32)
+    threads = max(1, min(16, os.cpu_count() or 1))
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        a_u8 = (aq.view(np.uint8) ^ np.uint8(0x80))
+        c, used_vnni = O.igemm(a_u8, b_kn, sample_rows, k, n, threads)
+        acc = (c - colsum128).astype(np.int32)
+        y = (acc.astype(np.float32) * sa[:, None]) * sw[None, :]
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    ops = 2.0 * sample_rows * n * k
+    return {"value": round(ops / t / 1e12, 4), "unit": "TOPS", "cores": threads,
+            "kind": "port",
+            "sample": f"W8A8 prefill rows 0..{sample_rows} of 2048 (x{k}x{n}), "
+                      f"igemm {'AVX-512 VNNI' if used_vnni else 'scalar'} incl. per-call B "
+                      f"repack, median of {repeats}, {t * 1e3:.1f} ms",
+            "y_checksum": float(np.float64(y).sum())}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default="all",
+                    choices=["all", "prefill", "gemv", "ternary", "rotorquant"])
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import rnn_hip as H
+    import workloads as W
+    H.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+              "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)"}
+    components = {}
+    if args.only in ("all", "prefill"):
+        log("prefill: W8A8 2048x4096x14336")
+        ms, tops, state = bench_prefill(H, W, dev, args.steps, args.warmup)
+        ops = 2.0 * state["m"] * state["n"] * state["k"]
+        result.update({
+            "value": round(tops, 2), "unit": "TOPS", "ms_per_step": round(ms, 5),
+            "config": {"workload": "w8a8_prefill_gemm", "m": state["m"], "k": state["k"],
+                       "n": state["n"], "out": "fp32", "epilogue": "(acc*sa[m])*sw[n]",
+                       "baseline_config_index": 2},
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS,
+                         "unit": "TOPS", "frac": round(tops / PEAK_INT8_TOPS, 4),
+                         "traffic": traffic_for("w8a8_prefill_gemm"),
+                         "ops_per_launch": ops,
+                         "kernel": "gemm_tiled_kernel (v_mfma_i32_16x16x64_i8)"},
+        })
+        if not args.no_cpu:
+            log("cpu baseline: oracle igemm on a row sample")
+            result["cpu_baseline"] = cpu_baseline(state)
+        del state
+        torch.cuda.empty_cache()
+    if args.only in ("all", "gemv"):
+        log("decode GEMV: 6 shapes")
+        components["w8a8_decode_gemv"] = bench_gemv(H, W, dev, args.steps)
+    if args.only in ("all", "ternary"):
+        log("ternary GEMM 512x4096x4096")
+        components["ternary_gemm"] = bench_ternary(H, W, dev, args.steps)
+    if args.only in ("all", "rotorquant"):
+        log("RotorQuant K+V [8,32,4096,128] 4-bit round trip")
+        components["rotorquant_kv"] = bench_rotorquant(H, W, dev, args.steps)
+    if components:
+        result["components"] = components
+    if "value" not in result:  # a single non-headline component was requested
+        result.update({"value": None, "unit": None, "ms_per_step": None,
+                       "config": {"workload": args.only}})
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,174 @@
+/*
+ * rnn_hip.h -- C ABI of the MI355X (gfx950) quantized-inference path of
+ * rust-nn (gugu8intel-i9/Rust-Neural-Network): W8A8 int8 GEMM/GEMV, 2-bit
+ * ternary matmul and RotorQuant KV quantize/dequantize.
+ *
+ * Conventions
+ *  - Every tensor pointer is a DEVICE pointer (HBM) on the current HIP device.
+ *    Matrices are row-major and dense; sizes are element counts.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream). Calls
+ *    are asynchronous on that stream; results are visible after it syncs.
+ *  - Return value: RNN_OK (0) or an RNN_ERR_* code; rnn_last_error() gives the
+ *    calling thread's message. The reference panics on the same conditions
+ *    (e.g. src/int8.rs:72, src/quant.rs:136,215-220); a Rust binding maps a
+ *    non-zero status to panic!.
+ *  - Thread safety: no global mutable state apart from the per-thread error
+ *    string; concurrent calls on different streams are independent.
+ *  - Numerics follow the reference exactly: IEEE division, round half away
+ *    from zero (f32::round), no FMA contraction, wrapping int32 accumulation,
+ *    epilogue ((float)acc * s1) * s2 + bias in that order.
+ * Each declaration names the reference interface it replaces (file:line).
+ */
+#ifndef RNN_HIP_H
+#define RNN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RNN_HIP_ABI_VERSION 1
+
+enum rnn_status {
+    RNN_OK = 0,
+    RNN_ERR_INVALID_ARG = 1, /* null pointer, bad size, bad flag            */
+    RNN_ERR_HIP = 2,         /* a HIP runtime call or kernel launch failed   */
+    RNN_ERR_UNSUPPORTED = 3, /* shape/alignment this entry point cannot take */
+    RNN_ERR_OUT_OF_MEMORY = 4
+};
+
+/* flags for the GEMM entry points */
+#define RNN_FLAG_RELU 0x1u          /* y = max(y, 0) after bias (src/tensor.rs:2025-2032) */
+#define RNN_ALGO_AUTO 0x00u         /* GEMV for m <= 16, MFMA tiles otherwise */
+#define RNN_ALGO_TILED 0x10u        /* force the MFMA tiled GEMM              */
+#define RNN_ALGO_GEMV 0x20u         /* force the skinny GEMV (m <= 16)        */
+#define RNN_ALGO_MASK 0xF0u
+
+int rnn_abi_version(void);
+const char *rnn_last_error(void);
+
+/* ------------------------------------------------------------ int8 (a1-a6) */
+
+/* Per-row symmetric int8: scale[r] = max_j|x[r,j]|/127 (1.0 for an all-zero
+ * row), q = (x/scale).round().clamp(-128,127).
+ * Replaces Int8Weights::quantize (src/int8.rs:24-52) when x is a weight
+ * [out,in], and is the per-row dynamic activation rule of
+ * QuantizedTensor::quantize_int8 with group_size=cols (src/quantize.rs:296-322). */
+int rnn_quant_rows_i8(const float *x, int64_t rows, int64_t cols, int8_t *q,
+                      float *scale, void *stream);
+
+/* w[r,j] = q[r,j] as f32 * scale[r].  Int8Weights::dequantize (src/int8.rs:55-65) */
+int rnn_int8_dequantize(const int8_t *q, const float *scale, int64_t rows,
+                        int64_t cols, float *w, void *stream);
+
+/* Int8Weights::matmul_f32 (src/int8.rs:70-88): y[m,o] =
+ * (sum_k i8((x*(1/s[o])).round().clamp) * wq[o,k]) as f32 * s[o] * s[o]. */
+int rnn_int8_matmul_f32(const int8_t *wq, const float *ws, int64_t out_f,
+                        int64_t in_f, const float *x, int64_t m, float *y,
+                        void *stream);
+
+/* Int8Linear::forward (src/int8.rs:134-172), reference semantics: the
+ * activation is quantized with the weight's channel scale inside the output
+ * loop; y = acc as f32 * s[o] * s[o] (+ bias[o]). bias may be NULL. */
+int rnn_int8_linear_forward(const float *x, int64_t batch, int64_t in_f,
+                            const int8_t *wq, const float *ws, int64_t out_f,
+                            const float *bias, float *y, void *stream);
+
+/* Device workspace rnn_igemm needs (bytes); 0 for m, n or k == 0. */
+size_t rnn_igemm_workspace_size(int64_t m, int64_t k, int64_t n);
+
+/* igemm (src/int8.rs:285-314) / igemm_scalar (:222-234): c[m,n] = sum_k
+ * a_u8[m,k] * b_i8[k,n] in wrapping int32; a is UNSIGNED [m,k], b SIGNED
+ * [k,n] (N-contiguous). Computed on signed int8 MFMA with the exact identity
+ * sum (a_s8+128)*b = sum a_s8*b + 128*colsum(b). `workspace` must hold
+ * rnn_igemm_workspace_size() bytes, or be NULL to let the call allocate and
+ * free stream-ordered memory. */
+int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m,
+              int64_t k, int64_t n, void *workspace, size_t workspace_bytes,
+              void *stream);
+
+/* W8A8 linear (the igemm contract's "caller applies scales"
+ * step of src/int8.rs:283-284 fused into the GEMM store, in the multiply
+ * order of src/int8.rs:159-162):
+ *   acc[m,n] = sum_k aq[m,k]*wq[n,k]   (wrapping int32)
+ *   y[m,n]   = ((float)acc * sa[m]) * sw[n] (+ bias[n]) (relu if flagged)
+ * aq [m,k] int8 row quantized (rnn_quant_rows_i8), wq [n,k] int8 (the
+ * Int8Weights layout, src/int8.rs:14-17), k must be a multiple of 16.
+ * bias, y and acc_out may each be NULL (not both y and acc_out). */
+int rnn_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *wq,
+                    const float *sw, const float *bias, int64_t m, int64_t k,
+                    int64_t n, unsigned flags, float *y, int32_t *acc_out,
+                    void *stream);
+
+/* ---------------------------------------------------------- ternary (a7-a9) */
+
+/* pack_ternary (src/ternary.rs:46-60): 16 codes per u32, LSB first,
+ * 0 -> 00, >0 -> 01, <0 -> 10; packed holds ceil(count/16) words. */
+int rnn_ternary_pack(const int8_t *t, int64_t count, uint32_t *packed,
+                     void *stream);
+/* unpack_ternary (src/ternary.rs:63-75); code 11 decodes to 0. */
+int rnn_ternary_unpack(const uint32_t *packed, int64_t count, int8_t *t,
+                       void *stream);
+
+#define RNN_TERNARY_ROWS 0    /* TernaryTensor::quantize rule (src/ternary.rs:97-137) */
+#define RNN_TERNARY_ABSMEAN 1 /* per-tensor absmean gamma (BitNet b1.58), broadcast */
+
+/* Quantize w [rows,cols] to packed ternary (flat row-major codes, as
+ * TernaryTensor::packed) and scales [rows]. ROWS: delta = 0.7*mean|w|,
+ * scale = max(mean|w|,1e-8) per row, sums sequential in k (bit-exact).
+ * ABSMEAN: gamma = max(mean|w|,1e-8) over the tensor (row sums in f32 added
+ * in double), t = round(w/gamma).clamp(-1,1), scales[r] = gamma. */
+int rnn_ternary_quantize(const float *w, int64_t rows, int64_t cols, int mode,
+                         uint32_t *packed, float *scales, void *stream);
+
+/* TernaryTensor::dequantize (src/ternary.rs:140-161). */
+int rnn_ternary_dequantize(const uint32_t *packed, int64_t numel,
+                           const float *scales, int64_t n_scales, int64_t cols,
+                           float *w, void *stream);
+
+/* TernaryLinear::forward (src/ternary.rs:239-279), reference semantics: f32
+ * shift-and-add in k order, then acc * scale[o] (+ bias[o]); bit-exact. */
+int rnn_ternary_linear_forward(const float *x, int64_t batch, int64_t in_f,
+                               const uint32_t *packed, const float *scales,
+                               int64_t out_f, const float *bias, float *y,
+                               void *stream);
+
+/* Ternary GEMM on int8 MFMA (BASELINE ternary config): t[n,k] unpacked from
+ * the 2-bit codes inside the kernel, acc = sum_k aq[m,k]*t[n,k], epilogue as
+ * rnn_w8a8_linear with sw[n]. k must be a multiple of 16 (rows word aligned). */
+int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_t *packed,
+                     const float *sw, const float *bias, int64_t m, int64_t k,
+                     int64_t n, unsigned flags, float *y, int32_t *acc_out,
+                     void *stream);
+
+/* ------------------------------------------------------- RotorQuant (a10-a12) */
+
+/* Rotor::rotation_matrix (src/quant.rs:101-113) for n rotors {s,p12,p13,p23};
+ * rot9 receives n row-major 3x3 matrices. */
+int rnn_rotor_rotation_matrices(const float *rotors, int64_t n, float *rot9,
+                                void *stream);
+
+/* RotorQuant::quantize / Module::forward (src/quant.rs:212-252, quantize_vec
+ * :170-208) over x [rows, dim]: zero-pad to padded_dim = ceil(dim/3)*3, per
+ * 3-group rotate, scale = max|rv|/qmax, q = (rv/scale).round().clamp(+-qmax),
+ * rv = q*scale, inverse-rotate, trim. rotors: ceil(dim/3) x {s,p12,p13,p23}
+ * (RotorQuant::rotors, src/quant.rs:127). bits in [2,8] (qmax = 2^(bits-1)-1).
+ * y [rows,dim] receives the reconstruction (may be NULL when codes is set);
+ * codes [rows,padded_dim] int8 and scales [rows,padded_dim/3] are optional.
+ * A group with max|rv| < 1e-12 is left untouched (:189-191): codes 0, scale 0. */
+int rnn_rotorquant_quantize(const float *x, int64_t rows, int64_t dim, int bits,
+                            const float *rotors, float *y, int8_t *codes,
+                            float *scales, void *stream);
+
+/* Reconstruction from codes + scales with the same expressions as :195-202
+ * (skipped groups reconstruct to 0). */
+int rnn_rotorquant_dequantize(const int8_t *codes, const float *scales,
+                              int64_t rows, int64_t dim, const float *rotors,
+                              float *y, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,585 @@
+/*
+ * oracle.c -- CPU restatement of rust-nn's quantized-inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker and timed CPU baseline); see
+ * oracle.h for the contract, the floating-point rules and what pins each
+ * function. Built by oracle/Makefile with -ffp-contract=off.
+ */
+#define _GNU_SOURCE
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#endif
+
+/* Rust `f32 as i8` after clamp: NaN -> 0, values already in range. */
+static inline int8_t f32_to_i8_sat(float v) {
+    if (v != v) return 0;
+    if (v <= -128.0f) return -128;
+    if (v >= 127.0f) return 127;
+    return (int8_t)v;
+}
+
+/* Rust f32::clamp(lo, hi): NaN passes through. */
+static inline float clampf_rs(float x, float lo, float hi) {
+    if (x < lo) return lo;
+    if (x > hi) return hi;
+    return x;
+}
+
+/* ------------------------------------------------------------------ */
+/* src/int8.rs:382-394                                                  */
+/* ------------------------------------------------------------------ */
+void orc_lcg_bytes(uint32_t *seed, int8_t *out, size_t n, int is_signed) {
+    uint32_t s = *seed;
+    for (size_t i = 0; i < n; ++i) {
+        s = s * 1664525u + 1013904223u;
+        uint8_t b = (uint8_t)(s >> 16);
+        out[i] = is_signed ? (int8_t)b : (int8_t)(b & 0x7f);
+    }
+    *seed = s;
+}
+
+/* ------------------------------------------------------------------ */
+/* src/int8.rs:222-234  igemm_scalar (wrapping int32)                   */
+/* ------------------------------------------------------------------ */
+void orc_igemm_scalar(const uint8_t *a, const int8_t *b, int32_t *c,
+                      size_t m, size_t k, size_t n) {
+    for (size_t i = 0; i < m; ++i) {
+        for (size_t j = 0; j < n; ++j) {
+            uint32_t s = 0;
+            for (size_t p = 0; p < k; ++p)
+                s += (uint32_t)((int32_t)a[i * k + p] * (int32_t)b[p * n + j]);
+            c[i * n + j] = (int32_t)s;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* src/int8.rs:195-314  igemm: VNNI repack of B + 4-row blocks          */
+/* ------------------------------------------------------------------ */
+#if defined(__x86_64__)
+/* B [k,n] -> tiles of (4 k x 16 n): tile (kq, nb) is 64 bytes, lane l holds
+ * b[4kq+0..3, 16nb+l] little-endian (the vpdpbusd operand order), zero padded
+ * to kp x np. Same layout as src/int8.rs:191-218. */
+static uint8_t *vnni_pack_b(const int8_t *b, size_t k, size_t n, size_t kp,
+                            size_t np) {
+    size_t nblk = np / 16;
+    uint8_t *out = (uint8_t *)calloc((kp / 4) * nblk * 64, 1);
+    for (size_t kq = 0; kq < kp / 4; ++kq)
+        for (size_t nb = 0; nb < nblk; ++nb) {
+            uint8_t *tile = out + (kq * nblk + nb) * 64;
+            for (size_t l = 0; l < 16; ++l) {
+                size_t col = nb * 16 + l;
+                for (size_t j = 0; j < 4; ++j) {
+                    size_t row = kq * 4 + j;
+                    tile[l * 4 + j] =
+                        (row < k && col < n) ? (uint8_t)b[row * n + col] : 0;
+                }
+            }
+        }
+    return out;
+}
+
+/* One block of up to 4 rows starting at row0: acc[r][16] per 16-column
+ * block, accumulated with vpdpbusd over the packed K. */
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+static void vnni_rows4(const uint8_t *apad, const uint8_t *bpack, int32_t *crow,
+                       size_t row0, size_t nrows, size_t kp, size_t np) {
+    size_t nblk = np / 16;
+    for (size_t nb = 0; nb < nblk; ++nb) {
+        __m512i acc0 = _mm512_setzero_si512(), acc1 = acc0, acc2 = acc0,
+                acc3 = acc0;
+        const uint8_t *bt = bpack + nb * 64;
+        const uint8_t *a0 = apad + (row0 + 0) * kp;
+        const uint8_t *a1 = apad + (row0 + 1) * kp;
+        const uint8_t *a2 = apad + (row0 + 2) * kp;
+        const uint8_t *a3 = apad + (row0 + 3) * kp;
+        for (size_t kq = 0; kq < kp / 4; ++kq) {
+            __m512i bv = _mm512_loadu_si512((const void *)(bt + kq * nblk * 64));
+            int32_t w0, w1, w2, w3;
+            memcpy(&w0, a0 + 4 * kq, 4);
+            memcpy(&w1, a1 + 4 * kq, 4);
+            memcpy(&w2, a2 + 4 * kq, 4);
+            memcpy(&w3, a3 + 4 * kq, 4);
+            acc0 = _mm512_dpbusd_epi32(acc0, _mm512_set1_epi32(w0), bv);
+            acc1 = _mm512_dpbusd_epi32(acc1, _mm512_set1_epi32(w1), bv);
+            acc2 = _mm512_dpbusd_epi32(acc2, _mm512_set1_epi32(w2), bv);
+            acc3 = _mm512_dpbusd_epi32(acc3, _mm512_set1_epi32(w3), bv);
+        }
+        __m512i accs[4] = {acc0, acc1, acc2, acc3};
+        for (size_t r = 0; r < nrows; ++r)
+            _mm512_storeu_si512((void *)(crow + r * np + nb * 16), accs[r]);
+    }
+}
+
+struct vnni_job {
+    const uint8_t *apad, *bpack;
+    int32_t *ctmp;
+    size_t m, kp, np, nblocks;
+    atomic_size_t next;
+};
+
+static void *vnni_worker(void *arg) {
+    struct vnni_job *j = (struct vnni_job *)arg;
+    for (;;) {
+        size_t blk = atomic_fetch_add(&j->next, 1);
+        if (blk >= j->nblocks) break;
+        size_t row0 = blk * 4;
+        size_t nrows = j->m - row0 < 4 ? j->m - row0 : 4;
+        vnni_rows4(j->apad, j->bpack, j->ctmp + row0 * j->np, row0, nrows,
+                   j->kp, j->np);
+    }
+    return NULL;
+}
+#endif
+
+int orc_igemm(const uint8_t *a, const int8_t *b, int32_t *c, size_t m,
+              size_t k, size_t n, int nthreads) {
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    if (__builtin_cpu_supports("avx512vnni") && m > 0 && n > 0) {
+        size_t kp = (k + 3) & ~(size_t)3, np = (n + 15) & ~(size_t)15,
+               mp = (m + 3) & ~(size_t)3;
+        uint8_t *apad = (uint8_t *)calloc((mp * kp) > 0 ? (mp * kp) : 1, 1);
+        for (size_t i = 0; i < m; ++i) memcpy(apad + i * kp, a + i * k, k);
+        uint8_t *bpack = vnni_pack_b(b, k, n, kp ? kp : 4, np);
+        int32_t *ctmp = (int32_t *)malloc(m * np * sizeof(int32_t));
+        struct vnni_job job = {apad, bpack, ctmp, m, kp, np, (m + 3) / 4, 0};
+        if (kp == 0) {
+            memset(ctmp, 0, m * np * sizeof(int32_t));
+        } else {
+            int nt = nthreads < 1 ? 1 : nthreads;
+            if ((size_t)nt > job.nblocks) nt = (int)job.nblocks;
+            pthread_t th[256];
+            if (nt > 256) nt = 256;
+            for (int t = 1; t < nt; ++t)
+                pthread_create(&th[t], NULL, vnni_worker, &job);
+            vnni_worker(&job);
+            for (int t = 1; t < nt; ++t) pthread_join(th[t], NULL);
+        }
+        for (size_t i = 0; i < m; ++i)
+            memcpy(c + i * n, ctmp + i * np, n * sizeof(int32_t));
+        free(apad);
+        free(bpack);
+        free(ctmp);
+        return 1;
+    }
+#endif
+    (void)nthreads;
+    orc_igemm_scalar(a, b, c, m, k, n);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* src/int8.rs:33-45, src/quantize.rs:296-311  per-row symmetric int8   */
+/* ------------------------------------------------------------------ */
+void orc_quant_rows_i8(const float *x, size_t rows, size_t cols, int8_t *q,
+                       float *scale) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        float max_abs = 0.0f;
+        for (size_t j = 0; j < cols; ++j) max_abs = fmaxf(max_abs, fabsf(row[j]));
+        float s = max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
+        scale[r] = s;
+        for (size_t j = 0; j < cols; ++j)
+            q[r * cols + j] = f32_to_i8_sat(clampf_rs(roundf(row[j] / s), -128.0f, 127.0f));
+    }
+}
+
+/* src/int8.rs:55-65 */
+void orc_int8_dequantize(const int8_t *q, const float *scale, size_t rows,
+                         size_t cols, float *w) {
+    for (size_t i = 0; i < rows; ++i)
+        for (size_t j = 0; j < cols; ++j)
+            w[i * cols + j] = (float)q[i * cols + j] * scale[i];
+}
+
+/* src/int8.rs:70-88 */
+void orc_int8_matmul_f32(const int8_t *wq, const float *ws, size_t out_f,
+                         size_t in_f, const float *x, size_t m, float *y) {
+    for (size_t row = 0; row < m; ++row)
+        for (size_t col = 0; col < out_f; ++col) {
+            uint32_t acc = 0;
+            for (size_t p = 0; p < in_f; ++p) {
+                float inv = 1.0f / ws[col];
+                int8_t av = f32_to_i8_sat(
+                    clampf_rs(roundf(x[row * in_f + p] * inv), -128.0f, 127.0f));
+                acc += (uint32_t)((int32_t)av * (int32_t)wq[col * in_f + p]);
+            }
+            y[row * out_f + col] = (float)(int32_t)acc * ws[col] * ws[col];
+        }
+}
+
+/* src/int8.rs:134-172 */
+void orc_int8_linear_forward(const float *x, size_t batch, size_t in_f,
+                             const int8_t *wq, const float *ws, size_t out_f,
+                             const float *bias, float *y) {
+    for (size_t b = 0; b < batch; ++b)
+        for (size_t o = 0; o < out_f; ++o) {
+            uint32_t acc = 0;
+            float s = ws[o];
+            for (size_t p = 0; p < in_f; ++p) {
+                int8_t aq = f32_to_i8_sat(
+                    clampf_rs(roundf(x[b * in_f + p] / s), -128.0f, 127.0f));
+                acc += (uint32_t)((int32_t)aq * (int32_t)wq[o * in_f + p]);
+            }
+            float v = (float)(int32_t)acc * s * s;
+            if (bias) v = v + bias[o];
+            y[b * out_f + o] = v;
+        }
+}
+
+/* W8A8 composition; epilogue order of src/int8.rs:159-162. */
+void orc_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *wq,
+                     const float *sw, const float *bias, size_t m, size_t k,
+                     size_t n, int relu, float *y, int32_t *acc_out) {
+    for (size_t i = 0; i < m; ++i)
+        for (size_t j = 0; j < n; ++j) {
+            uint32_t acc = 0;
+            const int8_t *ar = aq + i * k, *wr = wq + j * k;
+            for (size_t p = 0; p < k; ++p)
+                acc += (uint32_t)((int32_t)ar[p] * (int32_t)wr[p]);
+            if (acc_out) acc_out[i * n + j] = (int32_t)acc;
+            float v = (float)(int32_t)acc * sa[i] * sw[j];
+            if (bias) v = v + bias[j];
+            if (relu) v = fmaxf(v, 0.0f);
+            y[i * n + j] = v;
+        }
+}
+
+/* src/tensor.rs:2025-2032 */
+void orc_relu(float *x, size_t n) {
+    for (size_t i = 0; i < n; ++i) x[i] = fmaxf(x[i], 0.0f);
+}
+
+/* ------------------------------------------------------------------ */
+/* src/ternary.rs:46-75  2-bit packing, 16 codes per u32, LSB first     */
+/* ------------------------------------------------------------------ */
+void orc_pack_ternary(const int8_t *v, size_t n, uint32_t *packed) {
+    memset(packed, 0, ((n + 15) / 16) * sizeof(uint32_t));
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t code = v[i] == 0 ? 0u : (v[i] > 0 ? 1u : 2u);
+        packed[i / 16] |= code << ((i % 16) * 2);
+    }
+}
+
+void orc_unpack_ternary(const uint32_t *packed, size_t count, int8_t *out) {
+    for (size_t i = 0; i < count; ++i) {
+        uint32_t code = (packed[i / 16] >> ((i % 16) * 2)) & 3u;
+        out[i] = code == 1 ? 1 : (code == 2 ? -1 : 0);
+    }
+}
+
+/* src/ternary.rs:97-137 */
+void orc_ternary_quantize_rows(const float *w, size_t rows, size_t cols,
+                               int8_t *t, float *scales) {
+    for (size_t r = 0; r < rows; ++r) {
+        const float *row = w + r * cols;
+        float sum = 0.0f;
+        for (size_t j = 0; j < cols; ++j) sum = sum + fabsf(row[j]);
+        float mean_abs = sum / (float)(cols > 0 ? cols : 1);
+        float threshold = 0.7f * mean_abs;
+        scales[r] = fmaxf(mean_abs, 1e-8f);
+        for (size_t j = 0; j < cols; ++j) {
+            float v = row[j];
+            t[r * cols + j] = fabsf(v) < threshold ? 0 : (v > 0.0f ? 1 : -1);
+        }
+    }
+}
+
+float orc_ternary_quantize_absmean(const float *w, size_t rows, size_t cols,
+                                   int8_t *t) {
+    double total = 0.0;
+    for (size_t r = 0; r < rows; ++r) {
+        float sum = 0.0f;
+        for (size_t j = 0; j < cols; ++j) sum = sum + fabsf(w[r * cols + j]);
+        total = total + (double)sum;
+    }
+    size_t numel = rows * cols;
+    float gamma = (float)(total / (double)(numel > 0 ? numel : 1));
+    gamma = fmaxf(gamma, 1e-8f);
+    for (size_t i = 0; i < numel; ++i)
+        t[i] = f32_to_i8_sat(clampf_rs(roundf(w[i] / gamma), -1.0f, 1.0f));
+    return gamma;
+}
+
+/* src/ternary.rs:140-161 */
+void orc_ternary_dequantize(const uint32_t *packed, size_t numel,
+                            const float *scales, size_t n_scales, size_t cols,
+                            float *w) {
+    for (size_t i = 0; i < numel; ++i) {
+        uint32_t code = (packed[i / 16] >> ((i % 16) * 2)) & 3u;
+        int tv = code == 1 ? 1 : (code == 2 ? -1 : 0);
+        size_t r = i / cols;
+        if (r > n_scales - 1) r = n_scales - 1;
+        w[i] = (float)tv * scales[r];
+    }
+}
+
+/* src/ternary.rs:239-279 */
+void orc_ternary_linear_f32(const float *x, size_t batch, size_t in_f,
+                            const uint32_t *packed, const float *scales,
+                            size_t out_f, const float *bias, float *y) {
+    for (size_t b = 0; b < batch; ++b)
+        for (size_t o = 0; o < out_f; ++o) {
+            float acc = 0.0f;
+            for (size_t i = 0; i < in_f; ++i) {
+                size_t idx = o * in_f + i;
+                uint32_t code = (packed[idx / 16] >> ((idx % 16) * 2)) & 3u;
+                float xv = x[b * in_f + i];
+                if (code == 1) acc = acc + xv;
+                else if (code == 2) acc = acc - xv;
+            }
+            float v = acc * scales[o];
+            if (bias) v = v + bias[o];
+            y[b * out_f + o] = v;
+        }
+}
+
+void orc_ternary_gemm_i8(const int8_t *aq, const float *sa,
+                         const uint32_t *packed, const float *sw,
+                         const float *bias, size_t m, size_t k, size_t n,
+                         int relu, float *y, int32_t *acc_out) {
+    int8_t *wt = (int8_t *)malloc((n * k) > 0 ? (n * k) : 1);
+    orc_unpack_ternary(packed, n * k, wt);
+    orc_w8a8_linear(aq, sa, wt, sw, bias, m, k, n, relu, y, acc_out);
+    free(wt);
+}
+
+/* ------------------------------------------------------------------ */
+/* src/quant.rs:70-113  Cl(3,0) rotor sandwich                          */
+/* ------------------------------------------------------------------ */
+/* Sparse geometric product rotor*x for rotor (s,p12,p13,p23); multivector
+ * layout [1,e1,e2,e3,e12,e13,e23,e123] (src/quant.rs:23-24, :70-81). */
+static void rotor_apply(const float x[8], float s, float p12, float p13,
+                        float p23, float o[8]) {
+    o[0] = s * x[0] - p12 * x[4] - p13 * x[5] - p23 * x[6];
+    o[1] = s * x[1] + p12 * x[2] + p13 * x[3] + p23 * x[7];
+    o[2] = s * x[2] - p12 * x[1] + p23 * x[3] - p13 * x[7];
+    o[3] = s * x[3] - p13 * x[1] - p23 * x[2] + p12 * x[7];
+    o[4] = s * x[4] + p12 * x[0];
+    o[5] = s * x[5] + p13 * x[0];
+    o[6] = s * x[6] + p23 * x[0];
+    o[7] = s * x[7] - p23 * x[1] + p13 * x[2] - p12 * x[3];
+}
+
+void orc_rotor_sandwich(const float r[4], const float x[8], float out[8]) {
+    float t[8];
+    rotor_apply(x, r[0], r[1], r[2], r[3], t);
+    rotor_apply(t, r[0], -r[1], -r[2], -r[3], out);
+}
+
+void orc_rotor_inv_sandwich(const float r[4], const float x[8], float out[8]) {
+    float t[8];
+    rotor_apply(x, r[0], -r[1], -r[2], -r[3], t);
+    rotor_apply(t, r[0], r[1], r[2], r[3], out);
+}
+
+void orc_rotor_rotation_matrix(const float r[4], float rot[9]) {
+    float e[3][8], img[3][8];
+    memset(e, 0, sizeof e);
+    e[0][1] = 1.0f;
+    e[1][2] = 1.0f;
+    e[2][3] = 1.0f;
+    for (int j = 0; j < 3; ++j) orc_rotor_sandwich(r, e[j], img[j]);
+    for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j) rot[i * 3 + j] = img[j][1 + i];
+}
+
+/* ------------------------------------------------------------------ */
+/* src/quant.rs:164-239  RotorQuant                                     */
+/* ------------------------------------------------------------------ */
+void orc_rotorquant_quantize(const float *x, size_t rows, size_t dim, int bits,
+                             const float *rotors, float *y, int8_t *codes,
+                             float *scales) {
+    size_t padded = (dim + 2) / 3 * 3, ng = padded / 3;
+    float qmax = (float)((1u << (bits - 1)) - 1u);
+    float *rot = (float *)malloc((ng ? ng : 1) * 9 * sizeof(float));
+    for (size_t g = 0; g < ng; ++g) orc_rotor_rotation_matrix(rotors + 4 * g, rot + 9 * g);
+    float *row = (float *)malloc((padded ? padded : 1) * sizeof(float));
+    for (size_t r = 0; r < rows; ++r) {
+        for (size_t t = 0; t < padded; ++t) row[t] = t < dim ? x[r * dim + t] : 0.0f;
+        for (size_t g = 0; g < ng; ++g) {
+            const float *R = rot + 9 * g;
+            float v0 = row[3 * g], v1 = row[3 * g + 1], v2 = row[3 * g + 2];
+            float rv[3] = {R[0] * v0 + R[1] * v1 + R[2] * v2,
+                           R[3] * v0 + R[4] * v1 + R[5] * v2,
+                           R[6] * v0 + R[7] * v1 + R[8] * v2};
+            float max_abs = 0.0f;
+            for (int i = 0; i < 3; ++i) max_abs = fmaxf(max_abs, fabsf(rv[i]));
+            if (max_abs < 1e-12f) {
+                if (codes) codes[r * padded + 3 * g] = codes[r * padded + 3 * g + 1] =
+                               codes[r * padded + 3 * g + 2] = 0;
+                if (scales) scales[r * ng + g] = 0.0f;
+                continue;
+            }
+            float scale = max_abs / qmax;
+            for (int i = 0; i < 3; ++i) {
+                float q = clampf_rs(roundf(rv[i] / scale), -qmax, qmax);
+                if (codes) codes[r * padded + 3 * g + i] = f32_to_i8_sat(q);
+                rv[i] = q * scale;
+            }
+            if (scales) scales[r * ng + g] = scale;
+            row[3 * g] = R[0] * rv[0] + R[3] * rv[1] + R[6] * rv[2];
+            row[3 * g + 1] = R[1] * rv[0] + R[4] * rv[1] + R[7] * rv[2];
+            row[3 * g + 2] = R[2] * rv[0] + R[5] * rv[1] + R[8] * rv[2];
+        }
+        for (size_t t = 0; t < dim; ++t) y[r * dim + t] = row[t];
+    }
+    free(row);
+    free(rot);
+}
+
+void orc_rotorquant_dequantize(const int8_t *codes, const float *scales,
+                               size_t rows, size_t dim, const float *rotors,
+                               float *y) {
+    size_t padded = (dim + 2) / 3 * 3, ng = padded / 3;
+    float *rot = (float *)malloc((ng ? ng : 1) * 9 * sizeof(float));
+    for (size_t g = 0; g < ng; ++g) orc_rotor_rotation_matrix(rotors + 4 * g, rot + 9 * g);
+    float *row = (float *)malloc((padded ? padded : 1) * sizeof(float));
+    for (size_t r = 0; r < rows; ++r) {
+        for (size_t g = 0; g < ng; ++g) {
+            const float *R = rot + 9 * g;
+            float s = scales[r * ng + g];
+            const int8_t *q = codes + r * padded + 3 * g;
+            float rv[3] = {(float)q[0] * s, (float)q[1] * s, (float)q[2] * s};
+            row[3 * g] = R[0] * rv[0] + R[3] * rv[1] + R[6] * rv[2];
+            row[3 * g + 1] = R[1] * rv[0] + R[4] * rv[1] + R[7] * rv[2];
+            row[3 * g + 2] = R[2] * rv[0] + R[5] * rv[1] + R[8] * rv[2];
+        }
+        for (size_t t = 0; t < dim; ++t) y[r * dim + t] = row[t];
+    }
+    free(row);
+    free(rot);
+}
+
+/* ------------------------------------------------------------------ */
+/* Rotor::random via rand 0.8.5 StdRng (ChaCha12) -- parity unpinned   */
+/* ------------------------------------------------------------------ */
+static inline uint32_t rotl32(uint32_t v, int c) { return (v << c) | (v >> (32 - c)); }
+
+#define QR(a, b, c, d)            \
+    a += b; d ^= a; d = rotl32(d, 16); \
+    c += d; b ^= c; b = rotl32(b, 12); \
+    a += b; d ^= a; d = rotl32(d, 8);  \
+    c += d; b ^= c; b = rotl32(b, 7);
+
+static void chacha_core(const uint32_t in[16], int rounds, uint32_t out[16]) {
+    uint32_t x[16];
+    memcpy(x, in, sizeof x);
+    for (int i = 0; i < rounds; i += 2) {
+        QR(x[0], x[4], x[8], x[12]);
+        QR(x[1], x[5], x[9], x[13]);
+        QR(x[2], x[6], x[10], x[14]);
+        QR(x[3], x[7], x[11], x[15]);
+        QR(x[0], x[5], x[10], x[15]);
+        QR(x[1], x[6], x[11], x[12]);
+        QR(x[2], x[7], x[8], x[13]);
+        QR(x[3], x[4], x[9], x[14]);
+    }
+    for (int i = 0; i < 16; ++i) out[i] = x[i] + in[i];
+}
+
+static const uint32_t CHACHA_SIGMA[4] = {0x61707865u, 0x3320646eu, 0x79622d32u,
+                                         0x6b206574u};
+
+void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream,
+                      int rounds, uint32_t out[16]) {
+    uint32_t st[16];
+    memcpy(st, CHACHA_SIGMA, 16);
+    memcpy(st + 4, key, 32);
+    st[12] = (uint32_t)counter;
+    st[13] = (uint32_t)(counter >> 32);
+    st[14] = (uint32_t)stream;
+    st[15] = (uint32_t)(stream >> 32);
+    chacha_core(st, rounds, out);
+}
+
+void orc_chacha20_block_ietf(const uint32_t key[8], uint32_t counter,
+                             const uint32_t nonce[3], uint32_t out[16]) {
+    uint32_t st[16];
+    memcpy(st, CHACHA_SIGMA, 16);
+    memcpy(st + 4, key, 32);
+    st[12] = counter;
+    st[13] = nonce[0];
+    st[14] = nonce[1];
+    st[15] = nonce[2];
+    chacha_core(st, 20, out);
+}
+
+/* rand_chacha ChaCha12Rng as a block RNG: 4 consecutive blocks (64 words)
+ * per refill, 64-bit block counter starting at 0, stream 0. */
+struct std_rng {
+    uint32_t key[8];
+    uint64_t counter;
+    uint32_t buf[64];
+    int idx;
+};
+
+/* rand_core 0.6.4 SeedableRng::seed_from_u64: PCG32 output words fill the
+ * 32-byte seed little-endian. */
+static void std_rng_seed(struct std_rng *g, uint64_t state) {
+    const uint64_t MUL = 6364136223846793005ull, INC = 11634580027462260723ull;
+    for (int i = 0; i < 8; ++i) {
+        state = state * MUL + INC;
+        uint32_t xs = (uint32_t)(((state >> 18) ^ state) >> 27);
+        uint32_t rot = (uint32_t)(state >> 59);
+        g->key[i] = (xs >> rot) | (xs << ((32 - rot) & 31));
+    }
+    g->counter = 0;
+    g->idx = 64;
+}
+
+static uint32_t std_rng_next_u32(struct std_rng *g) {
+    if (g->idx >= 64) {
+        for (int b = 0; b < 4; ++b)
+            orc_chacha_block(g->key, g->counter + (uint64_t)b, 0, 12, g->buf + 16 * b);
+        g->counter += 4;
+        g->idx = 0;
+    }
+    return g->buf[g->idx++];
+}
+
+/* rand 0.8.5 UniformFloat<f32>::sample_single(low, high). */
+static float std_rng_range_f32(struct std_rng *g, float low, float high) {
+    float scale = high - low;
+    for (;;) {
+        uint32_t bits = (std_rng_next_u32(g) >> 9) | (127u << 23);
+        float v12;
+        memcpy(&v12, &bits, 4);
+        float v01 = v12 - 1.0f;
+        float res = v01 * scale + low;
+        if (res < high) return res;
+    }
+}
+
+void orc_rotorquant_rotors_from_seed(uint64_t seed, size_t n_groups, float *rotors) {
+    struct std_rng g;
+    std_rng_seed(&g, seed);
+    const float PI_F32 = 3.14159265358979323846f;
+    for (size_t i = 0; i < n_groups; ++i) {
+        float a = std_rng_range_f32(&g, -1.0f, 1.0f);
+        float b = std_rng_range_f32(&g, -1.0f, 1.0f);
+        float c = std_rng_range_f32(&g, -1.0f, 1.0f);
+        float norm = sqrtf(a * a + b * b + c * c);
+        float theta = std_rng_range_f32(&g, 0.0f, PI_F32);
+        float *r = rotors + 4 * i;
+        if (norm < 1e-8f) {
+            r[0] = 1.0f; r[1] = 0.0f; r[2] = 0.0f; r[3] = 0.0f;
+            continue;
+        }
+        float ua = a / norm, ub = b / norm, uc = c / norm;
+        float s = cosf(theta / 2.0f), mag = sinf(theta / 2.0f);
+        r[0] = s;
+        r[1] = mag * ua;
+        r[2] = mag * ub;
+        r[3] = mag * uc;
+    }
+}

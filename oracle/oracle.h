@@ -1,0 +1,161 @@
+/*
+ * oracle.h -- CPU restatement of rust-nn's quantized-inference path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP
+ * kernels and the timed CPU baseline in bench.py. Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
+ * product library (librnn_hip.so) never links or calls it.
+ *
+ * Each function restates one reference function expression by expression
+ * (file:line into gugu8intel-i9/Rust-Neural-Network). The reference is Rust and
+ * cannot be compiled in this image (no cargo/rustc), so there is no oracle/_ref
+ * build; every function here is pinned instead by the reference's own
+ * known-answer tests, by brute force, closed forms and invariants
+ * (tests/test_oracle.py). Functions whose exact values cannot be pinned are
+ * marked "parity unpinned" below.
+ *
+ * Floating point: compiled with -ffp-contract=off and no fast-math, so every
+ * `a*b + c` rounds twice exactly like Rust (which never contracts), divisions
+ * are IEEE, roundf() is half-away-from-zero like f32::round, fmaxf() returns the
+ * non-NaN operand like f32::max, and int32 accumulation wraps (release Rust).
+ */
+#ifndef RNN_ORACLE_H
+#define RNN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- deterministic generators used by the reference's own tests ---- */
+
+/* src/int8.rs:382-394 (lcg_bytes): s = s*1664525 + 1013904223, byte = s>>16;
+ * unsigned draws are masked with 0x7f. */
+void orc_lcg_bytes(uint32_t *seed, int8_t *out, size_t n, int is_signed);
+
+/* ---- int8 GEMM (igemm contract: A u8 [m,k], B i8 [k,n] N-contiguous) ---- */
+
+/* src/int8.rs:222-234 */
+void orc_igemm_scalar(const uint8_t *a, const int8_t *b, int32_t *c,
+                      size_t m, size_t k, size_t n);
+
+/* src/int8.rs:285-314: AVX-512 VNNI path (B repacked per call, 4-row blocks
+ * spread over `nthreads` workers); scalar fallback without VNNI.
+ * Returns 1 when the VNNI path ran, 0 for the scalar fallback. */
+int orc_igemm(const uint8_t *a, const int8_t *b, int32_t *c,
+              size_t m, size_t k, size_t n, int nthreads);
+
+/* ---- symmetric int8 quantization (per row of a row-major matrix) ---- */
+
+/* src/int8.rs:33-45 (Int8Weights::quantize, per output channel) and
+ * src/quantize.rs:296-311 (quantize_int8 with group_size = cols): the per-row
+ * dynamic activation rule is the same expression applied to rows of X. */
+void orc_quant_rows_i8(const float *x, size_t rows, size_t cols,
+                       int8_t *q, float *scale);
+
+/* src/int8.rs:55-65 */
+void orc_int8_dequantize(const int8_t *q, const float *scale, size_t rows,
+                         size_t cols, float *w);
+
+/* src/int8.rs:70-88 (Int8Weights::matmul_f32; activation scaled by 1/scale) */
+void orc_int8_matmul_f32(const int8_t *wq, const float *ws, size_t out_f,
+                         size_t in_f, const float *x, size_t m, float *y);
+
+/* src/int8.rs:134-172 (Int8Linear::forward, reference semantics: activation
+ * re-quantized with the weight's channel scale inside the output loop). */
+void orc_int8_linear_forward(const float *x, size_t batch, size_t in_f,
+                             const int8_t *wq, const float *ws, size_t out_f,
+                             const float *bias /* nullable */, float *y);
+
+/* W8A8 composition: acc = sum_k a[m,k]*w[n,k] (wrapping
+ * int32), y = ((float)acc * sa[m]) * sw[n] (+ bias[n]) (then max(y, 0) if relu).
+ * acc_out (nullable) receives the raw int32 accumulators. The epilogue keeps the
+ * reference's multiply-then-add order of src/int8.rs:159-162. */
+void orc_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *wq,
+                     const float *sw, const float *bias, size_t m, size_t k,
+                     size_t n, int relu, float *y, int32_t *acc_out);
+
+/* src/tensor.rs:2025-2032 (x.max(0.0)) */
+void orc_relu(float *x, size_t n);
+
+/* ---- ternary ---- */
+
+/* src/ternary.rs:46-60; packed has ceil(n/16) words. */
+void orc_pack_ternary(const int8_t *v, size_t n, uint32_t *packed);
+/* src/ternary.rs:63-75 */
+void orc_unpack_ternary(const uint32_t *packed, size_t count, int8_t *out);
+
+/* src/ternary.rs:97-137 (reference rule: per row delta = 0.7*mean|w|,
+ * scale = max(mean|w|, 1e-8)). t receives the ternary values. */
+void orc_ternary_quantize_rows(const float *w, size_t rows, size_t cols,
+                               int8_t *t, float *scales);
+
+/* Config rule (BitNet-b1.58 absmean, not in the reference): per-row sequential
+ * f32 sums of |w| (the reference's own sum, src/ternary.rs:114), added in row
+ * order in double; gamma = max((float)(total/numel), 1e-8);
+ * t = clamp(round(w/gamma), -1, 1). Returns gamma. */
+float orc_ternary_quantize_absmean(const float *w, size_t rows, size_t cols,
+                                   int8_t *t);
+
+/* src/ternary.rs:140-161 */
+void orc_ternary_dequantize(const uint32_t *packed, size_t numel,
+                            const float *scales, size_t n_scales, size_t cols,
+                            float *w);
+
+/* src/ternary.rs:239-279 (reference f32 shift-and-add, k order sequential). */
+void orc_ternary_linear_f32(const float *x, size_t batch, size_t in_f,
+                            const uint32_t *packed, const float *scales,
+                            size_t out_f, const float *bias, float *y);
+
+/* Config ternary GEMM: acc = sum_k a[m,k]*t[n,k] with t unpacked from the
+ * 2-bit codes, epilogue as orc_w8a8_linear with sw[n] (= gamma broadcast). */
+void orc_ternary_gemm_i8(const int8_t *aq, const float *sa,
+                         const uint32_t *packed, const float *sw,
+                         const float *bias, size_t m, size_t k, size_t n,
+                         int relu, float *y, int32_t *acc_out);
+
+/* ---- Cl(3,0) rotors and RotorQuant ---- */
+
+/* src/quant.rs:84-89 and :92-96 on a multivector [1,e1,e2,e3,e12,e13,e23,e123]
+ * with rotor r = {s, p12, p13, p23}. */
+void orc_rotor_sandwich(const float r[4], const float x[8], float out[8]);
+void orc_rotor_inv_sandwich(const float r[4], const float x[8], float out[8]);
+/* src/quant.rs:101-113; row-major 3x3. */
+void orc_rotor_rotation_matrix(const float r[4], float rot[9]);
+
+/* src/quant.rs:212-239 with quantize_vec :170-208. x is [rows, dim]; rotors
+ * holds ceil(dim/3) rotors of {s,p12,p13,p23}. y receives the reconstruction.
+ * codes (nullable) receives [rows, padded_dim] int8 codes q, scales (nullable)
+ * [rows, n_groups] per-group scales; a group skipped by the max_abs < 1e-12
+ * rule (:189-191) gets codes 0 and scale 0 while y keeps its input values. */
+void orc_rotorquant_quantize(const float *x, size_t rows, size_t dim, int bits,
+                             const float *rotors, float *y, int8_t *codes,
+                             float *scales);
+
+/* Reconstruction from codes + scales: rv = q*scale, out = rot^T rv, the same
+ * expressions as :195-202. Skipped groups (scale 0) reconstruct to 0. */
+void orc_rotorquant_dequantize(const int8_t *codes, const float *scales,
+                               size_t rows, size_t dim, const float *rotors,
+                               float *y);
+
+/* Rotor::random (src/quant.rs:39-65) driven by rand 0.8.5 StdRng
+ * (ChaCha12, rand_chacha 0.3.1) seeded through rand_core 0.6.4
+ * seed_from_u64, restated from those crates' published algorithms.
+ * PARITY UNPINNED: none of those crates is in this image and the reference's
+ * tests only check invariants, so the exact values are not verified; the
+ * ChaCha block function itself is pinned by the RFC 7539 test vector via
+ * orc_chacha_block. */
+void orc_rotorquant_rotors_from_seed(uint64_t seed, size_t n_groups, float *rotors);
+/* ChaCha block function with `rounds` rounds (20 = RFC 7539). */
+void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream,
+                      int rounds, uint32_t out[16]);
+/* RFC 7539 layout (32-bit counter, 96-bit nonce) for the published vector. */
+void orc_chacha20_block_ietf(const uint32_t key[8], uint32_t counter,
+                             const uint32_t nonce[3], uint32_t out[16]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,276 @@
+"""numpy front-end for the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for the HIP kernels and the CPU
+baseline timed by bench.py. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import this module. Every function restates a reference
+function of gugu8intel-i9/Rust-Neural-Network; the citation is in oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_P = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+
+
+def build() -> None:
+    """Compile liboracle.so with oracle/Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-B", "-C", _HERE, "liboracle.so"], check=True,
+                   stdout=subprocess.DEVNULL)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        sig = {
+            "orc_lcg_bytes": [_P, _P, _SZ, ctypes.c_int],
+            "orc_igemm_scalar": [_P, _P, _P, _SZ, _SZ, _SZ],
+            "orc_igemm": [_P, _P, _P, _SZ, _SZ, _SZ, ctypes.c_int],
+            "orc_quant_rows_i8": [_P, _SZ, _SZ, _P, _P],
+            "orc_int8_dequantize": [_P, _P, _SZ, _SZ, _P],
+            "orc_int8_matmul_f32": [_P, _P, _SZ, _SZ, _P, _SZ, _P],
+            "orc_int8_linear_forward": [_P, _SZ, _SZ, _P, _P, _SZ, _P, _P],
+            "orc_w8a8_linear": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, ctypes.c_int, _P, _P],
+            "orc_relu": [_P, _SZ],
+            "orc_pack_ternary": [_P, _SZ, _P],
+            "orc_unpack_ternary": [_P, _SZ, _P],
+            "orc_ternary_quantize_rows": [_P, _SZ, _SZ, _P, _P],
+            "orc_ternary_quantize_absmean": [_P, _SZ, _SZ, _P],
+            "orc_ternary_dequantize": [_P, _SZ, _P, _SZ, _SZ, _P],
+            "orc_ternary_linear_f32": [_P, _SZ, _SZ, _P, _P, _SZ, _P, _P],
+            "orc_ternary_gemm_i8": [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, ctypes.c_int, _P, _P],
+            "orc_rotor_sandwich": [_P, _P, _P],
+            "orc_rotor_inv_sandwich": [_P, _P, _P],
+            "orc_rotor_rotation_matrix": [_P, _P],
+            "orc_rotorquant_quantize": [_P, _SZ, _SZ, ctypes.c_int, _P, _P, _P, _P],
+            "orc_rotorquant_dequantize": [_P, _P, _SZ, _SZ, _P, _P],
+            "orc_rotorquant_rotors_from_seed": [ctypes.c_uint64, _SZ, _P],
+            "orc_chacha_block": [_P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _P],
+            "orc_chacha20_block_ietf": [_P, ctypes.c_uint32, _P, _P],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = None
+        L.orc_igemm.restype = ctypes.c_int
+        L.orc_ternary_quantize_absmean.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+# ---------------------------------------------------------------- generators
+def lcg_bytes(seed: int, n: int, signed: bool):
+    """src/int8.rs:382-394. Returns (bytes as int8, next seed)."""
+    s = (ctypes.c_uint32 * 1)(seed)
+    out = np.empty(n, np.int8)
+    lib().orc_lcg_bytes(ctypes.addressof(s), _ptr(out), n, int(signed))
+    return out, int(s[0])
+
+
+# ---------------------------------------------------------------- int8
+def igemm_scalar(a_u8, b_i8, m, k, n):
+    a, b = _c(a_u8, np.uint8), _c(b_i8, np.int8)
+    c = np.empty((m, n), np.int32)
+    lib().orc_igemm_scalar(_ptr(a), _ptr(b), _ptr(c), m, k, n)
+    return c
+
+
+def igemm(a_u8, b_i8, m, k, n, nthreads=1):
+    """src/int8.rs:285-314. Returns (C, used_vnni)."""
+    a, b = _c(a_u8, np.uint8), _c(b_i8, np.int8)
+    c = np.empty((m, n), np.int32)
+    used = lib().orc_igemm(_ptr(a), _ptr(b), _ptr(c), m, k, n, nthreads)
+    return c, bool(used)
+
+
+def quant_rows_i8(x):
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    lib().orc_quant_rows_i8(_ptr(x), rows, cols, _ptr(q), _ptr(s))
+    return q, s
+
+
+def int8_dequantize(q, s):
+    q, s = _c(q, np.int8), _c(s, np.float32)
+    w = np.empty(q.shape, np.float32)
+    lib().orc_int8_dequantize(_ptr(q), _ptr(s), q.shape[0], q.shape[1], _ptr(w))
+    return w
+
+
+def int8_matmul_f32(wq, ws, x):
+    wq, ws, x = _c(wq, np.int8), _c(ws, np.float32), _c(x, np.float32)
+    out_f, in_f = wq.shape
+    m = x.size // in_f
+    y = np.empty((m, out_f), np.float32)
+    lib().orc_int8_matmul_f32(_ptr(wq), _ptr(ws), out_f, in_f, _ptr(x), m, _ptr(y))
+    return y
+
+
+def int8_linear_forward(x, wq, ws, bias=None):
+    x, wq, ws = _c(x, np.float32), _c(wq, np.int8), _c(ws, np.float32)
+    bias = None if bias is None else _c(bias, np.float32)
+    batch, in_f = x.shape
+    out_f = wq.shape[0]
+    y = np.empty((batch, out_f), np.float32)
+    lib().orc_int8_linear_forward(_ptr(x), batch, in_f, _ptr(wq), _ptr(ws), out_f,
+                                  _ptr(bias), _ptr(y))
+    return y
+
+
+def w8a8_linear(aq, sa, wq, sw, bias=None, relu=False):
+    """Returns (y f32 [m,n], acc int32 [m,n])."""
+    aq, sa, wq, sw = _c(aq, np.int8), _c(sa, np.float32), _c(wq, np.int8), _c(sw, np.float32)
+    bias = None if bias is None else _c(bias, np.float32)
+    m, k = aq.shape
+    n = wq.shape[0]
+    y = np.empty((m, n), np.float32)
+    acc = np.empty((m, n), np.int32)
+    lib().orc_w8a8_linear(_ptr(aq), _ptr(sa), _ptr(wq), _ptr(sw), _ptr(bias), m, k, n,
+                          int(relu), _ptr(y), _ptr(acc))
+    return y, acc
+
+
+def relu(x):
+    y = _c(x, np.float32).copy()
+    lib().orc_relu(_ptr(y), y.size)
+    return y
+
+
+# ---------------------------------------------------------------- ternary
+def pack_ternary(v):
+    v = _c(v, np.int8).ravel()
+    out = np.empty((v.size + 15) // 16, np.uint32)
+    lib().orc_pack_ternary(_ptr(v), v.size, _ptr(out))
+    return out
+
+
+def unpack_ternary(packed, count):
+    p = _c(packed, np.uint32)
+    out = np.empty(count, np.int8)
+    lib().orc_unpack_ternary(_ptr(p), count, _ptr(out))
+    return out
+
+
+def ternary_quantize_rows(w):
+    w = _c(w, np.float32)
+    rows, cols = w.shape if w.ndim == 2 else (1, w.size)
+    t = np.empty(rows * cols, np.int8)
+    s = np.empty(rows, np.float32)
+    lib().orc_ternary_quantize_rows(_ptr(w), rows, cols, _ptr(t), _ptr(s))
+    return t.reshape(w.shape), s
+
+
+def ternary_quantize_absmean(w):
+    w = _c(w, np.float32)
+    rows, cols = w.shape
+    t = np.empty((rows, cols), np.int8)
+    g = lib().orc_ternary_quantize_absmean(_ptr(w), rows, cols, _ptr(t))
+    return t, np.float32(g)
+
+
+def ternary_dequantize(packed, numel, scales, cols):
+    p, s = _c(packed, np.uint32), _c(scales, np.float32)
+    w = np.empty(numel, np.float32)
+    lib().orc_ternary_dequantize(_ptr(p), numel, _ptr(s), s.size, cols, _ptr(w))
+    return w
+
+
+def ternary_linear_f32(x, packed, scales, out_f, bias=None):
+    x, p, s = _c(x, np.float32), _c(packed, np.uint32), _c(scales, np.float32)
+    bias = None if bias is None else _c(bias, np.float32)
+    batch, in_f = x.shape
+    y = np.empty((batch, out_f), np.float32)
+    lib().orc_ternary_linear_f32(_ptr(x), batch, in_f, _ptr(p), _ptr(s), out_f,
+                                 _ptr(bias), _ptr(y))
+    return y
+
+
+def ternary_gemm_i8(aq, sa, packed, sw, n, bias=None, relu=False):
+    aq, sa, p, sw = _c(aq, np.int8), _c(sa, np.float32), _c(packed, np.uint32), _c(sw, np.float32)
+    bias = None if bias is None else _c(bias, np.float32)
+    m, k = aq.shape
+    y = np.empty((m, n), np.float32)
+    acc = np.empty((m, n), np.int32)
+    lib().orc_ternary_gemm_i8(_ptr(aq), _ptr(sa), _ptr(p), _ptr(sw), _ptr(bias), m, k, n,
+                              int(relu), _ptr(y), _ptr(acc))
+    return y, acc
+
+
+# ---------------------------------------------------------------- rotors
+def rotor_sandwich(r, x, inverse=False):
+    r, x = _c(r, np.float32), _c(x, np.float32)
+    out = np.empty(8, np.float32)
+    fn = lib().orc_rotor_inv_sandwich if inverse else lib().orc_rotor_sandwich
+    fn(_ptr(r), _ptr(x), _ptr(out))
+    return out
+
+
+def rotor_rotation_matrix(r):
+    r = _c(r, np.float32)
+    out = np.empty(9, np.float32)
+    lib().orc_rotor_rotation_matrix(_ptr(r), _ptr(out))
+    return out.reshape(3, 3)
+
+
+def rotorquant_quantize(x, rotors, bits):
+    """src/quant.rs:212-239. Returns (y, codes [rows,padded], scales [rows,groups])."""
+    x, r = _c(x, np.float32), _c(rotors, np.float32)
+    dim = x.shape[-1]
+    rows = x.size // dim
+    padded = (dim + 2) // 3 * 3
+    y = np.empty(x.shape, np.float32)
+    codes = np.empty((rows, padded), np.int8)
+    scales = np.empty((rows, padded // 3), np.float32)
+    lib().orc_rotorquant_quantize(_ptr(x), rows, dim, bits, _ptr(r), _ptr(y),
+                                  _ptr(codes), _ptr(scales))
+    return y, codes, scales
+
+
+def rotorquant_dequantize(codes, scales, dim, rotors):
+    c, s, r = _c(codes, np.int8), _c(scales, np.float32), _c(rotors, np.float32)
+    rows = c.shape[0]
+    y = np.empty((rows, dim), np.float32)
+    lib().orc_rotorquant_dequantize(_ptr(c), _ptr(s), rows, dim, _ptr(r), _ptr(y))
+    return y
+
+
+def rotors_from_seed(seed, n_groups):
+    """Rotor::random via StdRng (src/quant.rs:39-65, :150-162). Parity unpinned."""
+    out = np.empty((n_groups, 4), np.float32)
+    lib().orc_rotorquant_rotors_from_seed(seed, n_groups, _ptr(out))
+    return out
+
+
+def chacha_block(key_words, counter, stream, rounds):
+    k = _c(key_words, np.uint32)
+    out = np.empty(16, np.uint32)
+    lib().orc_chacha_block(_ptr(k), counter, stream, rounds, _ptr(out))
+    return out
+
+
+def chacha20_block_ietf(key_words, counter, nonce_words):
+    k, nn = _c(key_words, np.uint32), _c(nonce_words, np.uint32)
+    out = np.empty(16, np.uint32)
+    lib().orc_chacha20_block_ietf(_ptr(k), counter, _ptr(nn), _ptr(out))
+    return out

@@ -1,0 +1,52 @@
+// numerics.hpp -- device arithmetic that must round exactly like the Rust
+// reference (every translation unit is compiled with -ffp-contract=off and
+// correctly rounded fp32 division).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rnn {
+
+// f32::clamp: NaN passes through.
+__device__ __forceinline__ float clamp_rs(float x, float lo, float hi) {
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// `f32 as i8` of a value already clamped to [-128, 127]; NaN -> 0.
+__device__ __forceinline__ int8_t to_i8_rs(float v) {
+    return v != v ? (int8_t)0 : (int8_t)(int)v;
+}
+
+// (t).round().clamp(-128.0, 127.0) as i8  -- roundf is half away from zero,
+// like f32::round.
+__device__ __forceinline__ int8_t quant_i8_from_ratio(float t) {
+    return to_i8_rs(clamp_rs(roundf(t), -128.0f, 127.0f));
+}
+
+// (v / s).round().clamp(-128.0, 127.0) as i8 with an IEEE division.
+__device__ __forceinline__ int8_t quant_i8(float v, float s) {
+    return quant_i8_from_ratio(v / s);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Block-wide max of non-negative values; `red` holds BLOCK/64 floats.
+template <int BLOCK>
+__device__ __forceinline__ float block_max(float v, float *red) {
+    v = wave_max(v);
+    const int wid = threadIdx.x / 64, lane = threadIdx.x % 64;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < BLOCK / 64; ++i) m = fmaxf(m, red[i]);
+    return m;
+}
+
+}  // namespace rnn

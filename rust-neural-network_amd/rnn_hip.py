@@ -1,0 +1,304 @@
+"""ctypes binding of librnn_hip.so (include/rnn_hip.h) for Python callers.
+
+Tensors are torch tensors already resident on the GPU (torch is used only for
+device memory and the current stream). Every call goes through the C ABI; a
+non-zero status raises RnnError carrying rnn_last_error(). There is no CPU
+fallback: if the library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librnn_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "rnn_hip.h")
+
+RNN_OK = 0
+RNN_ERR_INVALID_ARG = 1
+RNN_ERR_HIP = 2
+RNN_ERR_UNSUPPORTED = 3
+RNN_ERR_OUT_OF_MEMORY = 4
+
+FLAG_RELU = 0x1
+ALGO_AUTO = 0x00
+ALGO_TILED = 0x10
+ALGO_GEMV = 0x20
+
+TERNARY_ROWS = 0
+TERNARY_ABSMEAN = 1
+
+
+class RnnError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"[rnn status {status}] {msg}")
+        self.status = status
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_UINT = ctypes.c_uint
+
+# name -> (argtypes, restype)
+SIGNATURES = {
+    "rnn_abi_version": ([], _INT),
+    "rnn_last_error": ([], ctypes.c_char_p),
+    "rnn_quant_rows_i8": ([_P, _I64, _I64, _P, _P, _P], _INT),
+    "rnn_int8_dequantize": ([_P, _P, _I64, _I64, _P, _P], _INT),
+    "rnn_int8_matmul_f32": ([_P, _P, _I64, _I64, _P, _I64, _P, _P], _INT),
+    "rnn_int8_linear_forward": ([_P, _I64, _I64, _P, _P, _I64, _P, _P, _P], _INT),
+    "rnn_igemm_workspace_size": ([_I64, _I64, _I64], ctypes.c_size_t),
+    "rnn_igemm": ([_P, _P, _P, _I64, _I64, _I64, _P, ctypes.c_size_t, _P], _INT),
+    "rnn_w8a8_linear": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _UINT, _P, _P, _P], _INT),
+    "rnn_ternary_pack": ([_P, _I64, _P, _P], _INT),
+    "rnn_ternary_unpack": ([_P, _I64, _P, _P], _INT),
+    "rnn_ternary_quantize": ([_P, _I64, _I64, _INT, _P, _P, _P], _INT),
+    "rnn_ternary_dequantize": ([_P, _I64, _P, _I64, _I64, _P, _P], _INT),
+    "rnn_ternary_linear_forward": ([_P, _I64, _I64, _P, _P, _I64, _P, _P, _P], _INT),
+    "rnn_ternary_gemm": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _UINT, _P, _P, _P], _INT),
+    "rnn_rotor_rotation_matrices": ([_P, _I64, _P, _P], _INT),
+    "rnn_rotorquant_quantize": ([_P, _I64, _I64, _INT, _P, _P, _P, _P, _P], _INT),
+    "rnn_rotorquant_dequantize": ([_P, _P, _I64, _I64, _P, _P, _P], _INT),
+}
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/rnn_hip.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(rnn_\w+)\s*\(", text, re.M)))
+
+
+def load():
+    """Load librnn_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RnnError(RNN_ERR_UNSUPPORTED,
+                           f"{LIB_PATH} is missing: run rust-neural-network_amd/build.py")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return load().rnn_last_error().decode()
+
+
+def _check(status: int):
+    if status != RNN_OK:
+        raise RnnError(status, last_error())
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dev(t, dtype, name):
+    import torch
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise RnnError(RNN_ERR_INVALID_ARG, f"{name} must be contiguous")
+    return t
+
+
+def _empty(shape, dtype, like):
+    import torch
+    return torch.empty(shape, dtype=dtype, device=like.device)
+
+
+# ------------------------------------------------------------------ int8
+def quant_rows_i8(x, q=None, scale=None, stream=None):
+    """Per-row symmetric int8 (Int8Weights::quantize rule). Returns (q, scale)."""
+    import torch
+    _dev(x, torch.float32, "x")
+    rows, cols = x.shape
+    q = q if q is not None else _empty((rows, cols), torch.int8, x)
+    scale = scale if scale is not None else _empty((rows,), torch.float32, x)
+    _check(load().rnn_quant_rows_i8(_ptr(x), rows, cols, _ptr(q), _ptr(scale), _stream(stream)))
+    return q, scale
+
+
+def int8_dequantize(q, scale, stream=None):
+    import torch
+    _dev(q, torch.int8, "q"), _dev(scale, torch.float32, "scale")
+    w = _empty(q.shape, torch.float32, q)
+    _check(load().rnn_int8_dequantize(_ptr(q), _ptr(scale), q.shape[0], q.shape[1], _ptr(w),
+                                      _stream(stream)))
+    return w
+
+
+def int8_matmul_f32(wq, ws, x, stream=None):
+    import torch
+    _dev(wq, torch.int8, "wq"), _dev(ws, torch.float32, "ws"), _dev(x, torch.float32, "x")
+    out_f, in_f = wq.shape
+    m = x.numel() // in_f
+    y = _empty((m, out_f), torch.float32, x)
+    _check(load().rnn_int8_matmul_f32(_ptr(wq), _ptr(ws), out_f, in_f, _ptr(x), m, _ptr(y),
+                                      _stream(stream)))
+    return y
+
+
+def int8_linear_forward(x, wq, ws, bias=None, stream=None):
+    import torch
+    _dev(x, torch.float32, "x"), _dev(wq, torch.int8, "wq"), _dev(ws, torch.float32, "ws")
+    _dev(bias, torch.float32, "bias")
+    batch, in_f = x.shape
+    out_f = wq.shape[0]
+    y = _empty((batch, out_f), torch.float32, x)
+    _check(load().rnn_int8_linear_forward(_ptr(x), batch, in_f, _ptr(wq), _ptr(ws), out_f,
+                                          _ptr(bias), _ptr(y), _stream(stream)))
+    return y
+
+
+def igemm_workspace_size(m, k, n) -> int:
+    return int(load().rnn_igemm_workspace_size(m, k, n))
+
+
+def igemm(a_u8, b_i8, m, k, n, workspace=None, c=None, stream=None):
+    """igemm contract: a u8 [m,k], b i8 [k,n] -> c i32 [m,n]."""
+    import torch
+    _dev(a_u8, torch.uint8, "a"), _dev(b_i8, torch.int8, "b")
+    c = c if c is not None else _empty((m, n), torch.int32, a_u8)
+    wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(load().rnn_igemm(_ptr(a_u8), _ptr(b_i8), _ptr(c), m, k, n, _ptr(workspace), wsb,
+                            _stream(stream)))
+    return c
+
+
+def w8a8_linear(aq, sa, wq, sw, bias=None, relu=False, algo=ALGO_AUTO, want_y=True,
+                want_acc=False, y=None, acc=None, stream=None):
+    """Returns (y f32 [m,n] or None, acc i32 [m,n] or None)."""
+    import torch
+    _dev(aq, torch.int8, "aq"), _dev(wq, torch.int8, "wq")
+    _dev(sa, torch.float32, "sa"), _dev(sw, torch.float32, "sw"), _dev(bias, torch.float32, "bias")
+    m, k = aq.shape
+    n = wq.shape[0]
+    if want_y and y is None:
+        y = _empty((m, n), torch.float32, aq)
+    if want_acc and acc is None:
+        acc = _empty((m, n), torch.int32, aq)
+    flags = (FLAG_RELU if relu else 0) | algo
+    _check(load().rnn_w8a8_linear(_ptr(aq), _ptr(sa), _ptr(wq), _ptr(sw), _ptr(bias), m, k, n,
+                                  flags, _ptr(y), _ptr(acc), _stream(stream)))
+    return y, acc
+
+
+# ------------------------------------------------------------------ ternary
+def ternary_pack(t, stream=None):
+    import torch
+    _dev(t, torch.int8, "t")
+    count = t.numel()
+    packed = _empty(((count + 15) // 16,), torch.int32, t)
+    _check(load().rnn_ternary_pack(_ptr(t), count, _ptr(packed), _stream(stream)))
+    return packed
+
+
+def ternary_unpack(packed, count, stream=None):
+    import torch
+    _dev(packed, torch.int32, "packed")
+    t = _empty((count,), torch.int8, packed)
+    _check(load().rnn_ternary_unpack(_ptr(packed), count, _ptr(t), _stream(stream)))
+    return t
+
+
+def ternary_quantize(w, mode=TERNARY_ROWS, stream=None):
+    """Returns (packed int32 words [ceil(numel/16)], scales f32 [rows])."""
+    import torch
+    _dev(w, torch.float32, "w")
+    rows, cols = w.shape
+    packed = _empty(((rows * cols + 15) // 16,), torch.int32, w)
+    scales = _empty((rows,), torch.float32, w)
+    _check(load().rnn_ternary_quantize(_ptr(w), rows, cols, mode, _ptr(packed), _ptr(scales),
+                                       _stream(stream)))
+    return packed, scales
+
+
+def ternary_dequantize(packed, numel, scales, cols, stream=None):
+    import torch
+    _dev(packed, torch.int32, "packed"), _dev(scales, torch.float32, "scales")
+    w = _empty((numel,), torch.float32, packed)
+    _check(load().rnn_ternary_dequantize(_ptr(packed), numel, _ptr(scales), scales.numel(), cols,
+                                         _ptr(w), _stream(stream)))
+    return w
+
+
+def ternary_linear_forward(x, packed, scales, out_f, bias=None, stream=None):
+    import torch
+    _dev(x, torch.float32, "x"), _dev(packed, torch.int32, "packed")
+    _dev(scales, torch.float32, "scales"), _dev(bias, torch.float32, "bias")
+    batch, in_f = x.shape
+    y = _empty((batch, out_f), torch.float32, x)
+    _check(load().rnn_ternary_linear_forward(_ptr(x), batch, in_f, _ptr(packed), _ptr(scales),
+                                             out_f, _ptr(bias), _ptr(y), _stream(stream)))
+    return y
+
+
+def ternary_gemm(aq, sa, packed, sw, n, bias=None, relu=False, want_y=True, want_acc=False,
+                 y=None, stream=None):
+    import torch
+    _dev(aq, torch.int8, "aq"), _dev(packed, torch.int32, "packed")
+    _dev(sa, torch.float32, "sa"), _dev(sw, torch.float32, "sw"), _dev(bias, torch.float32, "bias")
+    m, k = aq.shape
+    if want_y and y is None:
+        y = _empty((m, n), torch.float32, aq)
+    acc = _empty((m, n), torch.int32, aq) if want_acc else None
+    _check(load().rnn_ternary_gemm(_ptr(aq), _ptr(sa), _ptr(packed), _ptr(sw), _ptr(bias), m, k,
+                                   n, FLAG_RELU if relu else 0, _ptr(y), _ptr(acc),
+                                   _stream(stream)))
+    return y, acc
+
+
+# ------------------------------------------------------------------ RotorQuant
+def rotation_matrices(rotors, stream=None):
+    import torch
+    _dev(rotors, torch.float32, "rotors")
+    n = rotors.shape[0]
+    out = _empty((n, 3, 3), torch.float32, rotors)
+    _check(load().rnn_rotor_rotation_matrices(_ptr(rotors), n, _ptr(out), _stream(stream)))
+    return out
+
+
+def rotorquant_quantize(x, rotors, bits, want_y=True, want_codes=False, y=None, stream=None):
+    """Returns (y or None, codes int8 [rows,padded] or None, scales [rows,groups] or None)."""
+    import torch
+    _dev(x, torch.float32, "x"), _dev(rotors, torch.float32, "rotors")
+    dim = x.shape[-1]
+    rows = x.numel() // dim
+    ng = (dim + 2) // 3
+    if want_y and y is None:
+        y = _empty(tuple(x.shape), torch.float32, x)
+    codes = _empty((rows, 3 * ng), torch.int8, x) if want_codes else None
+    scales = _empty((rows, ng), torch.float32, x) if want_codes else None
+    _check(load().rnn_rotorquant_quantize(_ptr(x), rows, dim, bits, _ptr(rotors), _ptr(y),
+                                          _ptr(codes), _ptr(scales), _stream(stream)))
+    return y, codes, scales
+
+
+def rotorquant_dequantize(codes, scales, dim, rotors, stream=None):
+    import torch
+    _dev(codes, torch.int8, "codes"), _dev(scales, torch.float32, "scales")
+    _dev(rotors, torch.float32, "rotors")
+    rows = codes.shape[0]
+    y = _empty((rows, dim), torch.float32, codes)
+    _check(load().rnn_rotorquant_dequantize(_ptr(codes), _ptr(scales), rows, dim, _ptr(rotors),
+                                            _ptr(y), _stream(stream)))
+    return y

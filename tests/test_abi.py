@@ -1,0 +1,112 @@
+"""CPU-only checks of the C ABI: the library loads, exports every symbol that
+include/rnn_hip.h declares, and rejects bad arguments before touching a GPU
+(the reference panics on these; the ABI returns a status code instead)."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+
+import rnn_hip as H
+
+FAKE = ctypes.c_void_p(256)  # never dereferenced: every case fails validation first
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(H.LIB_PATH):
+        import build as B
+        B.build()
+    return H.load()
+
+
+def test_header_symbols_are_exported(lib):
+    names = H.header_symbols()
+    assert len(names) >= 18
+    out = subprocess.run(["nm", "-D", "--defined-only", H.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    assert sorted(H.SIGNATURES) == names  # the binding covers the whole header
+
+
+def test_abi_version(lib):
+    assert lib.rnn_abi_version() == 1
+
+
+def _status(rc, code, needle):
+    assert rc == code, H.last_error()
+    assert needle in H.last_error()
+
+
+def test_negative_sizes_rejected(lib):
+    _status(lib.rnn_quant_rows_i8(FAKE, -1, 4, FAKE, FAKE, None), H.RNN_ERR_INVALID_ARG, "negative")
+    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 4, -16, 4, 0, FAKE, None, None),
+            H.RNN_ERR_INVALID_ARG, "negative")
+    _status(lib.rnn_igemm(FAKE, FAKE, FAKE, 1, 1, -1, None, 0, None), H.RNN_ERR_INVALID_ARG,
+            "negative")
+
+
+def test_gemm_argument_rules(lib):
+    # unknown flag bits
+    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 4, 16, 4, 0x100, FAKE, None, None),
+            H.RNN_ERR_INVALID_ARG, "unknown flags")
+    # neither output requested
+    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 4, 16, 4, 0, None, None, None),
+            H.RNN_ERR_INVALID_ARG, "both null")
+    # float output needs the scales
+    _status(lib.rnn_w8a8_linear(FAKE, None, FAKE, FAKE, None, 4, 16, 4, 0, FAKE, None, None),
+            H.RNN_ERR_INVALID_ARG, "requires sa")
+    # k must be a multiple of 16
+    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 4, 17, 4, 0, FAKE, None, None),
+            H.RNN_ERR_UNSUPPORTED, "multiple of 16")
+    # GEMV forced beyond 16 rows
+    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 17, 16, 4, H.ALGO_GEMV, FAKE, None,
+                                None), H.RNN_ERR_INVALID_ARG, "m <= 16")
+    _status(lib.rnn_ternary_gemm(FAKE, FAKE, FAKE, FAKE, None, 4, 20, 4, 0, FAKE, None, None),
+            H.RNN_ERR_UNSUPPORTED, "multiple of 16")
+
+
+def test_empty_shapes_are_noops(lib):
+    assert lib.rnn_w8a8_linear(None, None, None, None, None, 0, 16, 4, 0, None, None, None) == 0
+    assert lib.rnn_quant_rows_i8(None, 0, 5, None, None, None) == 0
+    assert lib.rnn_ternary_pack(None, 0, None, None) == 0
+    assert lib.rnn_rotorquant_quantize(None, 0, 12, 4, None, None, None, None, None) == 0
+
+
+def test_rotorquant_argument_rules(lib):
+    # RotorQuant needs at least 2 bits (src/quant.rs:136)
+    _status(lib.rnn_rotorquant_quantize(FAKE, 1, 12, 1, FAKE, FAKE, None, None, None),
+            H.RNN_ERR_INVALID_ARG, "at least 2 bits")
+    # int8 codes hold at most 8 bits
+    _status(lib.rnn_rotorquant_quantize(FAKE, 1, 12, 9, FAKE, None, FAKE, FAKE, None),
+            H.RNN_ERR_INVALID_ARG, "out of range")
+    _status(lib.rnn_rotorquant_quantize(FAKE, 1, 0, 4, FAKE, FAKE, None, None, None),
+            H.RNN_ERR_INVALID_ARG, "dim")
+    _status(lib.rnn_rotorquant_quantize(FAKE, 1, 4000, 4, FAKE, FAKE, None, None, None),
+            H.RNN_ERR_UNSUPPORTED, "unsupported")
+    _status(lib.rnn_ternary_quantize(FAKE, 2, 2, 7, FAKE, FAKE, None), H.RNN_ERR_INVALID_ARG,
+            "bad mode")
+
+
+def test_igemm_workspace_size(lib):
+    assert lib.rnn_igemm_workspace_size(0, 5, 5) == 0
+    # A' [m, kp] + B^T [n, kp] + colsum [n], each rounded up to 256 bytes, kp = ceil64(k)
+    assert lib.rnn_igemm_workspace_size(3, 5, 7) == 256 + 512 + 256
+    assert lib.rnn_igemm_workspace_size(2048, 4096, 14336) == 2048 * 4096 + 14336 * 4096 + 14336 * 4
+
+
+def test_product_path_has_no_cpu_fallback():
+    # the binding refuses to run without the HIP library (no silent fallback)
+    import importlib
+    mod = importlib.reload(H)
+    saved = mod.LIB_PATH
+    try:
+        mod.LIB_PATH = "/nonexistent/librnn_hip.so"
+        mod._lib = None
+        with pytest.raises(mod.RnnError):
+            mod.load()
+    finally:
+        mod.LIB_PATH = saved
+        mod._lib = None

@@ -1,0 +1,218 @@
+"""GPU parity: int8 quantization, igemm and W8A8 GEMM/GEMV through the C ABI
+against the CPU oracle. int32 accumulators and int8 codes must be bit-exact;
+fp32 outputs are required bit-exact too (same expressions, no contraction),
+which is stricter than the 1e-5 relative contract."""
+import numpy as np
+import pytest
+
+import oracle as O
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-5  # the contract; the assertions below demand exact equality
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def assert_f32_equal(got, exp):
+    assert got.shape == exp.shape
+    bad = ~((got == exp) | (np.isnan(got) & np.isnan(exp)))
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        rel = np.abs(got[bad] - exp[bad]) / np.maximum(np.abs(exp[bad]), 1e-30)
+        raise AssertionError(f"{bad.sum()} mismatches, first at {i}: {got[tuple(i)]} vs "
+                             f"{exp[tuple(i)]}; max rel {rel.max():.3g} (contract {REL_TOL})")
+
+
+# ------------------------------------------------------------------ quantization
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (16, 4096), (33, 784), (7, 13), (5, 1), (3, 0),
+                                       (2048, 4096)])
+def test_quant_rows_i8_parity(dev, hip, rows, cols):
+    x = W.activations(rows, cols, seed=rows * 7 + cols, outlier_frac=0.01)
+    if rows > 2:
+        x[1] = 0.0
+        x[2, : min(cols, 3)] = np.float32(2.5) * np.float32(1e-3)
+    q, s = hip.quant_rows_i8(to_dev(x, dev))
+    qo, so = O.quant_rows_i8(x)
+    assert np.array_equal(host(s), so)
+    assert np.array_equal(host(q), qo)
+
+
+def test_quant_rows_nan_and_unaligned(dev, hip):
+    import torch
+    x = W.activations(4, 33, seed=1)
+    x[0, 5] = np.nan
+    buf = to_dev(np.concatenate([np.zeros(1, np.float32), x.ravel()]), dev)
+    xv = buf[1:].view(4, 33)  # 4-byte aligned only: exercises the scalar path
+    q = torch.empty((4, 33), dtype=torch.int8, device=dev)
+    s = torch.empty(4, dtype=torch.float32, device=dev)
+    hip.quant_rows_i8(xv, q, s)
+    qo, so = O.quant_rows_i8(x)
+    assert np.array_equal(host(s), so) and np.array_equal(host(q), qo)
+
+
+def test_int8_dequantize_parity(dev, hip):
+    w = W.weights(64, 200, seed=2)
+    qo, so = O.quant_rows_i8(w)
+    got = host(hip.int8_dequantize(to_dev(qo, dev), to_dev(so, dev)))
+    assert np.array_equal(got, O.int8_dequantize(qo, so))
+
+
+# ------------------------------------------------------------------ reference Int8Linear
+@pytest.mark.parametrize("batch,in_f,out_f", [(2, 8, 4), (32, 784, 256), (3, 17, 300)])
+def test_int8_linear_forward_parity(dev, hip, batch, in_f, out_f):
+    w = W.weights(out_f, in_f, seed=in_f)
+    x = W.activations(batch, in_f, seed=out_f) * np.float32(0.01)
+    bias = W.activations(1, out_f, seed=3)[0]
+    wq, ws = O.quant_rows_i8(w)
+    got = host(hip.int8_linear_forward(to_dev(x, dev), to_dev(wq, dev), to_dev(ws, dev),
+                                       to_dev(bias, dev)))
+    assert_f32_equal(got, O.int8_linear_forward(x, wq, ws, bias))
+    got = host(hip.int8_linear_forward(to_dev(x, dev), to_dev(wq, dev), to_dev(ws, dev)))
+    assert_f32_equal(got, O.int8_linear_forward(x, wq, ws))
+
+
+def test_int8_matmul_f32_parity(dev, hip):
+    w = W.weights(50, 96, seed=4)
+    x = W.activations(6, 96, seed=5) * np.float32(0.02)
+    wq, ws = O.quant_rows_i8(w)
+    got = host(hip.int8_matmul_f32(to_dev(wq, dev), to_dev(ws, dev), to_dev(x, dev)))
+    assert_f32_equal(got, O.int8_matmul_f32(wq, ws, x))
+
+
+# ------------------------------------------------------------------ igemm
+def lcg_case(m, k, n):
+    a, s = O.lcg_bytes(1, m * k, signed=False)
+    b, _ = O.lcg_bytes(s, k * n, signed=True)
+    return a.view(np.uint8).reshape(m, k), b.reshape(k, n)
+
+
+def test_igemm_known_small(dev, hip):
+    # src/int8.rs:416-422
+    a = to_dev(np.array([[1, 2, 3, 4]], np.uint8), dev)
+    b = to_dev(np.array([1, -1, 2, 2, -3, 4, 0, -2], np.int8).reshape(4, 2), dev)
+    assert host(hip.igemm(a, b, 1, 4, 2)).ravel().tolist() == [-4, 7]
+
+
+@pytest.mark.parametrize("shape", [(16, 32, 48), (3, 5, 7), (13, 17, 29), (1, 1, 1), (4, 4, 16),
+                                   (33, 9, 33), (64, 64, 64)])
+def test_igemm_lcg_shapes(dev, hip, shape):
+    # src/int8.rs:425-433 (worst abs diff must be 0)
+    m, k, n = shape
+    a, b = lcg_case(m, k, n)
+    got = host(hip.igemm(to_dev(a, dev), to_dev(b, dev), m, k, n))
+    assert np.array_equal(got, O.igemm_scalar(a, b, m, k, n))
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 512, 512), (17, 300, 1000), (300, 4096, 129)])
+def test_igemm_full_u8_range(dev, hip, m, k, n):
+    # benches/core_ops.rs:152-153 inputs: a = i % 251 (u8), b = i % 255 (as i8)
+    a = (np.arange(m * k) % 251).astype(np.uint8).reshape(m, k)
+    b = (np.arange(k * n) % 255).astype(np.uint8).view(np.int8).reshape(k, n)
+    import torch
+    ws = torch.empty(hip.igemm_workspace_size(m, k, n), dtype=torch.uint8, device=dev)
+    got = host(hip.igemm(to_dev(a, dev), to_dev(b, dev), m, k, n, workspace=ws))
+    exp, _ = O.igemm(a, b, m, k, n, 8)
+    assert np.array_equal(got, exp)
+
+
+def test_igemm_wrapping(dev, hip):
+    m, k, n = 2, 70016, 3
+    a = np.full((m, k), 255, np.uint8)
+    b = np.full((k, n), 127, np.int8)
+    got = host(hip.igemm(to_dev(a, dev), to_dev(b, dev), m, k, n))
+    assert np.array_equal(got, O.igemm_scalar(a, b, m, k, n))
+
+
+# ------------------------------------------------------------------ W8A8
+def w8a8_case(m, k, n, seed, outliers=0.0):
+    w = W.weights(n, k, seed=seed)
+    x = W.activations(m, k, seed=seed + 1, outlier_frac=outliers)
+    wq, sw = O.quant_rows_i8(w)
+    aq, sa = O.quant_rows_i8(x)
+    bias = W.activations(1, n, seed=seed + 2)[0] * np.float32(0.1)
+    return aq, sa, wq, sw, bias
+
+
+def run_w8a8(dev, hip, aq, sa, wq, sw, bias, relu, algo):
+    y, acc = hip.w8a8_linear(to_dev(aq, dev), to_dev(sa, dev), to_dev(wq, dev), to_dev(sw, dev),
+                             None if bias is None else to_dev(bias, dev), relu=relu, algo=algo,
+                             want_acc=True)
+    return host(y), host(acc)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 64, 16), (16, 64, 16), (5, 48, 37), (64, 256, 128),
+                                   (130, 784, 257), (200, 1024, 300), (32, 784, 256), (32, 128, 10)])
+@pytest.mark.parametrize("algo", ["auto", "tiled"])
+def test_w8a8_small_shapes(dev, hip, m, k, n, algo):
+    aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=m + k + n)
+    a = hip.ALGO_AUTO if algo == "auto" else hip.ALGO_TILED
+    for relu, b in ((False, None), (True, bias)):
+        y, acc = run_w8a8(dev, hip, aq, sa, wq, sw, b, relu, a)
+        ye, acce = O.w8a8_linear(aq, sa, wq, sw, b, relu)
+        assert np.array_equal(acc, acce)
+        assert_f32_equal(y, ye)
+
+
+@pytest.mark.parametrize("m,k,n", W.GEMV_SHAPES)
+def test_w8a8_decode_gemv_full_size(dev, hip, m, k, n):
+    # BASELINE decode config: 1% activation outliers x20
+    aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=n + m, outliers=0.01)
+    y, acc = run_w8a8(dev, hip, aq, sa, wq, sw, None, False, hip.ALGO_AUTO)
+    ye, acce = O.w8a8_linear(aq, sa, wq, sw)
+    assert np.array_equal(acc, acce)
+    assert_f32_equal(y, ye)
+    # the tiled kernel agrees with the GEMV bit for bit
+    y2, acc2 = run_w8a8(dev, hip, aq, sa, wq, sw, None, False, hip.ALGO_TILED)
+    assert np.array_equal(acc2, acc) and np.array_equal(y2, y)
+
+
+def test_w8a8_prefill_full_size_sampled_rows(dev, hip):
+    """BASELINE prefill config (2048 x 4096 x 14336): every output of 24
+    sampled rows (covering all 16 row tiles) against the oracle, plus the
+    row-sum identity sum_n acc[m,n] = a[m,:] . (sum_n w[n,:]) for all rows."""
+    import torch
+    c = W.PREFILL
+    m, k, n = c["m"], c["k"], c["n"]
+    aq, sa, wq, sw, _ = w8a8_case(m, k, n, seed=99)
+    y, acc = hip.w8a8_linear(to_dev(aq, dev), to_dev(sa, dev), to_dev(wq, dev), to_dev(sw, dev),
+                             want_acc=True)
+    rows = np.unique(np.concatenate([np.arange(0, m, 128) + 127, W.rng(1).integers(0, m, 8)]))
+    ye, acce = O.w8a8_linear(aq[rows], sa[rows], wq, sw)
+    assert np.array_equal(host(acc[torch.as_tensor(rows, device=dev)]), acce)
+    assert_f32_equal(host(y[torch.as_tensor(rows, device=dev)]), ye)
+    wsum = wq.astype(np.int64).sum(axis=0)
+    rowsum = aq.astype(np.int64) @ wsum
+    got = host(acc.to(torch.int64).sum(dim=1))
+    assert np.array_equal(got, rowsum)
+
+
+def test_w8a8_mlp_784_256_128_10(dev, hip):
+    """int8 MLP 784-256-128-10, batch 32, per-channel
+    weights, per-row activations, bias + ReLU between layers, chained on the
+    device (quantize -> W8A8 -> quantize ...) against the oracle chain."""
+    layers = W.MLP_LAYERS
+    x = W.activations(W.MLP_BATCH, layers[0], seed=1)
+    params = []
+    for i, (fi, fo) in enumerate(zip(layers[:-1], layers[1:])):
+        wq, sw = O.quant_rows_i8(W.weights(fo, fi, seed=10 + i))
+        b = W.weights(1, fo, seed=20 + i)[0]
+        params.append((wq, sw, b))
+    h_ref = x
+    h = to_dev(x, dev)
+    for i, (wq, sw, b) in enumerate(params):
+        relu = i < len(params) - 1
+        aq, sa = O.quant_rows_i8(h_ref)
+        h_ref, _ = O.w8a8_linear(aq, sa, wq, sw, b, relu)
+        aq_d, sa_d = hip.quant_rows_i8(h)
+        h, _ = hip.w8a8_linear(aq_d, sa_d, to_dev(wq, dev), to_dev(sw, dev), to_dev(b, dev),
+                               relu=relu)
+    assert_f32_equal(host(h), h_ref)
