@@ -107,7 +107,8 @@ __global__ __launch_bounds__(kRqThreads) void rotorquant_kernel(
         __syncthreads();
         const int work = nv * ng;
         for (int f = tid; f < work; f += kRqThreads) {
-            int v = (int)__umulhi((uint32_t)f, ng_magic);
+            // ng == 1 has no 32-bit magic (2^32 overflows): v = f directly
+            int v = ng == 1 ? f : (int)__umulhi((uint32_t)f, ng_magic);
             int g = f - v * ng;
             if (g >= ng) { g -= ng; ++v; }
             if (g < 0) { g += ng; --v; }
@@ -202,7 +203,7 @@ extern "C" int rnn_rotorquant_quantize(const float *x, int64_t rows, int64_t dim
     RNN_REQUIRE(rows * ng < 0x7fffffffLL * 16, "%s: too many rows", name);
     const int vpt = std::max<int>(1, kRqTileFloats / (int)dim);
     const float qmax = (float)((1u << (bits - 1)) - 1u);
-    const uint32_t magic = (uint32_t)((0x100000000ULL + ng - 1) / ng);
+    const uint32_t magic = ng > 1 ? (uint32_t)((0x100000000ULL + ng - 1) / ng) : 0u;
     const int64_t ntiles = ceil_div(rows, vpt);
     const unsigned grid = (unsigned)std::min<int64_t>(ntiles, 4 * device_cu_count());
     const bool vec = dim % 4 == 0 && ((uintptr_t)x % 16) == 0 && (!y || ((uintptr_t)y % 16) == 0);
