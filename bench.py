@@ -169,6 +169,24 @@ def bench_rotorquant(H, W, dev, steps):
             "launches_per_step": 2}
 
 
+# ---------------------------------------------------------------- copy ceiling
+COPY_BYTES = 512 * 2**20
+
+
+def bench_copy(dev, steps):
+    """The measured HBM ceiling: a plain device-to-device copy of COPY_BYTES
+    (read + write = 2 * COPY_BYTES of traffic per launch). The same launch is
+    the known-size reference that FETCH_SIZE / WRITE_SIZE counters are scaled
+    by when HBM traffic per kernel is derived from rocprofv3 --pmc runs."""
+    import torch
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    ms = timed(lambda: dst.copy_(src), max(steps, 20), 5)
+    gbs = 2 * COPY_BYTES / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_launch": 2 * COPY_BYTES}
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline(state, sample_rows=256, repeats=3):
     """The reference CPU path for the prefill GEMM on the first `sample_rows`
@@ -210,12 +228,13 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    choices=["all", "prefill", "gemv", "ternary", "rotorquant"])
+                    choices=["all", "prefill", "gemv", "ternary", "rotorquant", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
-              "(this build has no multi-GPU path; see DESIGN.md for how it would shard)",
+              "(the quantized-inference path runs on one GPU; every kernel shards by output "
+              "columns or KV heads, with no collective on the hot path)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -260,6 +279,9 @@ def main():
     if args.only in ("all", "rotorquant"):
         log("RotorQuant K+V [8,32,4096,128] 4-bit round trip")
         components["rotorquant_kv"] = bench_rotorquant(H, W, dev, args.steps)
+    if args.only in ("all", "copy"):
+        log("streaming copy ceiling: 512 MiB device-to-device")
+        components["copy_ceiling"] = bench_copy(dev, args.steps)
     if components:
         result["components"] = components
     if "value" not in result:  # a single non-headline component was requested

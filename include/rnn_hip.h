@@ -41,9 +41,10 @@ enum rnn_status {
 
 /* flags for the GEMM entry points */
 #define RNN_FLAG_RELU 0x1u          /* y = max(y, 0) after bias (src/tensor.rs:2025-2032) */
-#define RNN_ALGO_AUTO 0x00u         /* GEMV for m <= 16, MFMA tiles otherwise */
-#define RNN_ALGO_TILED 0x10u        /* force the MFMA tiled GEMM              */
+#define RNN_ALGO_AUTO 0x00u         /* GEMV for m <= 16, else LDS-DMA tiles (k % 128 == 0, n % 4 == 0) or register-staged tiles */
+#define RNN_ALGO_TILED 0x10u        /* force the register-staged 128x128 MFMA GEMM */
 #define RNN_ALGO_GEMV 0x20u         /* force the skinny GEMV (m <= 16)        */
+#define RNN_ALGO_TILED_DMA 0x30u    /* force the LDS-DMA pipelined big-tile GEMM (k % 128 == 0, n % 4 == 0) */
 #define RNN_ALGO_MASK 0xF0u
 
 int rnn_abi_version(void);

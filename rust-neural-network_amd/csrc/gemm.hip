@@ -229,6 +229,310 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_tiled_kernel(
         }
 }
 
+// ------------------------------------------------- LDS-DMA pipelined GEMM
+// The large-shape kernel (prefill). Requires K % 64 == 0.
+//
+//  * Block tile BM x BN, WGM x WGN waves, each wave a (BM/WGM) x (BN/WGN)
+//    register tile of 16x16x64 MFMA blocks whose int32 accumulators live in
+//    the AGPR file (128x128 per wave = all 256 AGPRs; one wave per SIMD).
+//  * Operands go global -> LDS with global_load_lds_dwordx4 (no VGPR
+//    staging, no ds_write): every wave instruction moves 1 KiB = 16 tile rows
+//    x 64 B, lane l landing at byte 16*l. The 16-byte chunk order inside a
+//    row is XOR-swizzled (lane l fetches logical chunk (l&3) ^ swz16(row)),
+//    so the fragment reads (16 rows x one chunk per quarter-wave) hit 8
+//    distinct bank groups per 8 lanes.
+//  * STAGES LDS buffers, loads issued STAGES-1 K-steps ahead; each step waits
+//    only for its own stage (s_waitcnt vmcnt(n)) before the block barrier.
+//  * MFMA operand roles are swapped (A-operand = weight rows n, B-operand =
+//    activation rows m), so a lane's 4 accumulator registers are 4
+//    consecutive n of one m: the epilogue writes 16-byte float4 / int4.
+//  * Tiles are ordered so that the blocks the hardware places on one XCD
+//    (block id b goes to XCD b % 8) cover a compact range of tiles that
+//    share A rows and B columns in that XCD's L2.
+constexpr int kDmaBK = 64;
+
+// Swizzle of the 16-byte chunk index by tile row (depends on row & 15 only,
+// so a lane's swizzle is the same for every fragment it reads).
+__device__ __forceinline__ int swz16(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
+// acc += a . b on v_mfma_i32_16x16x64_i8 with the accumulator tied to an
+// AGPR quad. (Device pass only: the host pass parses but never emits kernel
+// bodies, and "a" is not an AGPR constraint there.)
+// ORDERED adds a memory clobber, so that the LDS reads and DMA issues placed
+// between such MFMAs in the source stay interleaved with them.
+template <bool ORDERED = false>
+__device__ __forceinline__ void mfma_i8_acc(v4i &acc, const v4i &a, const v4i &b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    if (ORDERED)
+        asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b) : "memory");
+    else
+        asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+#endif
+}
+
+// 16-byte global -> LDS DMA (global_load_lds_dwordx4): lane l's 16 bytes land
+// at lds + 16*l; `lds` must be wave-uniform. (Device pass only: the host pass
+// rejects the builtin with a const source and would silently drop the
+// kernel's launch stub.)
+__device__ __forceinline__ void dma16(const void *g, void *lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(const_cast<void *>(g),
+                                     (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+#endif
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int WGM, int WGN, int STAGES>
+struct DmaCfg {
+    static constexpr int NW = WGM * WGN;
+    static constexpr int NT = NW * 64;
+    static constexpr int WM = BM / WGM, WN = BN / WGN;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int A_INS = BM / 16, B_INS = BN / 16;  // 1 KiB wave loads per stage
+    static constexpr int INS = A_INS + B_INS;
+    // Every wave issues INS_PER_WAVE loads per stage; when INS does not split
+    // evenly the extra slots re-load a valid row into padding at the end of
+    // the stage, so the load count (and vmcnt threshold) is the same for all.
+    static constexpr int INS_PER_WAVE = (INS + NW - 1) / NW;
+    static constexpr int INS_MIN = INS_PER_WAVE;
+    static constexpr int STAGE_BYTES = INS_PER_WAVE * NW * 1024;
+    static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+    static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be a multiple of 16");
+    static_assert(BM % WGM == 0 && BN % WGN == 0, "waves must split the tile");
+    static_assert(INS_MIN >= 1 && STAGES >= 2, "pipeline shape");
+    static_assert((STAGES - 2) * INS_MIN < 64, "vmcnt range");
+    static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+};
+
+// Tile coordinates of block b. When the tile count splits evenly over the 8
+// XCDs, XCD x (blocks b with b % 8 == x) gets the contiguous tile range
+// [x*T/8, (x+1)*T/8), walked with m fastest.
+__device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int &tm, int &tn) {
+    const int T = tiles_m * tiles_n;
+    const int t = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+    tm = t % tiles_m;
+    tn = t / tiles_m;
+}
+
+// Epilogue of 4 consecutive columns n..n+3 of row m (a lane's 4 MFMA
+// registers), 16-byte stores. The host guarantees N % 4 == 0 and 16-byte
+// aligned y / acc_out / sw / bias / colsum for this path, so n..n+3 are all in
+// range whenever n is. swv/bv hold sw[n..n+3] and bias[n..n+3].
+template <bool OUT_Y, bool OUT_ACC>
+__device__ __forceinline__ void epi_store4(const Epilogue &epi, int64_t m, int64_t n,
+                                           const v4i &acc, float sam, const float4 &swv,
+                                           const float4 &bv) {
+    if (m >= epi.M || n >= epi.N) return;
+    if (OUT_ACC) {
+        v4i o = acc;
+        if (epi.colsum) {
+            const v4i cs = *reinterpret_cast<const v4i *>(epi.colsum + n);
+            o.x = (int)((uint32_t)o.x + 128u * (uint32_t)cs.x);
+            o.y = (int)((uint32_t)o.y + 128u * (uint32_t)cs.y);
+            o.z = (int)((uint32_t)o.z + 128u * (uint32_t)cs.z);
+            o.w = (int)((uint32_t)o.w + 128u * (uint32_t)cs.w);
+        }
+        *reinterpret_cast<v4i *>(epi.acc_out + m * epi.N + n) = o;
+    }
+    if (OUT_Y) {
+        float4 v;
+        v.x = (float)acc.x * sam * swv.x;
+        v.y = (float)acc.y * sam * swv.y;
+        v.z = (float)acc.z * sam * swv.z;
+        v.w = (float)acc.w * sam * swv.w;
+        if (epi.bias) {
+            v.x = v.x + bv.x;
+            v.y = v.y + bv.y;
+            v.z = v.z + bv.z;
+            v.w = v.w + bv.w;
+        }
+        if (epi.relu) {
+            v.x = fmaxf(v.x, 0.0f);
+            v.y = fmaxf(v.y, 0.0f);
+            v.z = fmaxf(v.z, 0.0f);
+            v.w = fmaxf(v.w, 0.0f);
+        }
+        *reinterpret_cast<float4 *>(epi.y + m * epi.N + n) = v;
+    }
+}
+
+// Fragments of one K step held in registers: FM activation blocks, FN weight
+// blocks (16 rows x 64 B each, one 16-byte chunk per lane).
+template <int FM, int FN>
+struct Frags {
+    v4i a[FM];
+    v4i b[FN];
+};
+
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool OUT_Y, bool OUT_ACC>
+__global__ __launch_bounds__(WGM *WGN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
+                     int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
+    using C = DmaCfg<BM, BN, WGM, WGN, STAGES>;
+    using F = Frags<C::FM, C::FN>;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[C::LDS_BYTES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tm, tn;
+    xcd_tile((int)blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t bm0 = (int64_t)tm * BM, bn0 = (int64_t)tn * BN;
+    const int nk = (int)(K / kDmaBK);  // even, >= 2 (host-checked)
+
+    // Global sources of this wave's DMA loads at k = 0. Instruction j of a
+    // stage fills LDS bytes [1024 j, 1024 j + 1024): A-tile rows for
+    // j < A_INS, then B-tile rows (a stage is [A tile | B tile]).
+    const int8_t *src[C::INS_PER_WAVE];
+    {
+        const int rr = lane >> 2, pc = lane & 3;
+#pragma unroll
+        for (int i = 0; i < C::INS_PER_WAVE; ++i) {
+            const int j = std::min(wid + i * C::NW, C::INS - 1);  // padding slots: last row block
+            if (j < C::A_INS) {
+                const int r = 16 * j + rr;
+                const int64_t g = std::min<int64_t>(bm0 + r, M - 1);
+                src[i] = A + g * K + 16 * (pc ^ swz16(r));
+            } else {
+                const int r = 16 * (j - C::A_INS) + rr;
+                const int64_t g = std::min<int64_t>(bn0 + r, N - 1);
+                src[i] = B + g * K + 16 * (pc ^ swz16(r));
+            }
+        }
+    }
+    // DMA of K step ks into LDS buffer `buf`. Past the last step the loop
+    // keeps issuing (ks clamped to nk-1) into a buffer that is never read
+    // again, so every step has the same number of loads in flight and one
+    // vmcnt threshold serves the whole loop.
+    auto issue = [&](int ks, int buf) {
+        int8_t *stage = smem + buf * C::STAGE_BYTES;
+        const int64_t k0 = (int64_t)ks * kDmaBK;
+#pragma unroll
+        for (int i = 0; i < C::INS_PER_WAVE; ++i) {
+            const int j = wid + i * C::NW;
+            dma16(src[i] + k0, stage + 1024 * j);
+        }
+    };
+    // Stage of step kt is in LDS (for every wave) once this wave has at most
+    // the loads of the STAGES-2 later stages in flight and the block has met.
+    auto wait_stage = [&]() {
+        wait_vmcnt<(STAGES - 2) * C::INS_MIN>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    const int wm = wid / WGN, wn = wid % WGN;
+    const int fr = lane & 15, fq = lane >> 4;
+    const int chunk = 16 * (fq ^ swz16(fr));
+    const int a_off = (wm * C::WM + fr) * kDmaBK + chunk;
+    const int b_off = BM * kDmaBK + (wn * C::WN + fr) * kDmaBK + chunk;
+    auto read_frags = [&](int buf, F &f) {
+        const int8_t *st = smem + buf * C::STAGE_BYTES;
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j)
+            f.a[j] = *reinterpret_cast<const v4i *>(st + a_off + j * 16 * kDmaBK);
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i)
+            f.b[i] = *reinterpret_cast<const v4i *>(st + b_off + i * 16 * kDmaBK);
+    };
+
+    v4i acc[C::FN][C::FM];
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    // The MFMA is issued as inline asm with its accumulator tied to an AGPR
+    // operand ("+a"): the builtin's untied form makes the register allocator
+    // rotate 224-256 live accumulators through copies at this register
+    // pressure. The compiler does not see these as MFMAs, so the wait states
+    // it would insert after the AGPR zero-fill and before the epilogue reads
+    // the accumulators are written out explicitly (s_nop below).
+    auto mfma_rows = [&](const F &f, int i0, int i1) {
+#pragma unroll
+        for (int i = i0; i < i1; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FM; ++j)
+                mfma_i8_acc(acc[i][j], f.b[i], f.a[j]);
+    };
+
+    // One K step with fragments `cur` (step kt) in registers: the first half
+    // of its MFMAs, then, while they run, the wait + barrier for step kt+1,
+    // the DMA of step kt+STAGES into the buffer `cur` came from and the
+    // fragment reads of step kt+1 into `nxt`; then the second half.
+    // In the second half each MFMA is followed by one memory operation, in
+    // the order they are needed: the FM activation and FN weight fragment
+    // reads of step kt+1, then the DMA issues of step kt+STAGES.
+    constexpr int H0 = C::FN / 2;
+    constexpr int NMEM = C::FM + C::FN + C::INS_PER_WAVE;
+    constexpr int NMF = (C::FN - H0) * C::FM;
+    constexpr int NSLOT = NMF > NMEM ? NMF : NMEM;
+    auto step = [&](int kt, F &cur, F &nxt) {
+        mfma_rows(cur, 0, H0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // cur fully read out of LDS
+        wait_stage();
+        const int8_t *rd = smem + ((kt + 1) % STAGES) * C::STAGE_BYTES;
+        int8_t *wr = smem + (kt % STAGES) * C::STAGE_BYTES;
+        const int64_t k0 = (int64_t)std::min(kt + STAGES, nk - 1) * kDmaBK;
+#pragma unroll
+        for (int t = 0; t < NSLOT; ++t) {
+            if (t < NMF) mfma_i8_acc<true>(acc[H0 + t / C::FM][t % C::FM], cur.b[H0 + t / C::FM],
+                                           cur.a[t % C::FM]);
+            if (t < C::FM) {
+                nxt.a[t] = *reinterpret_cast<const v4i *>(rd + a_off + t * 16 * kDmaBK);
+            } else if (t < C::FM + C::FN) {
+                const int ib = t - C::FM;
+                nxt.b[ib] = *reinterpret_cast<const v4i *>(rd + b_off + ib * 16 * kDmaBK);
+            } else if (t < NMEM) {
+                const int q = t - C::FM - C::FN;
+                dma16(src[q] + k0, wr + 1024 * (wid + q * C::NW));
+            }
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) issue(std::min(s, nk - 1), s);
+    wait_vmcnt<(STAGES - 1) * C::INS_MIN>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    asm volatile("s_nop 4" ::: "memory");  // AGPR writes of the zero-fill -> MFMA srcC
+    F f0, f1;
+    read_frags(0, f0);
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, f0, f1);
+        step(kt + 1, f1, f0);
+    }
+    wait_vmcnt<0>();  // drain the trailing DMA before the block's LDS is released
+    // last MFMA results -> accumulator reads (16-cycle MFMA: >= 18 wait states)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+    // D of block (i, j): lane l, register e = row n 4*(l/16)+e, column m l%16.
+    float4 swv[C::FN], bv[C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i) {
+        const int64_t n = std::min<int64_t>(bn0 + wn * C::WN + i * 16 + 4 * fq, N - 4);
+        swv[i] = float4{0.f, 0.f, 0.f, 0.f};
+        bv[i] = float4{0.f, 0.f, 0.f, 0.f};
+        if (OUT_Y) {
+            swv[i] = *reinterpret_cast<const float4 *>(epi.sw + n);
+            if (epi.bias) bv[i] = *reinterpret_cast<const float4 *>(epi.bias + n);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j) {
+        const int64_t m = bm0 + wm * C::WM + j * 16 + fr;
+        const float sam = OUT_Y ? epi.sa[std::min<int64_t>(m, M - 1)] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) {
+            const int64_t n = bn0 + wn * C::WN + i * 16 + 4 * fq;
+            epi_store4<OUT_Y, OUT_ACC>(epi, m, n, acc[i][j], sam, swv[i], bv[i]);
+        }
+    }
+}
+
 // ------------------------------------------------------------ skinny GEMV
 // M <= 16 (decode). One workgroup per 16 output columns; the WAVES waves of a
 // workgroup split K, each streaming its K range of the 16 weight rows with
@@ -336,6 +640,42 @@ static int launch_tiled(const int8_t *A, const void *B, int64_t M, int64_t N, in
     return check_launch(name);
 }
 
+template <int BM, int BN, int WGM, int WGN, int STAGES>
+static int launch_dma(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
+                      const Epilogue &epi, hipStream_t st, const char *name) {
+    using C = DmaCfg<BM, BN, WGM, WGN, STAGES>;
+    const int64_t tm = ceil_div(M, BM), tn = ceil_div(N, BN);
+    RNN_REQUIRE(tm * tn <= 0x7fffffffLL, "%s: too many tiles", name);
+    const unsigned grid = (unsigned)(tm * tn);
+    if (epi.y && epi.acc_out)
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, true><<<grid, C::NT, 0, st>>>(
+            A, B, M, N, K, (int)tm, (int)tn, epi);
+    else if (epi.y)
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, false><<<grid, C::NT, 0, st>>>(
+            A, B, M, N, K, (int)tm, (int)tn, epi);
+    else
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, false, true><<<grid, C::NT, 0, st>>>(
+            A, B, M, N, K, (int)tm, (int)tn, epi);
+    return check_launch(name);
+}
+
+// The LDS-DMA kernel's preconditions: K a positive multiple of 128, 16-byte
+// aligned operands, N % 4 == 0 and 16-byte aligned epilogue vectors.
+static bool dma_ok(const int8_t *A, const int8_t *B, int64_t N, int64_t K, const Epilogue &epi) {
+    auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    return K > 0 && K % (2 * kDmaBK) == 0 && N % 4 == 0 && al(A) && al(B) && al(epi.y) &&
+           al(epi.acc_out) && al(epi.sw) && al(epi.bias) && al(epi.colsum);
+}
+
+// Block-tile choice for the LDS-DMA kernel: 256x224 (one 256-thread block
+// per CU, 128x112 accumulators per wave; 2048x14336 is 512 tiles = two full
+// rounds on 256 CUs) for M > 128, else 128x128 (64x64 per wave).
+static int launch_dma_auto(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
+                           const Epilogue &epi, hipStream_t st, const char *name) {
+    if (M <= 128) return launch_dma<128, 128, 2, 2, 4>(A, B, M, N, K, epi, st, name);
+    return launch_dma<256, 224, 2, 2, 4>(A, B, M, N, K, epi, st, name);
+}
+
 static int launch_gemv(const int8_t *A, const int8_t *W, int64_t M, int64_t N, int64_t K,
                        const Epilogue &epi, hipStream_t st, const char *name) {
     gemv_kernel<4, 4><<<(unsigned)ceil_div(N, 16), 256, 0, st>>>(A, W, M, N, K, epi);
@@ -365,11 +705,22 @@ extern "C" int rnn_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *
                          name, (long long)k);
     Epilogue epi{sa, sw, bias, y, acc_out, nullptr, m, n, (flags & RNN_FLAG_RELU) ? 1 : 0};
     const unsigned algo = flags & RNN_ALGO_MASK;
-    const bool gemv = algo == RNN_ALGO_GEMV || (algo == RNN_ALGO_AUTO && m <= 16);
+    RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_TILED || algo == RNN_ALGO_GEMV ||
+                    algo == RNN_ALGO_TILED_DMA,
+                "%s: unknown algo 0x%x", name, algo);
     if (algo == RNN_ALGO_GEMV)
         RNN_REQUIRE(m <= 16, "%s: RNN_ALGO_GEMV needs m <= 16", name);
+    const bool dma = dma_ok(aq, wq, n, k, epi);
+    if (algo == RNN_ALGO_TILED_DMA && !dma)
+        return set_error(RNN_ERR_UNSUPPORTED,
+                         "%s: RNN_ALGO_TILED_DMA needs k %% 128 == 0, n %% 4 == 0 and 16-byte "
+                         "aligned buffers (k=%lld, n=%lld)",
+                         name, (long long)k, (long long)n);
     hipStream_t st = as_stream(stream);
-    if (gemv) return launch_gemv(aq, wq, m, n, k, epi, st, name);
+    if (algo == RNN_ALGO_GEMV || (algo == RNN_ALGO_AUTO && m <= 16))
+        return launch_gemv(aq, wq, m, n, k, epi, st, name);
+    if (algo == RNN_ALGO_TILED_DMA || (algo == RNN_ALGO_AUTO && dma))
+        return launch_dma_auto(aq, wq, m, n, k, epi, st, name);
     return launch_tiled<128, 128, 64, 64, false>(aq, wq, m, n, k, epi, st, name);
 }
 

@@ -25,6 +25,7 @@ FLAG_RELU = 0x1
 ALGO_AUTO = 0x00
 ALGO_TILED = 0x10
 ALGO_GEMV = 0x20
+ALGO_TILED_DMA = 0x30
 
 TERNARY_ROWS = 0
 TERNARY_ABSMEAN = 1

@@ -162,6 +162,35 @@ def test_w8a8_small_shapes(dev, hip, m, k, n, algo):
         assert_f32_equal(y, ye)
 
 
+@pytest.mark.parametrize("m,k,n", [(17, 128, 4), (64, 256, 128), (129, 128, 228), (200, 1024, 300),
+                                   (256, 256, 224), (300, 384, 1000), (513, 640, 452),
+                                   (1000, 128, 14336 // 16)])
+def test_w8a8_lds_dma_kernel(dev, hip, m, k, n):
+    """The LDS-DMA pipelined kernel (forced), on both tile variants (128x128
+    for m <= 128, 256x224 above) with ragged M/N edges, against the oracle: int32
+    bit-exact, fp32 bit-exact, for y only / acc only / both, bias + ReLU."""
+    aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=3 * m + k + n, outliers=0.01)
+    ye, acce = O.w8a8_linear(aq, sa, wq, sw, bias, True)
+    d = [to_dev(a, dev) for a in (aq, sa, wq, sw, bias)]
+    y, acc = hip.w8a8_linear(*d, relu=True, algo=hip.ALGO_TILED_DMA, want_acc=True)
+    assert np.array_equal(host(acc), acce)
+    assert_f32_equal(host(y), ye)
+    _, acc2 = hip.w8a8_linear(*d, relu=True, algo=hip.ALGO_TILED_DMA, want_y=False, want_acc=True)
+    assert np.array_equal(host(acc2), acce)
+    y3, _ = hip.w8a8_linear(d[0], d[1], d[2], d[3], None, relu=False, algo=hip.ALGO_TILED_DMA)
+    assert_f32_equal(host(y3), O.w8a8_linear(aq, sa, wq, sw)[0])
+
+
+def test_w8a8_lds_dma_rejects_unsupported(dev, hip):
+    aq, sa, wq, sw, _ = w8a8_case(32, 192, 64, seed=5)   # k % 128 != 0
+    d = [to_dev(a, dev) for a in (aq, sa, wq, sw)]
+    with pytest.raises(hip.RnnError) as e:
+        hip.w8a8_linear(*d, algo=hip.ALGO_TILED_DMA)
+    assert e.value.status == hip.RNN_ERR_UNSUPPORTED
+    y, _ = hip.w8a8_linear(*d)                             # AUTO falls back to the staged kernel
+    assert_f32_equal(host(y), O.w8a8_linear(aq, sa, wq, sw)[0])
+
+
 @pytest.mark.parametrize("m,k,n", W.GEMV_SHAPES)
 def test_w8a8_decode_gemv_full_size(dev, hip, m, k, n):
     # BASELINE decode config: 1% activation outliers x20
