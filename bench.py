@@ -89,6 +89,35 @@ def bench_prefill(H, W, dev, steps, warmup):
 
 
 # ---------------------------------------------------------------- GEMV
+def graph_timed(launch, n_launch, replays=5):
+    """Average ms per launch of `launch(i)` for i in range(n_launch), captured
+    once into a HIP graph and replayed (events on the replay stream), so the
+    per-call host overhead of the Python binding is not part of the figure."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(min(n_launch, 8)):      # warm up outside the capture
+            launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_launch):
+            launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(replays):
+        g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / (replays * n_launch)
+
+
 def bench_gemv(H, W, dev, steps):
     import torch
     out = {}
@@ -106,20 +135,15 @@ def bench_gemv(H, W, dev, steps):
         x = torch.where(mask, x * 20.0, x)
         aq, sa = H.quant_rows_i8(x)
         y = torch.empty((m, n), dtype=torch.float32, device=dev)
-        it = [0]
-
-        def fn():
-            i = it[0] % copies
-            it[0] += 1
-            H.w8a8_linear(aq, sa, ws[i], sws[i], y=y)
-
-        iters = max(steps, 200)
-        ms = timed(fn, iters, 20)
+        n_launch = copies * max(1, -(-max(steps, 100) // copies))
+        ms = graph_timed(lambda i: H.w8a8_linear(aq, sa, ws[i % copies], sws[i % copies], y=y),
+                         n_launch)
         nbytes = k * n + 4 * n + m * k + 4 * m + 4 * m * n
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"m{m}_k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
-                                  "weight_copies": copies}
+                                  "weight_copies": copies, "launches_timed": n_launch,
+                                  "timing": "HIP graph replay, events / launches"}
         del ws, sws
         torch.cuda.empty_cache()
     return out

@@ -66,14 +66,13 @@ __device__ __forceinline__ v4i ternary_word_to_i8x16(uint32_t w) {
 // ------------------------------------------------------------ tiled GEMM
 // Block tile BM x BN, K step 64 (one MFMA K), (BM/WM) x (BN/WN) waves, each
 // wave a WM x WN tile of 16x16 MFMA blocks. Operand tiles live in LDS as
-// [rows][64 bytes] with the 16-byte chunk index XOR-swizzled by
-// ((r>>1) ^ (r>>3)) & 3, which keeps the ds_read_b128 fragment loads (16 rows
-// x one chunk per quarter-wave) and the row-contiguous tile stores free of
-// bank conflicts. Global tiles are prefetched into registers one K step
+// [rows][64 bytes] with the 16-byte chunk index XOR-swizzled by (r>>1) & 3,
+// which keeps the ds_read_b128 fragment loads (16 rows x one chunk per
+// quarter-wave) free of bank conflicts on gfx950. Global tiles are prefetched into registers one K step
 // ahead (double-buffered LDS).
 constexpr int kBK = 64;
 
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
 
 template <int BM, int BN, int WM, int WN, bool TERNARY>
 struct TileGemm {
@@ -234,7 +233,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_tiled_kernel(
 //
 //  * Block tile BM x BN, WGM x WGN waves, each wave a (BM/WGM) x (BN/WGN)
 //    register tile of 16x16x64 MFMA blocks whose int32 accumulators live in
-//    the AGPR file (128x128 per wave = all 256 AGPRs; one wave per SIMD).
+//    the AGPR file.
 //  * Operands go global -> LDS with global_load_lds_dwordx4 (no VGPR
 //    staging, no ds_write): every wave instruction moves 1 KiB = 16 tile rows
 //    x 64 B, lane l landing at byte 16*l. The 16-byte chunk order inside a
@@ -252,8 +251,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_tiled_kernel(
 constexpr int kDmaBK = 64;
 
 // Swizzle of the 16-byte chunk index by tile row (depends on row & 15 only,
-// so a lane's swizzle is the same for every fragment it reads).
-__device__ __forceinline__ int swz16(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+// so a lane's swizzle is the same for every fragment it reads). With 64-byte
+// rows, chunk ^ ((row >> 1) & 3) is the pattern that measured conflict-free
+// for ds_read_b128 on gfx950's 256 B/clk LDS (231 B/clk/CU of fragment reads;
+// adding a (row >> 3) term halves that).
+__device__ __forceinline__ int swz16(int r) { return (r >> 1) & 3; }
 
 // acc += a . b on v_mfma_i32_16x16x64_i8 with the accumulator tied to an
 // AGPR quad. (Device pass only: the host pass parses but never emits kernel
@@ -370,7 +372,8 @@ struct Frags {
 };
 
 template <int BM, int BN, int WGM, int WGN, int STAGES, bool OUT_Y, bool OUT_ACC>
-__global__ __launch_bounds__(WGM *WGN * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(WGM *WGN * 64)
+__attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4)))
 void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
                      int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
     using C = DmaCfg<BM, BN, WGM, WGN, STAGES>;
@@ -667,18 +670,26 @@ static bool dma_ok(const int8_t *A, const int8_t *B, int64_t N, int64_t K, const
            al(epi.acc_out) && al(epi.sw) && al(epi.bias) && al(epi.colsum);
 }
 
-// Block-tile choice for the LDS-DMA kernel: 256x224 (one 256-thread block
-// per CU, 128x112 accumulators per wave; 2048x14336 is 512 tiles = two full
-// rounds on 256 CUs) for M > 128, else 128x128 (64x64 per wave).
+// Block-tile choice for the LDS-DMA kernel: for M > 128, 256x224 tiles with
+// 8 waves (2 per SIMD, 64x112 int32 accumulators each, so one wave's barrier
+// and DMA waits overlap the other's MFMAs; 2048x14336 is 512 tiles = two full
+// rounds on 256 CUs, one block per CU for the 128 KiB LDS ring), else 128x128
+// tiles with 4 waves of 64x64.
 static int launch_dma_auto(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
                            const Epilogue &epi, hipStream_t st, const char *name) {
     if (M <= 128) return launch_dma<128, 128, 2, 2, 4>(A, B, M, N, K, epi, st, name);
-    return launch_dma<256, 224, 2, 2, 4>(A, B, M, N, K, epi, st, name);
+    return launch_dma<256, 224, 4, 2, 4>(A, B, M, N, K, epi, st, name);
 }
 
+// Decode GEMV dispatch: one-shot workgroups of 4 waves per 16 weight rows,
+// each wave keeping 16 16-byte loads in flight per lane (the whole 4096-wide
+// row block of 64 KiB is requested at once). A persistent variant that walks
+// row blocks with one block of prefetch measured slower (per-item memory
+// latency exposed, uneven rounds), so the hardware dispatcher does the
+// balancing.
 static int launch_gemv(const int8_t *A, const int8_t *W, int64_t M, int64_t N, int64_t K,
                        const Epilogue &epi, hipStream_t st, const char *name) {
-    gemv_kernel<4, 4><<<(unsigned)ceil_div(N, 16), 256, 0, st>>>(A, W, M, N, K, epi);
+    gemv_kernel<4, 16><<<(unsigned)ceil_div(N, 16), 256, 0, st>>>(A, W, M, N, K, epi);
     return check_launch(name);
 }
 

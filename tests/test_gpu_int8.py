@@ -167,7 +167,7 @@ def test_w8a8_small_shapes(dev, hip, m, k, n, algo):
                                    (1000, 128, 14336 // 16)])
 def test_w8a8_lds_dma_kernel(dev, hip, m, k, n):
     """The LDS-DMA pipelined kernel (forced), on both tile variants (128x128
-    for m <= 128, 256x224 above) with ragged M/N edges, against the oracle: int32
+    with 4 waves for m <= 128, 256x224 with 8 waves above) with ragged M/N edges, against the oracle: int32
     bit-exact, fp32 bit-exact, for y only / acc only / both, bias + ReLU."""
     aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=3 * m + k + n, outliers=0.01)
     ye, acce = O.w8a8_linear(aq, sa, wq, sw, bias, True)

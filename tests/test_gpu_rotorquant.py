@@ -22,7 +22,8 @@ def test_rotation_matrices_parity(dev, hip):
 
 @pytest.mark.parametrize("rows,dim,bits", [(1, 12, 4), (2, 10, 3), (5, 6, 4), (333, 128, 4),
                                            (64, 129, 8), (7, 1, 2), (50, 2, 5), (3, 130, 4),
-                                           (4100, 128, 4), (9, 2688, 4)])
+                                           (4100, 128, 4), (9, 2688, 4), (37, 64, 4),
+                                           (19, 256, 4), (8, 256, 8), (1, 64, 2)])
 def test_rotorquant_parity(dev, hip, rows, dim, bits):
     x = W.activations(rows, dim, seed=rows + dim)
     x[0, : min(dim, 3)] = 0.0              # an all-zero group (skipped, src/quant.rs:189-191)
@@ -41,6 +42,61 @@ def test_rotorquant_parity(dev, hip, rows, dim, bits):
     # reconstruction from codes
     yd = hip.rotorquant_dequantize(codes, scales, dim, to_dev(rot, dev))
     assert_f32_equal(host(yd), O.rotorquant_dequantize(ce, se, dim, rot))
+
+
+@pytest.mark.parametrize("dim", [128, 64])
+def test_rotorquant_unaligned_generic_path(dev, hip, dim):
+    """A tensor view that is only 4-byte aligned takes the generic per-group
+    streaming kernel instead of the 16-byte tiled one; same results."""
+    import torch
+    rows = 45
+    x = W.activations(rows, dim, seed=dim + 5)
+    rot = W.rotors((dim + 2) // 3, seed=dim + 6)
+    buf = to_dev(np.concatenate([np.zeros(1, np.float32), x.ravel()]), dev)
+    xv = buf[1:].view(rows, dim)
+    y = torch.empty(rows * dim + 1, dtype=torch.float32, device=dev)[1:].view(rows, dim)
+    hip.rotorquant_quantize(xv, to_dev(rot, dev), 4, y=y)
+    ye, _, _ = O.rotorquant_quantize(x, rot, 4)
+    assert_f32_equal(host(y), ye)
+
+
+def half_integer_cases(n_rows, bits, seed):
+    """Rows of 3-groups whose quotient rv/scale sits exactly on, or within two
+    ulps of, a half-integer k + 0.5 (identity rotors make rv = x): the cases
+    where round-half-away-from-zero of the IEEE quotient is decided by the
+    last bit. Scales are both exact (1.0) and inexact (random)."""
+    g = W.rng(seed)
+    qmax = np.float32(2 ** (bits - 1) - 1)
+    groups = []
+    for i in range(n_rows * 43):
+        s = np.float32(1.0) if i % 4 == 0 else np.float32(g.uniform(1e-3, 10.0))
+        m = np.float32(qmax * s)                       # max |rv|: scale = m / qmax ~= s
+        scale = np.float32(m / qmax)
+        k = int(g.integers(-int(qmax), int(qmax)))
+        h = np.float32((np.float32(k) + np.float32(0.5)) * scale)
+        for _ in range(int(g.integers(-2, 3))):        # walk 0..2 ulps either way
+            h = np.nextafter(h, np.float32(np.inf) if k >= 0 else np.float32(-np.inf))
+        if abs(h) > m:
+            h = np.float32(np.sign(h) * m)
+        c = np.float32(g.uniform(-1, 1) * m)
+        groups.append((m if i % 2 else -m, h, c))
+    x = np.array(groups, np.float32).reshape(n_rows, 43 * 3)[:, :128]
+    return np.ascontiguousarray(x)
+
+
+@pytest.mark.parametrize("bits", [4, 8, 3])
+def test_rotorquant_half_integer_quotients(dev, hip, bits):
+    """The kernel rounds rv/scale through a reciprocal multiply and falls back
+    to the exact division near half-integers; codes, scales and
+    reconstructions must still equal the oracle's (true division + roundf)."""
+    x = half_integer_cases(512, bits, seed=bits)
+    rot = np.tile(np.array([1.0, 0.0, 0.0, 0.0], np.float32), (43, 1))
+    y, codes, scales = hip.rotorquant_quantize(to_dev(x, dev), to_dev(rot, dev), bits,
+                                               want_codes=True)
+    ye, ce, se = O.rotorquant_quantize(x, rot, bits)
+    assert np.array_equal(host(scales), se)
+    assert np.array_equal(host(codes), ce)
+    assert_f32_equal(host(y), ye)
 
 
 def test_rotorquant_reference_bounded_error(dev, hip):
