@@ -138,7 +138,10 @@ int rnn_ternary_linear_forward(const float *x, int64_t batch, int64_t in_f,
 
 /* Ternary GEMM on int8 MFMA (BASELINE ternary config): t[n,k] unpacked from
  * the 2-bit codes inside the kernel, acc = sum_k aq[m,k]*t[n,k], epilogue as
- * rnn_w8a8_linear with sw[n]. k must be a multiple of 16 (rows word aligned). */
+ * rnn_w8a8_linear with sw[n]. k must be a multiple of 16 (rows word aligned).
+ * flags: RNN_FLAG_RELU and an algo (AUTO: the LDS-DMA kernel when k % 128 == 0,
+ * n % 4 == 0 and buffers are 16-byte aligned, else TILED; TILED or TILED_DMA
+ * force one). */
 int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_t *packed,
                      const float *sw, const float *bias, int64_t m, int64_t k,
                      int64_t n, unsigned flags, float *y, int32_t *acc_out,

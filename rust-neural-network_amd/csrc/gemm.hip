@@ -289,13 +289,17 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES>
+// TER: B is 2-bit ternary codes (16 per u32, the TernaryTensor::packed layout),
+// 16 bytes per row per 64-k step instead of 64.
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool TER = false>
 struct DmaCfg {
     static constexpr int NW = WGM * WGN;
     static constexpr int NT = NW * 64;
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int FM = WM / 16, FN = WN / 16;
-    static constexpr int A_INS = BM / 16, B_INS = BN / 16;  // 1 KiB wave loads per stage
+    static constexpr int B_ROW = TER ? 16 : kDmaBK;  // bytes of a B row per K step
+    static constexpr int A_INS = BM / 16;            // 1 KiB wave loads per stage
+    static constexpr int B_INS = BN * B_ROW / 1024;
     static constexpr int INS = A_INS + B_INS;
     // Every wave issues INS_PER_WAVE loads per stage; when INS does not split
     // evenly the extra slots re-load a valid row into padding at the end of
@@ -309,7 +313,30 @@ struct DmaCfg {
     static_assert(INS_MIN >= 1 && STAGES >= 2, "pipeline shape");
     static_assert((STAGES - 2) * INS_MIN < 64, "vmcnt range");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(!TER || (BN % 64 == 0 && NT >= 256), "ternary B loads 64 rows per wave load");
 };
+
+// Ternary decode table: byte x holding four 2-bit codes (code i at bits
+// 2i..2i+1; 00 -> 0, 01 -> +1, 10 -> -1, 11 -> 0, src/ternary.rs:9-14, :63-75)
+// -> the four int8 values, byte i = code i. A u32 of 16 codes decodes with four
+// lookups into the 16 int8 of an MFMA operand fragment.
+__device__ __forceinline__ uint32_t ternary_lut_entry(uint32_t x) {
+    uint32_t r = 0;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t c = (x >> (2 * i)) & 3u;
+        r |= (c == 1u ? 0x01u : (c == 2u ? 0xffu : 0u)) << (8 * i);
+    }
+    return r;
+}
+
+__device__ __forceinline__ v4i ternary_lut_decode(const uint32_t *lut, uint32_t w) {
+    v4i r;
+    r.x = (int)lut[w & 0xffu];
+    r.y = (int)lut[(w >> 8) & 0xffu];
+    r.z = (int)lut[(w >> 16) & 0xffu];
+    r.w = (int)lut[w >> 24];
+    return r;
+}
 
 // Tile coordinates of block b. When the tile count splits evenly over the 8
 // XCDs, XCD x (blocks b with b % 8 == x) gets the contiguous tile range
@@ -364,21 +391,28 @@ __device__ __forceinline__ void epi_store4(const Epilogue &epi, int64_t m, int64
 }
 
 // Fragments of one K step held in registers: FM activation blocks, FN weight
-// blocks (16 rows x 64 B each, one 16-byte chunk per lane).
+// blocks (16 rows x 64 B each, one 16-byte chunk per lane); for ternary B the
+// lane's 32-bit word of 16 codes (w) is read first and decoded into b.
 template <int FM, int FN>
 struct Frags {
     v4i a[FM];
     v4i b[FN];
+    uint32_t w[FN];
 };
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, bool OUT_Y, bool OUT_ACC>
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool OUT_Y, bool OUT_ACC, bool TER>
 __global__ __launch_bounds__(WGM *WGN * 64)
 __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4)))
 void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
                      int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
-    using C = DmaCfg<BM, BN, WGM, WGN, STAGES>;
+    using C = DmaCfg<BM, BN, WGM, WGN, STAGES, TER>;
     using F = Frags<C::FM, C::FN>;
     __shared__ __attribute__((aligned(1024))) int8_t smem[C::LDS_BYTES];
+    __shared__ uint32_t lut[TER ? 256 : 1];
+    if (TER) {
+        for (int t = threadIdx.x; t < 256; t += C::NT) lut[t] = ternary_lut_entry((uint32_t)t);
+        __syncthreads();
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -387,19 +421,27 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
     const int64_t bm0 = (int64_t)tm * BM, bn0 = (int64_t)tn * BN;
     const int nk = (int)(K / kDmaBK);  // even, >= 2 (host-checked)
 
-    // Global sources of this wave's DMA loads at k = 0. Instruction j of a
-    // stage fills LDS bytes [1024 j, 1024 j + 1024): A-tile rows for
-    // j < A_INS, then B-tile rows (a stage is [A tile | B tile]).
+    // Global sources of this wave's DMA loads at k = 0, and how far each
+    // advances per K step (64 bytes, or 16 for packed ternary rows).
+    // Instruction j of a stage fills LDS bytes [1024 j, 1024 j + 1024):
+    // A-tile rows for j < A_INS, then B-tile rows (a stage is [A | B]).
     const int8_t *src[C::INS_PER_WAVE];
+    int kstep[C::INS_PER_WAVE];
     {
         const int rr = lane >> 2, pc = lane & 3;
 #pragma unroll
         for (int i = 0; i < C::INS_PER_WAVE; ++i) {
             const int j = std::min(wid + i * C::NW, C::INS - 1);  // padding slots: last row block
+            kstep[i] = kDmaBK;
             if (j < C::A_INS) {
                 const int r = 16 * j + rr;
                 const int64_t g = std::min<int64_t>(bm0 + r, M - 1);
                 src[i] = A + g * K + 16 * (pc ^ swz16(r));
+            } else if (TER) {  // 64 packed rows x 16 bytes, lane = row
+                const int r = 64 * (j - C::A_INS) + lane;
+                const int64_t g = std::min<int64_t>(bn0 + r, N - 1);
+                src[i] = B + g * (K / 4);
+                kstep[i] = C::B_ROW;
             } else {
                 const int r = 16 * (j - C::A_INS) + rr;
                 const int64_t g = std::min<int64_t>(bn0 + r, N - 1);
@@ -413,11 +455,10 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
     // vmcnt threshold serves the whole loop.
     auto issue = [&](int ks, int buf) {
         int8_t *stage = smem + buf * C::STAGE_BYTES;
-        const int64_t k0 = (int64_t)ks * kDmaBK;
 #pragma unroll
         for (int i = 0; i < C::INS_PER_WAVE; ++i) {
             const int j = wid + i * C::NW;
-            dma16(src[i] + k0, stage + 1024 * j);
+            dma16(src[i] + (int64_t)ks * kstep[i], stage + 1024 * j);
         }
     };
     // Stage of step kt is in LDS (for every wave) once this wave has at most
@@ -432,15 +473,27 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
     const int fr = lane & 15, fq = lane >> 4;
     const int chunk = 16 * (fq ^ swz16(fr));
     const int a_off = (wm * C::WM + fr) * kDmaBK + chunk;
-    const int b_off = BM * kDmaBK + (wn * C::WN + fr) * kDmaBK + chunk;
+    // B fragment i: 16 rows from b_off + i*16*B_ROW; packed ternary rows hold
+    // 4 words (one 16-code word per lane: row fr, word fq, conflict-free).
+    const int b_off = TER ? BM * kDmaBK + (wn * C::WN + fr) * C::B_ROW + 4 * fq
+                          : BM * kDmaBK + (wn * C::WN + fr) * kDmaBK + chunk;
+    auto read_b = [&](const int8_t *st, int i, F &f) {
+        if (TER)
+            f.w[i] = *reinterpret_cast<const uint32_t *>(st + b_off + i * 16 * C::B_ROW);
+        else
+            f.b[i] = *reinterpret_cast<const v4i *>(st + b_off + i * 16 * C::B_ROW);
+    };
     auto read_frags = [&](int buf, F &f) {
         const int8_t *st = smem + buf * C::STAGE_BYTES;
 #pragma unroll
         for (int j = 0; j < C::FM; ++j)
             f.a[j] = *reinterpret_cast<const v4i *>(st + a_off + j * 16 * kDmaBK);
 #pragma unroll
-        for (int i = 0; i < C::FN; ++i)
-            f.b[i] = *reinterpret_cast<const v4i *>(st + b_off + i * 16 * kDmaBK);
+        for (int i = 0; i < C::FN; ++i) read_b(st, i, f);
+        if (TER) {
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i) f.b[i] = ternary_lut_decode(lut, f.w[i]);
+        }
     };
 
     v4i acc[C::FN][C::FM];
@@ -467,10 +520,13 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
     // the DMA of step kt+STAGES into the buffer `cur` came from and the
     // fragment reads of step kt+1 into `nxt`; then the second half.
     // In the second half each MFMA is followed by one memory operation, in
-    // the order they are needed: the FM activation and FN weight fragment
-    // reads of step kt+1, then the DMA issues of step kt+STAGES.
+    // the order they are needed: for ternary B first the FN code words, then
+    // the FM activation fragment reads of step kt+1, the FN weight fragment
+    // reads (ternary: the LUT decodes of the words), then the DMA issues of
+    // step kt+STAGES.
     constexpr int H0 = C::FN / 2;
-    constexpr int NMEM = C::FM + C::FN + C::INS_PER_WAVE;
+    constexpr int W0 = TER ? C::FN : 0;  // leading slots for ternary code words
+    constexpr int NMEM = W0 + C::FM + C::FN + C::INS_PER_WAVE;
     constexpr int NMF = (C::FN - H0) * C::FM;
     constexpr int NSLOT = NMF > NMEM ? NMF : NMEM;
     auto step = [&](int kt, F &cur, F &nxt) {
@@ -479,19 +535,25 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
         wait_stage();
         const int8_t *rd = smem + ((kt + 1) % STAGES) * C::STAGE_BYTES;
         int8_t *wr = smem + (kt % STAGES) * C::STAGE_BYTES;
-        const int64_t k0 = (int64_t)std::min(kt + STAGES, nk - 1) * kDmaBK;
+        const int64_t kn = std::min(kt + STAGES, nk - 1);
 #pragma unroll
         for (int t = 0; t < NSLOT; ++t) {
             if (t < NMF) mfma_i8_acc<true>(acc[H0 + t / C::FM][t % C::FM], cur.b[H0 + t / C::FM],
                                            cur.a[t % C::FM]);
-            if (t < C::FM) {
-                nxt.a[t] = *reinterpret_cast<const v4i *>(rd + a_off + t * 16 * kDmaBK);
-            } else if (t < C::FM + C::FN) {
-                const int ib = t - C::FM;
-                nxt.b[ib] = *reinterpret_cast<const v4i *>(rd + b_off + ib * 16 * kDmaBK);
+            if (t < W0) {
+                read_b(rd, t, nxt);
+            } else if (t < W0 + C::FM) {
+                const int ja = t - W0;
+                nxt.a[ja] = *reinterpret_cast<const v4i *>(rd + a_off + ja * 16 * kDmaBK);
+            } else if (t < W0 + C::FM + C::FN) {
+                const int ib = t - W0 - C::FM;
+                if (TER)
+                    nxt.b[ib] = ternary_lut_decode(lut, nxt.w[ib]);
+                else
+                    read_b(rd, ib, nxt);
             } else if (t < NMEM) {
-                const int q = t - C::FM - C::FN;
-                dma16(src[q] + k0, wr + 1024 * (wid + q * C::NW));
+                const int q = t - W0 - C::FM - C::FN;
+                dma16(src[q] + kn * kstep[q], wr + 1024 * (wid + q * C::NW));
             }
         }
     };
@@ -643,21 +705,21 @@ static int launch_tiled(const int8_t *A, const void *B, int64_t M, int64_t N, in
     return check_launch(name);
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES>
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool TER = false>
 static int launch_dma(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
                       const Epilogue &epi, hipStream_t st, const char *name) {
-    using C = DmaCfg<BM, BN, WGM, WGN, STAGES>;
+    using C = DmaCfg<BM, BN, WGM, WGN, STAGES, TER>;
     const int64_t tm = ceil_div(M, BM), tn = ceil_div(N, BN);
     RNN_REQUIRE(tm * tn <= 0x7fffffffLL, "%s: too many tiles", name);
     const unsigned grid = (unsigned)(tm * tn);
     if (epi.y && epi.acc_out)
-        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, true><<<grid, C::NT, 0, st>>>(
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, true, TER><<<grid, C::NT, 0, st>>>(
             A, B, M, N, K, (int)tm, (int)tn, epi);
     else if (epi.y)
-        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, false><<<grid, C::NT, 0, st>>>(
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, false, TER><<<grid, C::NT, 0, st>>>(
             A, B, M, N, K, (int)tm, (int)tn, epi);
     else
-        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, false, true><<<grid, C::NT, 0, st>>>(
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, false, true, TER><<<grid, C::NT, 0, st>>>(
             A, B, M, N, K, (int)tm, (int)tn, epi);
     return check_launch(name);
 }
@@ -741,7 +803,11 @@ extern "C" int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_
                                 void *stream) {
     const char *name = "rnn_ternary_gemm";
     RNN_REQUIRE(m >= 0 && k >= 0 && n >= 0, "%s: negative size", name);
-    RNN_REQUIRE((flags & ~RNN_FLAG_RELU) == 0, "%s: unknown flags 0x%x", name, flags);
+    RNN_REQUIRE((flags & ~(RNN_FLAG_RELU | RNN_ALGO_MASK)) == 0, "%s: unknown flags 0x%x", name,
+                flags);
+    const unsigned algo = flags & RNN_ALGO_MASK;
+    RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_TILED || algo == RNN_ALGO_TILED_DMA,
+                "%s: algo 0x%x not available for the ternary GEMM", name, algo);
     if (m == 0 || n == 0) return RNN_OK;
     RNN_REQUIRE(y || acc_out, "%s: y and acc_out both null", name);
     RNN_REQUIRE(!y || (sa && sw), "%s: y requires sa and sw", name);
@@ -751,7 +817,20 @@ extern "C" int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_
                          "%s: k must be a multiple of 16 and aq 16-byte aligned (k=%lld)", name,
                          (long long)k);
     Epilogue epi{sa, sw, bias, y, acc_out, nullptr, m, n, (flags & RNN_FLAG_RELU) ? 1 : 0};
-    return launch_tiled<128, 128, 64, 64, true>(aq, packed, m, n, k, epi, as_stream(stream), name);
+    const int8_t *pb = reinterpret_cast<const int8_t *>(packed);
+    // LDS-DMA path: packed rows are K/4 bytes, 16-byte aligned when k % 64 == 0
+    const bool dma = dma_ok(aq, pb, n, k, epi);
+    if (algo == RNN_ALGO_TILED_DMA && !dma)
+        return set_error(RNN_ERR_UNSUPPORTED,
+                         "%s: RNN_ALGO_TILED_DMA needs k %% 128 == 0, n %% 4 == 0 and 16-byte "
+                         "aligned buffers (k=%lld, n=%lld)",
+                         name, (long long)k, (long long)n);
+    hipStream_t st = as_stream(stream);
+    // 128x64 tiles (4 waves of 64x32): a 512x4096 output is 256 tiles, one per
+    // CU; each weight code word is decoded once per 128 activation rows.
+    if (algo == RNN_ALGO_TILED_DMA || (algo == RNN_ALGO_AUTO && dma))
+        return launch_dma<128, 64, 2, 2, 4, true>(aq, pb, m, n, k, epi, st, name);
+    return launch_tiled<128, 128, 64, 64, true>(aq, packed, m, n, k, epi, st, name);
 }
 
 static int64_t igemm_kp(int64_t k) { return (k + 63) / 64 * 64; }

@@ -254,7 +254,7 @@ def ternary_linear_forward(x, packed, scales, out_f, bias=None, stream=None):
 
 
 def ternary_gemm(aq, sa, packed, sw, n, bias=None, relu=False, want_y=True, want_acc=False,
-                 y=None, stream=None):
+                 y=None, stream=None, algo=ALGO_AUTO):
     import torch
     _dev(aq, torch.int8, "aq"), _dev(packed, torch.int32, "packed")
     _dev(sa, torch.float32, "sa"), _dev(sw, torch.float32, "sw"), _dev(bias, torch.float32, "bias")
@@ -263,7 +263,7 @@ def ternary_gemm(aq, sa, packed, sw, n, bias=None, relu=False, want_y=True, want
         y = _empty((m, n), torch.float32, aq)
     acc = _empty((m, n), torch.int32, aq) if want_acc else None
     _check(load().rnn_ternary_gemm(_ptr(aq), _ptr(sa), _ptr(packed), _ptr(sw), _ptr(bias), m, k,
-                                   n, FLAG_RELU if relu else 0, _ptr(y), _ptr(acc),
+                                   n, (FLAG_RELU if relu else 0) | algo, _ptr(y), _ptr(acc),
                                    _stream(stream)))
     return y, acc
 

@@ -94,6 +94,27 @@ def test_ternary_gemm_parity(dev, hip, m, k, n):
         assert_f32_equal(host(y), ye)
 
 
+@pytest.mark.parametrize("m,k,n", [(128, 128, 64), (200, 4096, 300), (17, 256, 4), (512, 1024, 452),
+                                   (300, 384, 1000)])
+@pytest.mark.parametrize("algo", ["tiled", "dma"])
+def test_ternary_gemm_forced_kernels(dev, hip, m, k, n, algo):
+    """Both ternary kernels, forced: the register-staged 128x128 tiles and the
+    LDS-DMA 128x64 tiles whose 2-bit words are decoded through an LDS table,
+    with ragged M/N edges; int32 and fp32 bit-exact."""
+    t, p = rand_ternary(n, k, seed=3 * m + n, with_code3=True)
+    aq = W.rng(m + 5).integers(-128, 128, (m, k)).astype(np.int8)
+    sa = W.rng(m + 6).random(m).astype(np.float32)
+    sw = W.rng(n).random(n).astype(np.float32)
+    bias = W.rng(3).standard_normal(n).astype(np.float32)
+    a = hip.ALGO_TILED if algo == "tiled" else hip.ALGO_TILED_DMA
+    y, acc = hip.ternary_gemm(to_dev(aq, dev), to_dev(sa, dev), to_dev(p.view(np.int32), dev),
+                              to_dev(sw, dev), n, to_dev(bias, dev), relu=True, want_acc=True,
+                              algo=a)
+    ye, acce = O.ternary_gemm_i8(aq, sa, p, sw, n, bias, True)
+    assert np.array_equal(host(acc), acce)
+    assert_f32_equal(host(y), ye)
+
+
 def test_ternary_gemm_full_config_sampled(dev, hip):
     """BASELINE ternary config (512 x 4096 x 4096, absmean weights, per-row int8
     activations): 32 sampled rows against the oracle, all rows via the
