@@ -301,17 +301,16 @@ struct DmaCfg {
     static constexpr int A_INS = BM / 16;            // 1 KiB wave loads per stage
     static constexpr int B_INS = BN * B_ROW / 1024;
     static constexpr int INS = A_INS + B_INS;
-    // Every wave issues INS_PER_WAVE loads per stage; when INS does not split
-    // evenly the extra slots re-load a valid row into padding at the end of
-    // the stage, so the load count (and vmcnt threshold) is the same for all.
+    // Wave w issues the stage's loads j = w, w + NW, ... < INS: INS_HI of them
+    // for w < INS % NW, else INS_LO (the two vmcnt thresholds of the loop).
     static constexpr int INS_PER_WAVE = (INS + NW - 1) / NW;
-    static constexpr int INS_MIN = INS_PER_WAVE;
-    static constexpr int STAGE_BYTES = INS_PER_WAVE * NW * 1024;
+    static constexpr int INS_HI = INS_PER_WAVE, INS_LO = INS / NW;
+    static constexpr int STAGE_BYTES = INS * 1024;
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
     static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile must be a multiple of 16");
     static_assert(BM % WGM == 0 && BN % WGN == 0, "waves must split the tile");
-    static_assert(INS_MIN >= 1 && STAGES >= 2, "pipeline shape");
-    static_assert((STAGES - 2) * INS_MIN < 64, "vmcnt range");
+    static_assert(INS_LO >= 1 && STAGES >= 2, "pipeline shape");
+    static_assert((STAGES - 1) * INS_HI < 64, "vmcnt range");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(!TER || (BN % 64 == 0 && NT >= 256), "ternary B loads 64 rows per wave load");
 };
@@ -431,7 +430,7 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
         const int rr = lane >> 2, pc = lane & 3;
 #pragma unroll
         for (int i = 0; i < C::INS_PER_WAVE; ++i) {
-            const int j = std::min(wid + i * C::NW, C::INS - 1);  // padding slots: last row block
+            const int j = std::min(wid + i * C::NW, C::INS - 1);  // (clamped: slot unused when >= INS)
             kstep[i] = kDmaBK;
             if (j < C::A_INS) {
                 const int r = 16 * j + rr;
@@ -453,18 +452,25 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
     // keeps issuing (ks clamped to nk-1) into a buffer that is never read
     // again, so every step has the same number of loads in flight and one
     // vmcnt threshold serves the whole loop.
+    const bool hi = C::INS % C::NW == 0 || wid < C::INS % C::NW;  // wave-uniform
     auto issue = [&](int ks, int buf) {
         int8_t *stage = smem + buf * C::STAGE_BYTES;
 #pragma unroll
         for (int i = 0; i < C::INS_PER_WAVE; ++i) {
             const int j = wid + i * C::NW;
-            dma16(src[i] + (int64_t)ks * kstep[i], stage + 1024 * j);
+            if (i < C::INS_LO || hi) dma16(src[i] + (int64_t)ks * kstep[i], stage + 1024 * j);
         }
     };
     // Stage of step kt is in LDS (for every wave) once this wave has at most
     // the loads of the STAGES-2 later stages in flight and the block has met.
+    auto wait_later = [&]() {
+        if (hi)
+            wait_vmcnt<(STAGES - 2) * C::INS_HI>();
+        else
+            wait_vmcnt<(STAGES - 2) * C::INS_LO>();
+    };
     auto wait_stage = [&]() {
-        wait_vmcnt<(STAGES - 2) * C::INS_MIN>();
+        wait_later();
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
@@ -553,14 +559,17 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
                     read_b(rd, ib, nxt);
             } else if (t < NMEM) {
                 const int q = t - W0 - C::FM - C::FN;
-                dma16(src[q] + kn * kstep[q], wr + 1024 * (wid + q * C::NW));
+                if (q < C::INS_LO || hi) dma16(src[q] + kn * kstep[q], wr + 1024 * (wid + q * C::NW));
             }
         }
     };
 
 #pragma unroll
     for (int s = 0; s < STAGES; ++s) issue(std::min(s, nk - 1), s);
-    wait_vmcnt<(STAGES - 1) * C::INS_MIN>();
+    if (hi)  // stage 0 of this wave landed
+        wait_vmcnt<(STAGES - 1) * C::INS_HI>();
+    else
+        wait_vmcnt<(STAGES - 1) * C::INS_LO>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     asm volatile("s_nop 4" ::: "memory");  // AGPR writes of the zero-fill -> MFMA srcC
