@@ -1,0 +1,117 @@
+"""GPU parity against the committed golden vectors (tests/golden/golden_small.npz)
+through the C ABI, with no oracle in the loop: integer outputs and codes bit-exact,
+fp32 outputs within the 1e-5 relative contract (assert_f32_equal demands bit
+equality, which is stricter)."""
+import os
+
+import numpy as np
+import pytest
+
+from test_gpu_int8 import assert_f32_equal, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+NPZ = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden_small.npz")
+
+
+@pytest.fixture(scope="module")
+def G():
+    with np.load(NPZ, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("case", ["igemm_kat", "igemm_lcg"])
+def test_golden_igemm(dev, hip, G, case):
+    a, b = G[f"{case}.a"], G[f"{case}.b"]
+    m, k = a.shape
+    n = b.shape[1]
+    c = hip.igemm(to_dev(a, dev), to_dev(b, dev), m, k, n)
+    assert np.array_equal(host(c), G[f"{case}.c"])
+
+
+def test_golden_quant_rows_and_dequant(dev, hip, G):
+    q, s = hip.quant_rows_i8(to_dev(G["quant_rows.x"], dev))
+    assert np.array_equal(host(q), G["quant_rows.q"])
+    assert np.array_equal(host(s), G["quant_rows.scale"])
+    w = hip.int8_dequantize(q, s)
+    assert_f32_equal(host(w), G["int8_dequant.w"])
+
+
+def test_golden_int8_linear(dev, hip, G):
+    wq, ws = to_dev(G["int8_lin.wq"], dev), to_dev(G["int8_lin.ws"], dev)
+    x, b = to_dev(G["int8_lin.x"], dev), to_dev(G["int8_lin.bias"], dev)
+    assert_f32_equal(host(hip.int8_matmul_f32(wq, ws, x)), G["int8_lin.matmul_y"])
+    assert_f32_equal(host(hip.int8_linear_forward(x, wq, ws, b)), G["int8_lin.forward_y"])
+
+
+@pytest.mark.parametrize("algo", ["AUTO", "TILED", "GEMV", "TILED_DMA"])
+def test_golden_w8a8(dev, hip, G, algo):
+    args = [to_dev(G[f"w8a8.{n}"], dev) for n in ("aq", "sa", "wq", "sw")]
+    a = getattr(hip, f"ALGO_{algo}")
+    y, acc = hip.w8a8_linear(*args, None, False, algo=a, want_acc=True)
+    assert np.array_equal(host(acc), G["w8a8.acc"])
+    assert_f32_equal(host(y), G["w8a8.y"])
+    y, _ = hip.w8a8_linear(*args, to_dev(G["w8a8.bias"], dev), True, algo=a)
+    assert_f32_equal(host(y), G["w8a8.y_bias_relu"])
+
+
+@pytest.mark.parametrize("case", ["ternary_pack_kat", "ternary_pack_large"])
+def test_golden_ternary_pack(dev, hip, G, case):
+    t = G[f"{case}.t"]
+    p = hip.ternary_pack(to_dev(t, dev))
+    assert np.array_equal(host(p).view(np.uint32), G[f"{case}.packed"])
+    assert np.array_equal(host(hip.ternary_unpack(p, t.size)), t)
+
+
+def test_golden_ternary_quantize(dev, hip, G):
+    p, s = hip.ternary_quantize(to_dev(G["ternary_rows.w"], dev), hip.TERNARY_ROWS)
+    assert np.array_equal(host(p).view(np.uint32), G["ternary_rows.packed"])
+    assert np.array_equal(host(s), G["ternary_rows.scale"])
+    w = hip.ternary_dequantize(p, G["ternary_rows.w"].size, s, G["ternary_rows.w"].shape[1])
+    assert_f32_equal(host(w), G["ternary_dequant.w"])
+    p, s = hip.ternary_quantize(to_dev(G["ternary_absmean.w"], dev), hip.TERNARY_ABSMEAN)
+    assert np.array_equal(host(p).view(np.uint32), G["ternary_absmean.packed"])
+    assert np.all(host(s) == G["ternary_absmean.gamma"][0])
+
+
+def test_golden_ternary_linear(dev, hip, G):
+    p = to_dev(G["ternary_rows.packed"].view(np.int32), dev)
+    y = hip.ternary_linear_forward(to_dev(G["ternary_lin.x"], dev), p,
+                                   to_dev(G["ternary_rows.scale"], dev), 6,
+                                   to_dev(G["ternary_lin.bias"], dev))
+    assert_f32_equal(host(y), G["ternary_lin.y"])
+
+
+@pytest.mark.parametrize("algo", ["AUTO", "TILED", "TILED_DMA"])
+def test_golden_ternary_gemm(dev, hip, G, algo):
+    aq, sa = to_dev(G["ternary_gemm.aq"], dev), to_dev(G["ternary_gemm.sa"], dev)
+    p = to_dev(G["ternary_absmean.packed"].view(np.int32), dev)
+    n = 24
+    sw = to_dev(np.full(n, G["ternary_absmean.gamma"][0], np.float32), dev)
+    a = getattr(hip, f"ALGO_{algo}")
+    y, acc = hip.ternary_gemm(aq, sa, p, sw, n, None, False, want_acc=True, algo=a)
+    assert np.array_equal(host(acc), G["ternary_gemm.acc"])
+    assert_f32_equal(host(y), G["ternary_gemm.y"])
+    y, _ = hip.ternary_gemm(aq, sa, p, sw, n, to_dev(G["ternary_gemm.bias"], dev), True, algo=a)
+    assert_f32_equal(host(y), G["ternary_gemm.y_bias_relu"])
+
+
+def test_golden_rotation_matrices(dev, hip, G):
+    m = hip.rotation_matrices(to_dev(G["rotor_mats.rotors"], dev))
+    assert_f32_equal(host(m), G["rotor_mats.m"])
+
+
+@pytest.mark.parametrize("case", ["rq_ref.b4", "rq_d128.b3", "rq_d128.b4", "rq_d128.b8",
+                                  "rq_d10.b3", "rq_d10.b4", "rq_d10.b8"])
+def test_golden_rotorquant(dev, hip, G, case):
+    base, b = case.split(".")
+    bits = int(b[1:])
+    pre = base if base == "rq_ref" else case
+    x, r = to_dev(G[f"{base}.x"], dev), to_dev(G[f"{base}.rotors"], dev)
+    y, codes, scales = hip.rotorquant_quantize(x, r, bits, want_codes=True)
+    assert np.array_equal(host(codes), G[f"{pre}.codes"])
+    assert np.array_equal(host(scales), G[f"{pre}.scales"])
+    assert_f32_equal(host(y), G[f"{pre}.y"])
+    if base != "rq_ref":
+        yd = hip.rotorquant_dequantize(codes, scales, x.shape[-1], r)
+        assert_f32_equal(host(yd), G[f"{pre}.deq"])
