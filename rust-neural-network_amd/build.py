@@ -9,6 +9,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -37,12 +38,32 @@ HIPFLAGS = [
 ]
 
 
+def _scratch_kernels(remarks: str) -> list[str]:
+    """Kernels whose resource-usage remark reports private (scratch) memory."""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            bad.append(f"{name} ({m.group(1)} B/lane)")
+    return bad
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *HIPFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *HIPFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+    # Every kernel here keeps its accumulators and fragments in registers; a
+    # kernel the compiler demoted to scratch memory still computes the right
+    # values but runs one to two orders of magnitude slower, so it is a build
+    # error rather than a silent regression.
+    bad = _scratch_kernels(r.stderr)
+    if bad:
+        raise RuntimeError(f"{src}: kernels use scratch memory: {', '.join(bad)}")
     return obj
 
 

@@ -6,6 +6,8 @@
 // (the reference's u8 x i8 [K,N] contract via a pack step + zero-point
 // correction) and rnn_ternary_gemm (B = 2-bit codes decoded in the tile loader).
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "common.hpp"
 #include "numerics.hpp"
@@ -347,45 +349,92 @@ __device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int &t
     tn = t / tiles_m;
 }
 
-// Epilogue of 4 consecutive columns n..n+3 of row m (a lane's 4 MFMA
-// registers), 16-byte stores. The host guarantees N % 4 == 0 and 16-byte
-// aligned y / acc_out / sw / bias / colsum for this path, so n..n+3 are all in
-// range whenever n is. swv/bv hold sw[n..n+3] and bias[n..n+3].
-template <bool OUT_Y, bool OUT_ACC>
-__device__ __forceinline__ void epi_store4(const Epilogue &epi, int64_t m, int64_t n,
-                                           const v4i &acc, float sam, const float4 &swv,
-                                           const float4 &bv) {
-    if (m >= epi.M || n >= epi.N) return;
-    if (OUT_ACC) {
-        v4i o = acc;
-        if (epi.colsum) {
-            const v4i cs = *reinterpret_cast<const v4i *>(epi.colsum + n);
-            o.x = (int)((uint32_t)o.x + 128u * (uint32_t)cs.x);
-            o.y = (int)((uint32_t)o.y + 128u * (uint32_t)cs.y);
-            o.z = (int)((uint32_t)o.z + 128u * (uint32_t)cs.z);
-            o.w = (int)((uint32_t)o.w + 128u * (uint32_t)cs.w);
+// Epilogue of a wave tile held as FN x FM 16x16 MFMA blocks with the operand
+// roles swapped (D of block (i, j): lane l, register e = column n0 + 16i + e,
+// row m0 + 16j, where m0 = tile row + l%16 and n0 = tile column + 4*(l/16)):
+// a lane stores 4 consecutive columns of one row as one 16-byte float4 / int4.
+// The host guarantees N % 4 == 0 and 16-byte aligned y / acc_out / sw / bias /
+// colsum, so n..n+3 are in range whenever n is.
+//  * Every operand (row and column scales, bias, colsum) is loaded before the
+//    first store: stores count in vmcnt, so a wait for a load issued after
+//    them would drain them too.
+//  * Bias and ReLU are uniform selects and the bounds check exists only for
+//    edge tiles (INTERIOR = false): a branch per store makes the compiler
+//    merge its wait-count state at every join and drain the stores there.
+//  * The arithmetic is the reference's: ((float)acc * sa[m]) * sw[n], then
+//    + bias[n], then max(., 0) (src/int8.rs:159-162).
+template <int FM, int FN, bool OUT_Y, bool OUT_ACC, int G = (FN < 4 ? FN : 4)>
+__device__ __forceinline__ void tile_epilogue(const Epilogue &epi, const v4i (&acc)[FN][FM],
+                                              int64_t m0, int64_t n0) {
+    const bool has_bias = epi.bias != nullptr, relu = epi.relu != 0;
+    float sam[FM];
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+        sam[j] = OUT_Y ? epi.sa[std::min<int64_t>(m0 + 16 * j, epi.M - 1)] : 0.0f;
+    // the wave tile's corner: bounds checks are needed only past the edges
+    const bool interior = m0 - (m0 & 15) + 16 * FM <= epi.M && n0 - (n0 & 15) + 16 * FN <= epi.N;
+
+    // Column blocks in groups of G (the operand registers of a group stay
+    // within a two-waves-per-SIMD budget): operand loads, then the stores.
+#pragma unroll
+    for (int g = 0; g < FN; g += G) {
+        float4 swv[G], bv[G];
+        v4i csv[G];
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const int64_t n = std::min<int64_t>(n0 + 16 * std::min(g + k, FN - 1), epi.N - 4);
+            swv[k] = float4{0.f, 0.f, 0.f, 0.f};
+            bv[k] = float4{0.f, 0.f, 0.f, 0.f};
+            csv[k] = v4i{0, 0, 0, 0};
+            if (OUT_Y) {
+                swv[k] = *reinterpret_cast<const float4 *>(epi.sw + n);
+                if (has_bias) bv[k] = *reinterpret_cast<const float4 *>(epi.bias + n);
+            }
+            if (OUT_ACC && epi.colsum) csv[k] = *reinterpret_cast<const v4i *>(epi.colsum + n);
         }
-        *reinterpret_cast<v4i *>(epi.acc_out + m * epi.N + n) = o;
-    }
-    if (OUT_Y) {
-        float4 v;
-        v.x = (float)acc.x * sam * swv.x;
-        v.y = (float)acc.y * sam * swv.y;
-        v.z = (float)acc.z * sam * swv.z;
-        v.w = (float)acc.w * sam * swv.w;
-        if (epi.bias) {
-            v.x = v.x + bv.x;
-            v.y = v.y + bv.y;
-            v.z = v.z + bv.z;
-            v.w = v.w + bv.w;
+        auto store = [&](int k, int j, bool guard) {
+            const int i = g + k;
+            const int64_t m = m0 + 16 * j, n = n0 + 16 * i;
+            if (guard && (m >= epi.M || n >= epi.N)) return;
+            const v4i &a = acc[i][j];
+            if (OUT_ACC) {
+                v4i o;
+                o.x = (int)((uint32_t)a.x + 128u * (uint32_t)csv[k].x);
+                o.y = (int)((uint32_t)a.y + 128u * (uint32_t)csv[k].y);
+                o.z = (int)((uint32_t)a.z + 128u * (uint32_t)csv[k].z);
+                o.w = (int)((uint32_t)a.w + 128u * (uint32_t)csv[k].w);
+                *reinterpret_cast<v4i *>(epi.acc_out + m * epi.N + n) = o;
+            }
+            if (OUT_Y) {
+                float4 v;
+                v.x = (float)a.x * sam[j] * swv[k].x;
+                v.y = (float)a.y * sam[j] * swv[k].y;
+                v.z = (float)a.z * sam[j] * swv[k].z;
+                v.w = (float)a.w * sam[j] * swv[k].w;
+                v.x = has_bias ? v.x + bv[k].x : v.x;
+                v.y = has_bias ? v.y + bv[k].y : v.y;
+                v.z = has_bias ? v.z + bv[k].z : v.z;
+                v.w = has_bias ? v.w + bv[k].w : v.w;
+                v.x = relu ? fmaxf(v.x, 0.0f) : v.x;
+                v.y = relu ? fmaxf(v.y, 0.0f) : v.y;
+                v.z = relu ? fmaxf(v.z, 0.0f) : v.z;
+                v.w = relu ? fmaxf(v.w, 0.0f) : v.w;
+                *reinterpret_cast<float4 *>(epi.y + m * epi.N + n) = v;
+            }
+        };
+        if (interior) {
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int k = 0; k < G; ++k)
+                    if (g + k < FN) store(k, j, false);
+        } else {
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int k = 0; k < G; ++k)
+                    if (g + k < FN) store(k, j, true);
         }
-        if (epi.relu) {
-            v.x = fmaxf(v.x, 0.0f);
-            v.y = fmaxf(v.y, 0.0f);
-            v.z = fmaxf(v.z, 0.0f);
-            v.w = fmaxf(v.w, 0.0f);
-        }
-        *reinterpret_cast<float4 *>(epi.y + m * epi.N + n) = v;
     }
 }
 
@@ -583,28 +632,248 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
     // last MFMA results -> accumulator reads (16-cycle MFMA: >= 18 wait states)
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
-    // D of block (i, j): lane l, register e = row n 4*(l/16)+e, column m l%16.
-    float4 swv[C::FN], bv[C::FN];
+    tile_epilogue<C::FM, C::FN, OUT_Y, OUT_ACC>(epi, acc, bm0 + wm * C::WM + fr,
+                                                bn0 + wn * C::WN + 4 * fq);
+}
+
+// --------------------------------------- prefill GEMM on 128-byte LDS rows
+// The M > 128 kernel: block tile 256 x 224, WGM x WGN waves with int32
+// accumulators in AGPRs, as gemm_dma_kernel, but staged in K steps of 128
+// bytes so that every DMA instruction moves whole 128-byte cache lines (8 tile
+// rows x 128 B). With 64-byte rows each instruction used half of each line it
+// pulled from L2, and the DMA stream ran at ~60% of the full-line rate (14.6
+// vs 24.5 TB/s L2 -> LDS on this tile order).
+//
+//  * LDS: activations in a ring of 3 stages (3 x 32 KiB), weights in a ring
+//    of 2 (2 x 28 KiB): 152 KiB. A stage's activation loads are issued two
+//    stages ahead, its weight loads one stage ahead (weights first, so that
+//    one vmcnt threshold -- the activation loads of the stage after -- waits
+//    for exactly what the next stage needs).
+//  * Row layout: 128 B per tile row, 16-byte chunk c stored at c ^ swz8(row),
+//    conflict-free for the fragment reads (16 rows x one chunk per quarter
+//    wave).
+//  * One barrier per stage, placed PRE MFMAs into the stage's second half
+//    (64-K). After it, the DMA of the next stages is spread one instruction
+//    per IL MFMAs (a burst of DMA issues stalls the issuing waves' MFMAs
+//    behind the memory queue); the sequence runs into the next stage and is
+//    complete before the next barrier.
+//  * Fragment reads of the next half-stage are interleaved one per MFMA.
+//  * The stage body is generated slot by slot at compile time (static_for),
+//    so the 56-112 MFMA slots and their memory operations are straight-line
+//    code whatever the unroller's thresholds.
+constexpr int kL = 128;  // K bytes per stage
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N-1>{}):
+// a loop unrolled by construction, whose body sees its index as a constant.
+template <class Fn, int... Is>
+__device__ __forceinline__ void static_for_impl(Fn &&f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class Fn>
+__device__ __forceinline__ void static_for(Fn &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+__device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
+
+// WGM x WGN waves; PRE: MFMAs of a stage's second half before its barrier;
+// IL: MFMAs per DMA issue.
+template <int WGM_, int WGN_, int PRE, int IL>
+struct L128Cfg {
+    static constexpr int BM = 256, BN = 224, WGM = WGM_, WGN = WGN_;
+    static constexpr int NW = WGM * WGN, NT = NW * 64;
+    static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
+    static constexpr int RA = 3, RW = 2;                        // ring stages
+    static constexpr int A_SLOT = BM * kL, W_SLOT = BN * kL;    // 32 KiB, 28 KiB
+    static constexpr int A_INS = BM / 8, W_INS = BN / 8;        // 1 KiB loads per stage
+    static constexpr int APW = A_INS / NW;                      // per wave
+    static constexpr int WPW = (W_INS + NW - 1) / NW;           // waves >= W_INS % NW: WPW - 1
+    static constexpr bool W_EVEN = W_INS % NW == 0;             // every wave issues WPW
+    static constexpr int NDMA = WPW + APW;                      // DMA slots per stage
+    static constexpr int LDS_BYTES = RA * A_SLOT + RW * W_SLOT;
+    static constexpr int HALF = FM * FN;                        // MFMAs per 64-K half
+    static constexpr int T0 = HALF + PRE;                       // barrier slot
+    static_assert(A_INS % NW == 0 && (W_EVEN || W_INS / NW == WPW - 1), "load split");
+    static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(FM + FN <= HALF && T0 + FM + FN <= 2 * HALF, "fragment-read slots");
+    // DMA op q of the sequence started at the barrier of stage s sits after
+    // MFMA slot pos(q) (counted from stage s's first MFMA): ops with
+    // pos < 2*HALF ("head") are issued in stage s, the rest ("tail") at
+    // pos - 2*HALF in stage s+1, all before the next barrier.
+    static constexpr int pos(int q) { return T0 + IL * (q + 1) - 1; }
+    static constexpr bool head(int q) { return pos(q) < 2 * HALF; }
+    // head ops a wave issues (waves without the last W load skip op WPW-1)
+    static constexpr int head_ops(bool w_hi) {
+        int n = 0;
+        for (int q = 0; q < NDMA; ++q) n += head(q) && (q != WPW - 1 || w_hi);
+        return n;
+    }
+    static constexpr bool window_ok() { return pos(NDMA - 1) - 2 * HALF < T0; }
+};
+// The prefill configuration: 8 waves of 64 x 112 (two per SIMD). Four waves
+// of 128 x 112 (L128Cfg<2, 2, 8, 7>, one per SIMD) read 32% fewer LDS
+// fragment bytes and run at a higher clock, but lose that to single-wave
+// issue stalls: 1-2% slower on the prefill shape.
+using L128W8 = L128Cfg<4, 2, 8, 6>;
+static_assert(L128W8::window_ok(), "DMA window");
+
+template <class C, bool OUT_Y, bool OUT_ACC>
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NW / 4, C::NW / 4)))
+void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
+                      int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
+    using F = Frags<C::FM, C::FN>;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[C::LDS_BYTES];
+    int8_t *const sa = smem;
+    int8_t *const sw = smem + C::RA * C::A_SLOT;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tm, tn;
+    xcd_tile((int)blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t bm0 = (int64_t)tm * C::BM, bn0 = (int64_t)tn * C::BN;
+    const int nk = (int)(K / kL);  // >= 1 (host-checked K % 128 == 0)
+
+    // DMA instruction j of a stage covers tile rows 8j..8j+7: lane l takes row
+    // 8j + l/8 and fills LDS chunk l%8 with the row's logical chunk
+    // (l%8) ^ swz8(row). Wave w issues A loads j = w + NW*i and W loads
+    // j = w + NW*i < W_INS (with 8 waves: 4 A loads each, and 4 W loads for
+    // waves 0-3, 3 for waves 4-7).
+    const int8_t *pa[C::APW];
+    const int8_t *pw[C::WPW];
+    {
+        const int rr = lane >> 3, pc = lane & 7;
 #pragma unroll
-    for (int i = 0; i < C::FN; ++i) {
-        const int64_t n = std::min<int64_t>(bn0 + wn * C::WN + i * 16 + 4 * fq, N - 4);
-        swv[i] = float4{0.f, 0.f, 0.f, 0.f};
-        bv[i] = float4{0.f, 0.f, 0.f, 0.f};
-        if (OUT_Y) {
-            swv[i] = *reinterpret_cast<const float4 *>(epi.sw + n);
-            if (epi.bias) bv[i] = *reinterpret_cast<const float4 *>(epi.bias + n);
+        for (int i = 0; i < C::APW; ++i) {
+            const int r = 8 * (wid + C::NW * i) + rr;
+            pa[i] = A + std::min<int64_t>(bm0 + r, M - 1) * K + 16 * (pc ^ swz8(r));
+        }
+#pragma unroll
+        for (int i = 0; i < C::WPW; ++i) {
+            const int r = 8 * std::min(wid + C::NW * i, C::W_INS - 1) + rr;
+            pw[i] = B + std::min<int64_t>(bn0 + r, N - 1) * K + 16 * (pc ^ swz8(r));
         }
     }
-#pragma unroll
-    for (int j = 0; j < C::FM; ++j) {
-        const int64_t m = bm0 + wm * C::WM + j * 16 + fr;
-        const float sam = OUT_Y ? epi.sa[std::min<int64_t>(m, M - 1)] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < C::FN; ++i) {
-            const int64_t n = bn0 + wn * C::WN + i * 16 + 4 * fq;
-            epi_store4<OUT_Y, OUT_ACC>(epi, m, n, acc[i][j], sam, swv[i], bv[i]);
+    const bool w_hi = C::W_EVEN || wid < C::W_INS % C::NW;  // issues the last W load
+    // Loads of stage ks (clamped to the last stage: past the end the loop keeps
+    // issuing into slots that are never read again, so every barrier waits for
+    // the same count).
+    auto dma_w = [&](int i, int ks) {
+        const int kc = std::min(ks, nk - 1);
+        dma16(pw[i] + (int64_t)kc * kL, sw + (ks & 1) * C::W_SLOT + 1024 * (wid + C::NW * i));
+    };
+    auto dma_a = [&](int i, int ks, int slot3) {
+        const int kc = std::min(ks, nk - 1);
+        dma16(pa[i] + (int64_t)kc * kL, sa + slot3 * C::A_SLOT + 1024 * (wid + C::NW * i));
+    };
+    // Op q of the DMA sequence that follows the barrier of stage s: W loads of
+    // stage s+2, then A loads of stage s+3.
+    auto dma_op = [&](int q, int s, int slot3_s) {
+        if (q < C::WPW) {
+            if (q < C::WPW - 1 || w_hi) dma_w(q, s + 2);
+        } else {
+            dma_a(q - C::WPW, s + 3, slot3_s);  // (s+3) % 3 == s % 3
         }
+    };
+
+    const int wm = wid / C::WGN, wn = wid % C::WGN;
+    const int fr = lane & 15, fq = lane >> 4;
+    // fragment rows start at multiples of 16, so swz8(row) == swz8(fr)
+    const int a_row = (wm * C::WM + fr) * kL, b_row = (wn * C::WN + fr) * kL;
+    const int ch0 = 16 * (fq ^ swz8(fr)), ch1 = 16 * ((4 + fq) ^ swz8(fr));
+
+    v4i acc[C::FN][C::FM];
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    // Prologue: A(0); the sequence of "stage -2" (W(0), A(1)); the head ops of
+    // the sequence of "stage -1" (W(1), A(2)) -- its tail ops are issued by
+    // the first loop iteration, as every iteration issues the previous
+    // sequence's tail.
+#pragma unroll
+    for (int i = 0; i < C::APW; ++i) dma_a(i, 0, 0);
+#pragma unroll
+    for (int i = 0; i < C::WPW; ++i)
+        if (i < C::WPW - 1 || w_hi) dma_w(i, 0);
+#pragma unroll
+    for (int i = 0; i < C::APW; ++i) dma_a(i, 1, 1);
+#pragma unroll
+    for (int q = 0; q < C::NDMA; ++q)
+        if (C::head(q)) dma_op(q, -1, 2);
+    // A(0), W(0) of this wave landed: only A(1) and the head ops outstanding
+    if (w_hi)
+        wait_vmcnt<C::APW + C::head_ops(true)>();
+    else
+        wait_vmcnt<C::APW + C::head_ops(false)>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    asm volatile("s_nop 4" ::: "memory");  // AGPR writes of the zero-fill -> MFMA srcC
+
+    F f0, f1;
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j)
+        f0.a[j] = *reinterpret_cast<const v4i *>(sa + a_row + j * 16 * kL + ch0);
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+        f0.b[i] = *reinterpret_cast<const v4i *>(sw + b_row + i * 16 * kL + ch0);
+
+    int slot3 = 0;  // s % 3
+    for (int s = 0; s < nk; ++s) {
+        const int slot3n = slot3 == 2 ? 0 : slot3 + 1;            // (s+1) % 3
+        const int slot3p = slot3 == 0 ? 2 : slot3 - 1;            // (s-1) % 3 == (s+2) % 3
+        const int8_t *a_cur = sa + slot3 * C::A_SLOT, *w_cur = sw + (s & 1) * C::W_SLOT;
+        const int8_t *a_nxt = sa + slot3n * C::A_SLOT, *w_nxt = sw + ((s + 1) & 1) * C::W_SLOT;
+        // One MFMA slot t of the stage (t < HALF: first half on f0, else second
+        // half on f1) and the memory operations that follow it, generated at
+        // compile time for every t.
+        static_for<2 * C::HALF>([&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            if constexpr (t == C::T0) {
+                // fragments of this stage fully read; next stage's A and W in LDS
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                wait_vmcnt<C::APW>();
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            }
+            if constexpr (t < C::HALF) {
+                mfma_i8_acc<true>(acc[t / C::FM][t % C::FM], f0.b[t / C::FM], f0.a[t % C::FM]);
+            } else {
+                constexpr int u = t - C::HALF;
+                mfma_i8_acc<true>(acc[u / C::FM][u % C::FM], f1.b[u / C::FM], f1.a[u % C::FM]);
+            }
+            // second half of this stage -> f1 (weight fragments first: they
+            // were released earliest by the previous stage's MFMAs)
+            if constexpr (t < C::FN) {
+                f1.b[t] = *reinterpret_cast<const v4i *>(w_cur + b_row + t * 16 * kL + ch1);
+            } else if constexpr (t < C::FN + C::FM) {
+                constexpr int j = t - C::FN;
+                f1.a[j] = *reinterpret_cast<const v4i *>(a_cur + a_row + j * 16 * kL + ch1);
+            }
+            // first half of the next stage -> f0, after the barrier
+            if constexpr (t >= C::T0 && t < C::T0 + C::FM) {
+                constexpr int j = t - C::T0;
+                f0.a[j] = *reinterpret_cast<const v4i *>(a_nxt + a_row + j * 16 * kL + ch0);
+            } else if constexpr (t >= C::T0 + C::FM && t < C::T0 + C::FM + C::FN) {
+                constexpr int i = t - C::T0 - C::FM;
+                f0.b[i] = *reinterpret_cast<const v4i *>(w_nxt + b_row + i * 16 * kL + ch0);
+            }
+            // DMA: the tail of the sequence started at the previous barrier,
+            // then the head of this stage's
+            static_for<C::NDMA>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                if constexpr (!C::head(q) && t == C::pos(q) - 2 * C::HALF) dma_op(q, s - 1, slot3p);
+                if constexpr (C::head(q) && t == C::pos(q)) dma_op(q, s, slot3);
+            });
+        });
+        slot3 = slot3n;
     }
+    wait_vmcnt<0>();  // drain the trailing DMA before the block's LDS is released
+    // last MFMA results -> accumulator reads (16-cycle MFMA: >= 18 wait states)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+    tile_epilogue<C::FM, C::FN, OUT_Y, OUT_ACC>(epi, acc, bm0 + wm * C::WM + fr,
+                                                bn0 + wn * C::WN + 4 * fq);
 }
 
 // ------------------------------------------------------------ skinny GEMV
@@ -746,10 +1015,24 @@ static bool dma_ok(const int8_t *A, const int8_t *B, int64_t N, int64_t K, const
 // and DMA waits overlap the other's MFMAs; 2048x14336 is 512 tiles = two full
 // rounds on 256 CUs, one block per CU for the 128 KiB LDS ring), else 128x128
 // tiles with 4 waves of 64x64.
+template <class C>
+static int launch_l128(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
+                       const Epilogue &epi, hipStream_t st, const char *name) {
+    const int64_t tm = ceil_div(M, C::BM), tn = ceil_div(N, C::BN);
+    RNN_REQUIRE(tm * tn <= 0x7fffffffLL, "%s: too many tiles", name);
+    const unsigned grid = (unsigned)(tm * tn);
+    if (epi.y && epi.acc_out)
+        gemm_l128_kernel<C, true, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+    else if (epi.y)
+        gemm_l128_kernel<C, true, false><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+    else
+        gemm_l128_kernel<C, false, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+    return check_launch(name);
+}
 static int launch_dma_auto(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
                            const Epilogue &epi, hipStream_t st, const char *name) {
     if (M <= 128) return launch_dma<128, 128, 2, 2, 4>(A, B, M, N, K, epi, st, name);
-    return launch_dma<256, 224, 4, 2, 4>(A, B, M, N, K, epi, st, name);
+    return launch_l128<L128W8>(A, B, M, N, K, epi, st, name);
 }
 
 // Decode GEMV dispatch: one-shot workgroups of 4 waves per 16 weight rows,

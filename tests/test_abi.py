@@ -110,3 +110,17 @@ def test_product_path_has_no_cpu_fallback():
     finally:
         mod.LIB_PATH = saved
         mod._lib = None
+
+
+def test_build_rejects_kernels_demoted_to_scratch():
+    """build.py parses hipcc's resource-usage remarks and refuses a kernel that
+    uses scratch (private) memory: such a kernel computes correct values but
+    runs one to two orders of magnitude slower."""
+    import build
+    ok = ("remark: gemm.hip:10:0: Function Name: _ZN3rnn4goodEv\n"
+          "remark: gemm.hip:10:0:     ScratchSize [bytes/lane]: 0\n")
+    bad = ok + ("remark: gemm.hip:20:0: Function Name: _ZN3rnn3badEv\n"
+                "remark: gemm.hip:20:0:     VGPRs: 88\n"
+                "remark: gemm.hip:20:0:     ScratchSize [bytes/lane]: 1456\n")
+    assert build._scratch_kernels(ok) == []
+    assert build._scratch_kernels(bad) == ["_ZN3rnn3badEv (1456 B/lane)"]
