@@ -285,6 +285,23 @@ __device__ __forceinline__ void dma16(const void *g, void *lds) {
 #endif
 }
 
+// 16-byte buffer -> LDS DMA (buffer_load_dwordx4 ... offen lds): lane l's 16
+// bytes at base + voff + soff land at lds + 16*l (`lds` wave-uniform). The
+// descriptor covers `bytes` from `base`, so an offset past the operand reads
+// zeros instead of faulting. voff is a per-lane VGPR that the caller keeps
+// loop-invariant; soff (scalar) carries the per-stage advance. (Device pass
+// only, as dma16.)
+__device__ __forceinline__ void dma16_buf(const void *base, uint32_t bytes, uint32_t voff,
+                                          uint32_t soff, void *lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    // word 3 of a gfx9 buffer descriptor: 32-bit data format, no swizzle
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                             voff, soff, 0, 0);
+#endif
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
@@ -327,6 +344,19 @@ __device__ __forceinline__ uint32_t ternary_lut_entry(uint32_t x) {
         const uint32_t c = (x >> (2 * i)) & 3u;
         r |= (c == 1u ? 0x01u : (c == 2u ? 0xffu : 0u)) << (8 * i);
     }
+    return r;
+}
+
+// The same lookup in a table replicated R times (entry x of copy c at x*R + c)
+// with lane l reading copy l % R: lanes that look up different entries fall in
+// different LDS banks far more often than with a single 256-entry table.
+template <int R>
+__device__ __forceinline__ v4i ternary_lut_decode_rep(const uint32_t *lut_lane, uint32_t w) {
+    v4i r;
+    r.x = (int)lut_lane[(w & 0xffu) * R];
+    r.y = (int)lut_lane[((w >> 8) & 0xffu) * R];
+    r.z = (int)lut_lane[((w >> 16) & 0xffu) * R];
+    r.w = (int)lut_lane[(w >> 24) * R];
     return r;
 }
 
@@ -448,26 +478,38 @@ struct Frags {
     uint32_t w[FN];
 };
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, bool OUT_Y, bool OUT_ACC, bool TER>
-__global__ __launch_bounds__(WGM *WGN * 64)
-__attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4)))
+// KS > 1 splits K inside the block: KS groups of WGM x WGN waves each run the
+// pipeline below over K/KS with their own LDS stages, and the int32 partial
+// sums are added through LDS before group 0's epilogue (exact: wrapping int32
+// addition is associative). It gives a small tile more waves per CU.
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool OUT_Y, bool OUT_ACC, bool TER,
+          int KS = 1>
+__global__ __launch_bounds__(KS *WGM *WGN * 64)
+__attribute__((amdgpu_waves_per_eu(KS * WGM * WGN / 4, KS * WGM * WGN / 4)))
 void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
                      int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
     using C = DmaCfg<BM, BN, WGM, WGN, STAGES, TER>;
     using F = Frags<C::FM, C::FN>;
-    __shared__ __attribute__((aligned(1024))) int8_t smem[C::LDS_BYTES];
-    __shared__ uint32_t lut[TER ? 256 : 1];
+    constexpr int PART = C::NW * C::FN * C::FM * 64 * 16;  // one group's partial sums
+    static_assert(KS == 1 || (KS - 1) * PART <= KS * C::LDS_BYTES, "split-K partials fit in LDS");
+    static_assert(KS * C::LDS_BYTES <= 159 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    // one LDS object (stages, then the ternary decode table): see gemm_l128_kernel
+    __shared__ __attribute__((aligned(1024))) int8_t smem_all[KS * C::LDS_BYTES + (TER ? 1024 : 0)];
+    uint32_t *const lut = reinterpret_cast<uint32_t *>(smem_all + KS * C::LDS_BYTES);
     if (TER) {
-        for (int t = threadIdx.x; t < 256; t += C::NT) lut[t] = ternary_lut_entry((uint32_t)t);
+        for (int t = threadIdx.x; t < 256; t += KS * C::NT) lut[t] = ternary_lut_entry((uint32_t)t);
         __syncthreads();
     }
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = wave / C::NW, wid = wave % C::NW;  // K group, wave within the group
+    int8_t *const smem = smem_all + kg * C::LDS_BYTES;
     int tm, tn;
     xcd_tile((int)blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t bm0 = (int64_t)tm * BM, bn0 = (int64_t)tn * BN;
-    const int nk = (int)(K / kDmaBK);  // even, >= 2 (host-checked)
+    const int64_t kbase = kg * (K / KS);             // this group's K range
+    const int nk = (int)(K / KS / kDmaBK);           // even, >= 2 (host-checked)
 
     // Global sources of this wave's DMA loads at k = 0, and how far each
     // advances per K step (64 bytes, or 16 for packed ternary rows).
@@ -484,16 +526,16 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
             if (j < C::A_INS) {
                 const int r = 16 * j + rr;
                 const int64_t g = std::min<int64_t>(bm0 + r, M - 1);
-                src[i] = A + g * K + 16 * (pc ^ swz16(r));
+                src[i] = A + g * K + kbase + 16 * (pc ^ swz16(r));
             } else if (TER) {  // 64 packed rows x 16 bytes, lane = row
                 const int r = 64 * (j - C::A_INS) + lane;
                 const int64_t g = std::min<int64_t>(bn0 + r, N - 1);
-                src[i] = B + g * (K / 4);
+                src[i] = B + g * (K / 4) + kbase / 4;
                 kstep[i] = C::B_ROW;
             } else {
                 const int r = 16 * (j - C::A_INS) + rr;
                 const int64_t g = std::min<int64_t>(bn0 + r, N - 1);
-                src[i] = B + g * K + 16 * (pc ^ swz16(r));
+                src[i] = B + g * K + kbase + 16 * (pc ^ swz16(r));
             }
         }
     }
@@ -632,6 +674,38 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
     // last MFMA results -> accumulator reads (16-cycle MFMA: >= 18 wait states)
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
+    if constexpr (KS > 1) {
+        // groups 1..KS-1 park their partial sums in the (now idle) stage
+        // buffers, lane-contiguous 16-byte slots; group 0 adds them
+        __builtin_amdgcn_s_barrier();  // every group is done reading its stages
+        constexpr int WPART = C::FN * C::FM * 64;  // v4i per wave
+        v4i *red = reinterpret_cast<v4i *>(smem_all);
+        if (kg > 0) {
+            v4i *dst = red + ((kg - 1) * C::NW + wid) * WPART + lane;
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FM; ++j) dst[(i * C::FM + j) * 64] = acc[i][j];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kg > 0) return;
+#pragma unroll
+        for (int g = 1; g < KS; ++g) {
+            const v4i *srcp = red + ((g - 1) * C::NW + wid) * WPART + lane;
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FM; ++j) {
+                    const v4i p = srcp[(i * C::FM + j) * 64];
+                    acc[i][j].x = (int)((uint32_t)acc[i][j].x + (uint32_t)p.x);
+                    acc[i][j].y = (int)((uint32_t)acc[i][j].y + (uint32_t)p.y);
+                    acc[i][j].z = (int)((uint32_t)acc[i][j].z + (uint32_t)p.z);
+                    acc[i][j].w = (int)((uint32_t)acc[i][j].w + (uint32_t)p.w);
+                }
+        }
+    }
     tile_epilogue<C::FM, C::FN, OUT_Y, OUT_ACC>(epi, acc, bm0 + wm * C::WM + fr,
                                                 bn0 + wn * C::WN + 4 * fq);
 }
@@ -662,6 +736,7 @@ void gemm_dma_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B,
 //    so the 56-112 MFMA slots and their memory operations are straight-line
 //    code whatever the unroller's thresholds.
 constexpr int kL = 128;  // K bytes per stage
+constexpr int kTerLutCopies = 16;  // ternary decode table copies (16 KiB)
 
 // f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N-1>{}):
 // a loop unrolled by construction, whose body sees its index as a constant.
@@ -676,26 +751,41 @@ __device__ __forceinline__ void static_for(Fn &&f) {
 
 __device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
 
-// WGM x WGN waves; PRE: MFMAs of a stage's second half before its barrier;
-// IL: MFMAs per DMA issue.
-template <int WGM_, int WGN_, int PRE, int IL>
+// BM x BN block tile of WGM x WGN waves per K group; PRE: MFMAs of a stage's
+// second half before its barrier; IL: MFMAs per DMA issue; KS: K groups (K
+// split inside the block, partial sums added in LDS); TER: the weights are
+// packed 2-bit ternary codes (TernaryTensor::packed rows, 32 bytes per row per
+// 128-K stage), decoded to int8 MFMA operands through an LDS table.
+template <int BM_, int BN_, int WGM_, int WGN_, int PRE, int IL, int KS_ = 1, bool TER_ = false>
 struct L128Cfg {
-    static constexpr int BM = 256, BN = 224, WGM = WGM_, WGN = WGN_;
-    static constexpr int NW = WGM * WGN, NT = NW * 64;
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, KS = KS_;
+    static constexpr bool TER = TER_;
+    static constexpr int NW = WGM * WGN, NT = NW * 64;          // per K group
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
+    static constexpr int W_ROW = TER ? kL / 4 : kL;             // weight bytes per row per stage
+    static constexpr int W_LPR = W_ROW / 16;                    // lanes per weight row in a load
     static constexpr int RA = 3, RW = 2;                        // ring stages
-    static constexpr int A_SLOT = BM * kL, W_SLOT = BN * kL;    // 32 KiB, 28 KiB
-    static constexpr int A_INS = BM / 8, W_INS = BN / 8;        // 1 KiB loads per stage
+    static constexpr int A_SLOT = BM * kL, W_SLOT = BN * W_ROW;
+    static constexpr int A_INS = A_SLOT / 1024, W_INS = W_SLOT / 1024;  // 1 KiB loads per stage
     static constexpr int APW = A_INS / NW;                      // per wave
     static constexpr int WPW = (W_INS + NW - 1) / NW;           // waves >= W_INS % NW: WPW - 1
     static constexpr bool W_EVEN = W_INS % NW == 0;             // every wave issues WPW
     static constexpr int NDMA = WPW + APW;                      // DMA slots per stage
-    static constexpr int LDS_BYTES = RA * A_SLOT + RW * W_SLOT;
+    static constexpr int GROUP_LDS = RA * A_SLOT + RW * W_SLOT;
+    static constexpr int LDS_BYTES = KS * GROUP_LDS;
+    static constexpr int LUT_BYTES = TER ? 1024 * kTerLutCopies : 0;  // decode table copies
     static constexpr int HALF = FM * FN;                        // MFMAs per 64-K half
     static constexpr int T0 = HALF + PRE;                       // barrier slot
+    // fragment-read slots of a half: weight fragments (ternary: code words,
+    // then table decodes) and activation fragments
+    static constexpr int RD = TER ? 2 * FN + FM : FN + FM;
+    static constexpr int PART = NW * FN * FM * 64 * 16;         // one group's partial sums
+    static_assert(WM % 16 == 0 && WN % 16 == 0 && BM % WGM == 0 && BN % WGN == 0, "wave tiles");
+    static_assert(A_SLOT % 1024 == 0 && W_SLOT % 1024 == 0, "whole 1 KiB loads");
     static_assert(A_INS % NW == 0 && (W_EVEN || W_INS / NW == WPW - 1), "load split");
-    static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
-    static_assert(FM + FN <= HALF && T0 + FM + FN <= 2 * HALF, "fragment-read slots");
+    static_assert(LDS_BYTES + LUT_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(KS == 1 || (KS - 1) * PART <= LDS_BYTES, "split-K partials fit in LDS");
+    static_assert(RD <= HALF && T0 + RD <= 2 * HALF, "fragment-read slots");
     // DMA op q of the sequence started at the barrier of stage s sits after
     // MFMA slot pos(q) (counted from stage s's first MFMA): ops with
     // pos < 2*HALF ("head") are issued in stage s, the rest ("tail") at
@@ -711,59 +801,88 @@ struct L128Cfg {
     static constexpr bool window_ok() { return pos(NDMA - 1) - 2 * HALF < T0; }
 };
 // The prefill configuration: 8 waves of 64 x 112 (two per SIMD). Four waves
-// of 128 x 112 (L128Cfg<2, 2, 8, 7>, one per SIMD) read 32% fewer LDS
-// fragment bytes and run at a higher clock, but lose that to single-wave
+// of 128 x 112 (L128Cfg<256, 224, 2, 2, 8, 7>, one per SIMD) read 32% fewer
+// LDS fragment bytes and run at a higher clock, but lose that to single-wave
 // issue stalls: 1-2% slower on the prefill shape.
-using L128W8 = L128Cfg<4, 2, 8, 6>;
-static_assert(L128W8::window_ok(), "DMA window");
+using L128W8 = L128Cfg<256, 224, 4, 2, 8, 6>;
+// Ternary: 128 x 64 tiles (512 x 4096 is 256 tiles, one per CU) of two K
+// groups of 4 waves (64 x 32 each): 8 waves per CU. The barrier opens the
+// second half (PRE = 0) so that the next stage's code words can be read and
+// decoded inside the half.
+using L128Ter = L128Cfg<128, 64, 2, 2, 0, 3, 2, true>;
+static_assert(L128W8::window_ok() && L128Ter::window_ok(), "DMA window");
 
 template <class C, bool OUT_Y, bool OUT_ACC>
-__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(C::NW / 4, C::NW / 4)))
+__global__ __launch_bounds__(C::KS *C::NT)
+__attribute__((amdgpu_waves_per_eu(C::KS * C::NW / 4, C::KS * C::NW / 4)))
 void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
                       int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
     using F = Frags<C::FM, C::FN>;
-    __shared__ __attribute__((aligned(1024))) int8_t smem[C::LDS_BYTES];
-    int8_t *const sa = smem;
-    int8_t *const sw = smem + C::RA * C::A_SLOT;
+    // One LDS array (stage rings, then the ternary decode table): with a
+    // second __shared__ object the compiler tags LDS accesses with per-object
+    // alias scopes and then makes every fragment read that follows a DMA into
+    // the same object wait for all outstanding loads.
+    __shared__ __attribute__((aligned(1024))) int8_t smem_all[C::LDS_BYTES + C::LUT_BYTES];
+    uint32_t *const lut = reinterpret_cast<uint32_t *>(smem_all + C::LDS_BYTES);
+    if constexpr (C::TER) {
+        for (int t = threadIdx.x; t < 256 * kTerLutCopies; t += C::KS * C::NT)
+            lut[t] = ternary_lut_entry((uint32_t)(t / kTerLutCopies));
+        __syncthreads();
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = wave / C::NW, wid = wave % C::NW;  // K group, wave within the group
+    int8_t *const sa = smem_all + kg * C::GROUP_LDS;
+    int8_t *const sw = sa + C::RA * C::A_SLOT;
     int tm, tn;
     xcd_tile((int)blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t bm0 = (int64_t)tm * C::BM, bn0 = (int64_t)tn * C::BN;
-    const int nk = (int)(K / kL);  // >= 1 (host-checked K % 128 == 0)
+    const int64_t kbase = kg * (K / C::KS);  // this group's K range
+    const int nk = (int)(K / C::KS / kL);    // >= 1 (host-checked)
 
-    // DMA instruction j of a stage covers tile rows 8j..8j+7: lane l takes row
-    // 8j + l/8 and fills LDS chunk l%8 with the row's logical chunk
-    // (l%8) ^ swz8(row). Wave w issues A loads j = w + NW*i and W loads
-    // j = w + NW*i < W_INS (with 8 waves: 4 A loads each, and 4 W loads for
-    // waves 0-3, 3 for waves 4-7).
-    const int8_t *pa[C::APW];
-    const int8_t *pw[C::WPW];
+    // DMA instruction j of a stage covers activation rows 8j..8j+7 (lane l:
+    // row 8j + l/8, LDS chunk l%8 filled with the row's logical chunk
+    // (l%8) ^ swz8(row)), or weight rows W_ROW/16-lanes each: int8 as the
+    // activations; ternary 32 rows x 32 B (lane l: row 32j + l/2, LDS half l%2
+    // filled with the row's logical half (l%2) ^ ((row >> 3) & 1)). Wave w
+    // issues A loads j = w + NW*i and W loads j = w + NW*i < W_INS.
+    // A lane's source is a loop-invariant 32-bit byte offset into the operand
+    // (the host checks that the operands span less than 4 GiB) and the stage
+    // advance is the load's scalar offset, so no address register is written
+    // in the loop: the compiler makes a write to a register that an
+    // outstanding load used as its address wait for every outstanding load.
+    uint32_t oa[C::APW], ow[C::WPW];
     {
         const int rr = lane >> 3, pc = lane & 7;
 #pragma unroll
         for (int i = 0; i < C::APW; ++i) {
             const int r = 8 * (wid + C::NW * i) + rr;
-            pa[i] = A + std::min<int64_t>(bm0 + r, M - 1) * K + 16 * (pc ^ swz8(r));
+            oa[i] = (uint32_t)(std::min<int64_t>(bm0 + r, M - 1) * K + kbase + 16 * (pc ^ swz8(r)));
         }
+        const int wr = lane / C::W_LPR, wc = lane % C::W_LPR;
 #pragma unroll
         for (int i = 0; i < C::WPW; ++i) {
-            const int r = 8 * std::min(wid + C::NW * i, C::W_INS - 1) + rr;
-            pw[i] = B + std::min<int64_t>(bn0 + r, N - 1) * K + 16 * (pc ^ swz8(r));
+            const int r = (1024 / C::W_ROW) * std::min(wid + C::NW * i, C::W_INS - 1) + wr;
+            const int64_t g = std::min<int64_t>(bn0 + r, N - 1);
+            if constexpr (C::TER)
+                ow[i] = (uint32_t)(g * (K / 4) + kbase / 4 + 16 * (wc ^ ((r >> 3) & 1)));
+            else
+                ow[i] = (uint32_t)(g * K + kbase + 16 * (wc ^ swz8(r)));
         }
     }
     const bool w_hi = C::W_EVEN || wid < C::W_INS % C::NW;  // issues the last W load
     // Loads of stage ks (clamped to the last stage: past the end the loop keeps
     // issuing into slots that are never read again, so every barrier waits for
     // the same count).
+    const uint32_t a_bytes = (uint32_t)(M * K), w_bytes = (uint32_t)(N * (C::TER ? K / 4 : K));
     auto dma_w = [&](int i, int ks) {
-        const int kc = std::min(ks, nk - 1);
-        dma16(pw[i] + (int64_t)kc * kL, sw + (ks & 1) * C::W_SLOT + 1024 * (wid + C::NW * i));
+        dma16_buf(B, w_bytes, ow[i], (uint32_t)(std::min(ks, nk - 1) * C::W_ROW),
+                  sw + (ks & 1) * C::W_SLOT + 1024 * (wid + C::NW * i));
     };
     auto dma_a = [&](int i, int ks, int slot3) {
-        const int kc = std::min(ks, nk - 1);
-        dma16(pa[i] + (int64_t)kc * kL, sa + slot3 * C::A_SLOT + 1024 * (wid + C::NW * i));
+        dma16_buf(A, a_bytes, oa[i], (uint32_t)(std::min(ks, nk - 1) * kL),
+                  sa + slot3 * C::A_SLOT + 1024 * (wid + C::NW * i));
     };
     // Op q of the DMA sequence that follows the barrier of stage s: W loads of
     // stage s+2, then A loads of stage s+3.
@@ -777,9 +896,35 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
 
     const int wm = wid / C::WGN, wn = wid % C::WGN;
     const int fr = lane & 15, fq = lane >> 4;
-    // fragment rows start at multiples of 16, so swz8(row) == swz8(fr)
-    const int a_row = (wm * C::WM + fr) * kL, b_row = (wn * C::WN + fr) * kL;
+    const uint32_t *const lut_lane = lut + lane % kTerLutCopies;  // this lane's table copy
+    // fragment rows start at multiples of 16, so the row swizzles depend on fr
+    const int a_row = (wm * C::WM + fr) * kL, b_row = (wn * C::WN + fr) * C::W_ROW;
     const int ch0 = 16 * (fq ^ swz8(fr)), ch1 = 16 * ((4 + fq) ^ swz8(fr));
+    // weight fragment of half h: int8 chunk 4h+fq; ternary code word 4h+fq of
+    // the 32-byte row (16 codes), in the half h ^ ((fr >> 3) & 1)
+    const int wb0 = C::TER ? 16 * ((fr >> 3) & 1) + 4 * fq : ch0;
+    const int wb1 = C::TER ? 16 * (1 ^ ((fr >> 3) & 1)) + 4 * fq : ch1;
+    auto read_w = [&](const int8_t *slot, int i, int wb, F &f) {
+        if constexpr (C::TER)
+            f.w[i] = *reinterpret_cast<const uint32_t *>(slot + b_row + i * 16 * C::W_ROW + wb);
+        else
+            f.b[i] = *reinterpret_cast<const v4i *>(slot + b_row + i * 16 * C::W_ROW + wb);
+    };
+    auto read_a = [&](const int8_t *slot, int j, int ch, F &f) {
+        f.a[j] = *reinterpret_cast<const v4i *>(slot + a_row + j * 16 * kL + ch);
+    };
+    // the fragment-read slots of a half, starting at slot t0: weight words /
+    // fragments, activation fragments, (ternary) decodes
+    auto read_slot = [&](auto uc, const int8_t *aslot, const int8_t *wslot, int ch, int wb, F &f) {
+        constexpr int u = decltype(uc)::value;
+        if constexpr (u < C::FN) {
+            read_w(wslot, u, wb, f);
+        } else if constexpr (u < C::FN + C::FM) {
+            read_a(aslot, u - C::FN, ch, f);
+        } else if constexpr (C::TER && u < C::RD) {
+            f.b[u - C::FN - C::FM] = ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f.w[u - C::FN - C::FM]);
+        }
+    };
 
     v4i acc[C::FN][C::FM];
 #pragma unroll
@@ -811,12 +956,7 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
     asm volatile("s_nop 4" ::: "memory");  // AGPR writes of the zero-fill -> MFMA srcC
 
     F f0, f1;
-#pragma unroll
-    for (int j = 0; j < C::FM; ++j)
-        f0.a[j] = *reinterpret_cast<const v4i *>(sa + a_row + j * 16 * kL + ch0);
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i)
-        f0.b[i] = *reinterpret_cast<const v4i *>(sw + b_row + i * 16 * kL + ch0);
+    static_for<C::RD>([&](auto uc) { read_slot(uc, sa, sw, ch0, wb0, f0); });
 
     int slot3 = 0;  // s % 3
     for (int s = 0; s < nk; ++s) {
@@ -844,20 +984,11 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
             }
             // second half of this stage -> f1 (weight fragments first: they
             // were released earliest by the previous stage's MFMAs)
-            if constexpr (t < C::FN) {
-                f1.b[t] = *reinterpret_cast<const v4i *>(w_cur + b_row + t * 16 * kL + ch1);
-            } else if constexpr (t < C::FN + C::FM) {
-                constexpr int j = t - C::FN;
-                f1.a[j] = *reinterpret_cast<const v4i *>(a_cur + a_row + j * 16 * kL + ch1);
-            }
+            if constexpr (t < C::RD)
+                read_slot(std::integral_constant<int, t>{}, a_cur, w_cur, ch1, wb1, f1);
             // first half of the next stage -> f0, after the barrier
-            if constexpr (t >= C::T0 && t < C::T0 + C::FM) {
-                constexpr int j = t - C::T0;
-                f0.a[j] = *reinterpret_cast<const v4i *>(a_nxt + a_row + j * 16 * kL + ch0);
-            } else if constexpr (t >= C::T0 + C::FM && t < C::T0 + C::FM + C::FN) {
-                constexpr int i = t - C::T0 - C::FM;
-                f0.b[i] = *reinterpret_cast<const v4i *>(w_nxt + b_row + i * 16 * kL + ch0);
-            }
+            if constexpr (t >= C::T0 && t < C::T0 + C::RD)
+                read_slot(std::integral_constant<int, t - C::T0>{}, a_nxt, w_nxt, ch0, wb0, f0);
             // DMA: the tail of the sequence started at the previous barrier,
             // then the head of this stage's
             static_for<C::NDMA>([&](auto qc) {
@@ -872,6 +1003,40 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
     // last MFMA results -> accumulator reads (16-cycle MFMA: >= 18 wait states)
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
+    if constexpr (C::KS > 1) {
+        // groups 1..KS-1 park their partial sums in the (now idle) stage
+        // buffers, lane-contiguous 16-byte slots; group 0 adds them (exact:
+        // wrapping int32 addition is associative)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every group is done with its stages
+        constexpr int WPART = C::FN * C::FM * 64;  // v4i per wave
+        v4i *red = reinterpret_cast<v4i *>(smem_all);
+        if (kg > 0) {
+            v4i *dst = red + ((kg - 1) * C::NW + wid) * WPART + lane;
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FM; ++j) dst[(i * C::FM + j) * 64] = acc[i][j];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kg > 0) return;
+#pragma unroll
+        for (int g = 1; g < C::KS; ++g) {
+            const v4i *srcp = red + ((g - 1) * C::NW + wid) * WPART + lane;
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+                for (int j = 0; j < C::FM; ++j) {
+                    const v4i p = srcp[(i * C::FM + j) * 64];
+                    acc[i][j].x = (int)((uint32_t)acc[i][j].x + (uint32_t)p.x);
+                    acc[i][j].y = (int)((uint32_t)acc[i][j].y + (uint32_t)p.y);
+                    acc[i][j].z = (int)((uint32_t)acc[i][j].z + (uint32_t)p.z);
+                    acc[i][j].w = (int)((uint32_t)acc[i][j].w + (uint32_t)p.w);
+                }
+        }
+    }
     tile_epilogue<C::FM, C::FN, OUT_Y, OUT_ACC>(epi, acc, bm0 + wm * C::WM + fr,
                                                 bn0 + wn * C::WN + 4 * fq);
 }
@@ -983,21 +1148,23 @@ static int launch_tiled(const int8_t *A, const void *B, int64_t M, int64_t N, in
     return check_launch(name);
 }
 
-template <int BM, int BN, int WGM, int WGN, int STAGES, bool TER = false>
+template <int BM, int BN, int WGM, int WGN, int STAGES, bool TER = false, int KS = 1>
 static int launch_dma(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
                       const Epilogue &epi, hipStream_t st, const char *name) {
     using C = DmaCfg<BM, BN, WGM, WGN, STAGES, TER>;
     const int64_t tm = ceil_div(M, BM), tn = ceil_div(N, BN);
     RNN_REQUIRE(tm * tn <= 0x7fffffffLL, "%s: too many tiles", name);
-    const unsigned grid = (unsigned)(tm * tn);
+    RNN_REQUIRE(K % (2 * kDmaBK * KS) == 0, "%s: K must be a multiple of %d here", name,
+                2 * kDmaBK * KS);
+    const unsigned grid = (unsigned)(tm * tn), nt = KS * C::NT;
     if (epi.y && epi.acc_out)
-        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, true, TER><<<grid, C::NT, 0, st>>>(
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, true, TER, KS><<<grid, nt, 0, st>>>(
             A, B, M, N, K, (int)tm, (int)tn, epi);
     else if (epi.y)
-        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, false, TER><<<grid, C::NT, 0, st>>>(
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, true, false, TER, KS><<<grid, nt, 0, st>>>(
             A, B, M, N, K, (int)tm, (int)tn, epi);
     else
-        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, false, true, TER><<<grid, C::NT, 0, st>>>(
+        gemm_dma_kernel<BM, BN, WGM, WGN, STAGES, false, true, TER, KS><<<grid, nt, 0, st>>>(
             A, B, M, N, K, (int)tm, (int)tn, epi);
     return check_launch(name);
 }
@@ -1015,24 +1182,32 @@ static bool dma_ok(const int8_t *A, const int8_t *B, int64_t N, int64_t K, const
 // and DMA waits overlap the other's MFMAs; 2048x14336 is 512 tiles = two full
 // rounds on 256 CUs, one block per CU for the 128 KiB LDS ring), else 128x128
 // tiles with 4 waves of 64x64.
+// The 128-byte-row kernels address their DMA sources with 32-bit offsets.
+static bool l128_fits(int64_t M, int64_t N, int64_t K, bool ter) {
+    const uint64_t lim = 1ull << 32;
+    return (uint64_t)M * (uint64_t)K < lim && (uint64_t)N * (uint64_t)(ter ? K / 4 : K) < lim;
+}
 template <class C>
 static int launch_l128(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
                        const Epilogue &epi, hipStream_t st, const char *name) {
     const int64_t tm = ceil_div(M, C::BM), tn = ceil_div(N, C::BN);
     RNN_REQUIRE(tm * tn <= 0x7fffffffLL, "%s: too many tiles", name);
-    const unsigned grid = (unsigned)(tm * tn);
+    RNN_REQUIRE(K % (kL * C::KS) == 0, "%s: K must be a multiple of %d here", name, kL * C::KS);
+    RNN_REQUIRE(l128_fits(M, N, K, C::TER), "%s: operands of 4 GiB or more", name);
+    const unsigned grid = (unsigned)(tm * tn), nt = C::KS * C::NT;
     if (epi.y && epi.acc_out)
-        gemm_l128_kernel<C, true, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+        gemm_l128_kernel<C, true, true><<<grid, nt, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
     else if (epi.y)
-        gemm_l128_kernel<C, true, false><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+        gemm_l128_kernel<C, true, false><<<grid, nt, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
     else
-        gemm_l128_kernel<C, false, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+        gemm_l128_kernel<C, false, true><<<grid, nt, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
     return check_launch(name);
 }
 static int launch_dma_auto(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
                            const Epilogue &epi, hipStream_t st, const char *name) {
     if (M <= 128) return launch_dma<128, 128, 2, 2, 4>(A, B, M, N, K, epi, st, name);
-    return launch_l128<L128W8>(A, B, M, N, K, epi, st, name);
+    if (l128_fits(M, N, K, false)) return launch_l128<L128W8>(A, B, M, N, K, epi, st, name);
+    return launch_dma<256, 224, 4, 2, 4>(A, B, M, N, K, epi, st, name);
 }
 
 // Decode GEMV dispatch: one-shot workgroups of 4 waves per 16 weight rows,
@@ -1119,9 +1294,15 @@ extern "C" int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_
                          name, (long long)k, (long long)n);
     hipStream_t st = as_stream(stream);
     // 128x64 tiles (4 waves of 64x32): a 512x4096 output is 256 tiles, one per
-    // CU; each weight code word is decoded once per 128 activation rows.
-    if (algo == RNN_ALGO_TILED_DMA || (algo == RNN_ALGO_AUTO && dma))
+    // CU; each weight code word is decoded once per 128 activation rows. With
+    // one wave per SIMD, each 64-K step's dependent chain (code word read, LDS
+    // table lookups, MFMAs) is exposed, so K is split over 2 wave groups when
+    // it divides (8 waves per CU, int32 partial sums added in LDS).
+    if (algo == RNN_ALGO_TILED_DMA || (algo == RNN_ALGO_AUTO && dma)) {
+        if (k % (kL * L128Ter::KS) == 0 && l128_fits(m, n, k, true))
+            return launch_l128<L128Ter>(aq, pb, m, n, k, epi, st, name);
         return launch_dma<128, 64, 2, 2, 4, true>(aq, pb, m, n, k, epi, st, name);
+    }
     return launch_tiled<128, 128, 64, 64, true>(aq, packed, m, n, k, epi, st, name);
 }
 
