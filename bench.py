@@ -293,7 +293,7 @@ def main():
                          "traffic": traffic_for("w8a8_prefill_gemm"),
                          "op_kind": "int8 MFMA ops, 2 per multiply-accumulate (T int-op/s)",
                          "ops_per_launch": ops,
-                         "kernel": "gemm_dma_kernel<256,224,4,2,4> (v_mfma_i32_16x16x64_i8)",
+                         "kernel": "gemm_l128_kernel<L128Cfg<256,224,4,2,8,6>> (v_mfma_i32_16x16x64_i8, 128-byte LDS rows)",
                          "timing": "HIP events on the launch stream, average over the timed "
                                    "launches"},
         })
