@@ -191,6 +191,29 @@ def test_w8a8_lds_dma_rejects_unsupported(dev, hip):
     assert_f32_equal(host(y), O.w8a8_linear(aq, sa, wq, sw)[0])
 
 
+def test_w8a8_activations_over_4gib(dev, hip):
+    """An activation matrix of more than 4 GiB: the 128-byte-row kernel
+    addresses its DMA sources with 32-bit offsets, so this shape takes the
+    64-bit-addressed LDS-DMA kernel. Rows on both sides of byte offset 2^32
+    (row 2^20 at K = 4096), the first and the last, against the oracle."""
+    import torch
+    k, n = 4096, 228                      # ragged N tile
+    m = (1 << 20) + 300                   # 4 GiB + 1.2 MB of int8 activations
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    aq = torch.randint(-128, 128, (m, k), dtype=torch.int8, device=dev, generator=g)
+    sa = torch.rand(m, device=dev, generator=g) + 0.5
+    _, _, wq, sw, bias = w8a8_case(4, k, n, seed=12)
+    y, _ = hip.w8a8_linear(aq, sa, to_dev(wq, dev), to_dev(sw, dev), to_dev(bias, dev), relu=True)
+    rows = [0, 1, (1 << 20) - 1, 1 << 20, (1 << 20) + 1, m - 1]
+    idx = torch.tensor(rows, device=dev)
+    aq_s, sa_s, y_s = host(aq[idx]), host(sa[idx]), host(y[idx])
+    del aq, y
+    torch.cuda.empty_cache()
+    ye, _ = O.w8a8_linear(aq_s, sa_s, wq, sw, bias, True)
+    assert_f32_equal(y_s, ye)
+
+
 @pytest.mark.parametrize("m,k,n", W.GEMV_SHAPES)
 def test_w8a8_decode_gemv_full_size(dev, hip, m, k, n):
     # BASELINE decode config: 1% activation outliers x20
