@@ -254,8 +254,10 @@ def cpu_baseline(state, max_repeats=5, budget_s=20.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # The warmup covers the clock ramp: from idle the first ~100 prefill
+    # launches run up to 25% slower while the GPU raises its clocks.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--only", default="all",
                     choices=["all", "prefill", "gemv", "ternary", "rotorquant", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
@@ -293,7 +295,7 @@ def main():
                          "traffic": traffic_for("w8a8_prefill_gemm"),
                          "op_kind": "int8 MFMA ops, 2 per multiply-accumulate (T int-op/s)",
                          "ops_per_launch": ops,
-                         "kernel": "gemm_l128_kernel<L128Cfg<256,224,4,2,8,6>> (v_mfma_i32_16x16x64_i8, 128-byte LDS rows)",
+                         "kernel": "gemm_pp_kernel<L128Cfg<256,224,4,2,0,1>> (ping-pong, v_mfma_i32_16x16x64_i8, 128-byte LDS rows)",
                          "timing": "HIP events on the launch stream, average over the timed "
                                    "launches"},
         })

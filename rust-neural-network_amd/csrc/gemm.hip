@@ -393,6 +393,12 @@ __device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int &t
 //    merge its wait-count state at every join and drain the stores there.
 //  * The arithmetic is the reference's: ((float)acc * sa[m]) * sw[n], then
 //    + bias[n], then max(., 0) (src/int8.rs:159-162).
+// True when the wave tile at (m0, n0) (lane-adjusted as in tile_epilogue) lies
+// inside M x N, so that every lane issues all of its FM * FN stores.
+template <int FM, int FN>
+__device__ __forceinline__ bool tile_interior(const Epilogue &epi, int64_t m0, int64_t n0) {
+    return m0 - (m0 & 15) + 16 * FM <= epi.M && n0 - (n0 & 15) + 16 * FN <= epi.N;
+}
 template <int FM, int FN, bool OUT_Y, bool OUT_ACC, int G = (FN < 4 ? FN : 4)>
 __device__ __forceinline__ void tile_epilogue(const Epilogue &epi, const v4i (&acc)[FN][FM],
                                               int64_t m0, int64_t n0) {
@@ -402,7 +408,7 @@ __device__ __forceinline__ void tile_epilogue(const Epilogue &epi, const v4i (&a
     for (int j = 0; j < FM; ++j)
         sam[j] = OUT_Y ? epi.sa[std::min<int64_t>(m0 + 16 * j, epi.M - 1)] : 0.0f;
     // the wave tile's corner: bounds checks are needed only past the edges
-    const bool interior = m0 - (m0 & 15) + 16 * FM <= epi.M && n0 - (n0 & 15) + 16 * FN <= epi.N;
+    const bool interior = tile_interior<FM, FN>(epi, m0, n0);
 
     // Column blocks in groups of G (the operand registers of a group stay
     // within a two-waves-per-SIMD budget): operand loads, then the stores.
@@ -800,17 +806,18 @@ struct L128Cfg {
     }
     static constexpr bool window_ok() { return pos(NDMA - 1) - 2 * HALF < T0; }
 };
-// The prefill configuration: 8 waves of 64 x 112 (two per SIMD). Four waves
-// of 128 x 112 (L128Cfg<256, 224, 2, 2, 8, 7>, one per SIMD) read 32% fewer
-// LDS fragment bytes and run at a higher clock, but lose that to single-wave
-// issue stalls: 1-2% slower on the prefill shape.
-using L128W8 = L128Cfg<256, 224, 4, 2, 8, 6>;
+// The prefill geometry (run by gemm_pp_kernel, whose schedule does not use
+// PRE / IL): 256 x 224 block tiles, 8 waves of 64 x 112 (two per SIMD). Four
+// waves of 128 x 112 (one per SIMD) read 32% fewer LDS fragment bytes and run
+// at a higher clock, but lose that to single-wave issue stalls: 1-2% slower
+// on the prefill shape.
+using PrefillCfg = L128Cfg<256, 224, 4, 2, 0, 1>;
 // Ternary: 128 x 64 tiles (512 x 4096 is 256 tiles, one per CU) of two K
 // groups of 4 waves (64 x 32 each): 8 waves per CU. The barrier opens the
 // second half (PRE = 0) so that the next stage's code words can be read and
 // decoded inside the half.
 using L128Ter = L128Cfg<128, 64, 2, 2, 0, 3, 2, true>;
-static_assert(L128W8::window_ok() && L128Ter::window_ok(), "DMA window");
+static_assert(L128Ter::window_ok(), "DMA window");
 
 template <class C, bool OUT_Y, bool OUT_ACC>
 __global__ __launch_bounds__(C::KS *C::NT)
@@ -1041,6 +1048,171 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
                                                 bn0 + wn * C::WN + 4 * fq);
 }
 
+// ------------------------------------------ prefill: ping-pong (8 waves)
+// The tiles, LDS rings, DMA addressing and epilogue of gemm_l128_kernel, with
+// the two waves of a SIMD taking turns instead of each interleaving reads and
+// MFMAs: in each phase one group of 4 waves (one per SIMD) issues the 28 MFMAs
+// of a half-stage back to back while the other group reads its next fragments
+// and issues its share of the DMA; a barrier swaps the roles (1% faster than
+// the interleaved schedule on the prefill shape). Four phases per 128-K stage s:
+//   phase 4s   : G0 computes (s,0)      G1 reads (s,0), DMA
+//   phase 4s+1 : G0 reads (s,1), DMA    G1 computes (s,0)
+//   phase 4s+2 : G0 computes (s,1)      G1 reads (s,1), DMA
+//   phase 4s+3 : G0 reads (s+1,0), DMA  G1 computes (s,1)
+// Stage s is read in phases 4s-1 .. 4s+2, so its slots take the DMA of
+// sequence s (W(s+2), then A(s+3)) from phase 4s+3 on; each wave issues its
+// ops of a sequence in its two load phases of the window [4s+3, 4s+7), weight
+// loads first. At the end of phase 4s+2 every wave waits until only its A
+// loads of the latest sequence are in flight: stage s+1 has landed.
+template <class C, bool OUT_Y, bool OUT_ACC>
+__global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_pp_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
+                    int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
+    static_assert(C::NW == 8 && C::KS == 1 && !C::TER, "two groups of four int8 waves");
+    static_assert(C::NDMA % 2 == 0 && C::NDMA / 2 == C::WPW, "first half: W ops, second: A ops");
+    using F = Frags<C::FM, C::FN>;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[C::LDS_BYTES];
+    int8_t *const sa = smem;
+    int8_t *const sw = smem + C::RA * C::A_SLOT;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wid >> 2;  // waves w and w+4 share SIMD w
+    int tm, tn;
+    xcd_tile((int)blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t bm0 = (int64_t)tm * C::BM, bn0 = (int64_t)tn * C::BN;
+    const int nk = (int)(K / kL);
+
+    uint32_t oa[C::APW], ow[C::WPW];
+    {
+        const int rr = lane >> 3, pc = lane & 7;
+#pragma unroll
+        for (int i = 0; i < C::APW; ++i) {
+            const int r = 8 * (wid + C::NW * i) + rr;
+            oa[i] = (uint32_t)(std::min<int64_t>(bm0 + r, M - 1) * K + 16 * (pc ^ swz8(r)));
+        }
+#pragma unroll
+        for (int i = 0; i < C::WPW; ++i) {
+            const int r = 8 * std::min(wid + C::NW * i, C::W_INS - 1) + rr;
+            ow[i] = (uint32_t)(std::min<int64_t>(bn0 + r, N - 1) * K + 16 * (pc ^ swz8(r)));
+        }
+    }
+    const bool w_hi = C::W_EVEN || wid < C::W_INS % C::NW;
+    const uint32_t a_bytes = (uint32_t)(M * K), w_bytes = (uint32_t)(N * K);
+    auto dma_w = [&](int i, int ks) {
+        dma16_buf(B, w_bytes, ow[i], (uint32_t)(std::min(ks, nk - 1) * kL),
+                  sw + (ks & 1) * C::W_SLOT + 1024 * (wid + C::NW * i));
+    };
+    auto dma_a = [&](int i, int ks, int slot3) {
+        dma16_buf(A, a_bytes, oa[i], (uint32_t)(std::min(ks, nk - 1) * kL),
+                  sa + slot3 * C::A_SLOT + 1024 * (wid + C::NW * i));
+    };
+    // the two halves of sequence s: its W loads (stage s+2), its A loads
+    // (stage s+3, into slot s % 3)
+    auto dma_w_half = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < C::WPW; ++i)
+            if (i < C::WPW - 1 || w_hi) dma_w(i, s + 2);
+    };
+    auto dma_a_half = [&](int s, int slot3_s) {
+#pragma unroll
+        for (int i = 0; i < C::APW; ++i) dma_a(i, s + 3, slot3_s);
+    };
+
+    const int wm = wid / C::WGN, wn = wid % C::WGN;
+    const int fr = lane & 15, fq = lane >> 4;
+    const int a_row = (wm * C::WM + fr) * kL, b_row = (wn * C::WN + fr) * kL;
+    const int ch0 = 16 * (fq ^ swz8(fr)), ch1 = 16 * ((4 + fq) ^ swz8(fr));
+    auto load = [&](const int8_t *aslot, const int8_t *wslot, int ch, F &f) {
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j)
+            f.a[j] = *reinterpret_cast<const v4i *>(aslot + a_row + j * 16 * kL + ch);
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i)
+            f.b[i] = *reinterpret_cast<const v4i *>(wslot + b_row + i * 16 * kL + ch);
+    };
+    v4i acc[C::FN][C::FM];
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    auto compute = [&](const F &f) {
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FM; ++j) mfma_i8_acc<true>(acc[i][j], f.b[i], f.a[j]);
+    };
+    auto barrier = [&]() {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // Prologue: A(0), W(0), A(1); G0 also the first half of sequence -1
+    // (W(1)), which the loop would have issued in phase -1.
+#pragma unroll
+    for (int i = 0; i < C::APW; ++i) dma_a(i, 0, 0);
+#pragma unroll
+    for (int i = 0; i < C::WPW; ++i)
+        if (i < C::WPW - 1 || w_hi) dma_w(i, 0);
+#pragma unroll
+    for (int i = 0; i < C::APW; ++i) dma_a(i, 1, 1);
+    F f;
+    if (grp == 0) {
+        dma_w_half(-1);
+        // A(0), W(0) landed: A(1) and W(1) outstanding
+        if (w_hi)
+            wait_vmcnt<C::APW + C::WPW>();
+        else
+            wait_vmcnt<C::APW + C::WPW - 1>();
+        barrier();
+        asm volatile("s_nop 4" ::: "memory");  // AGPR writes of the zero-fill -> MFMA srcC
+        load(sa, sw, ch0, f);                  // (0,0), phase -1
+        barrier();
+        int slot3 = 0;
+        for (int s = 0; s < nk; ++s) {
+            const int slot3n = slot3 == 2 ? 0 : slot3 + 1, slot3p = slot3 == 0 ? 2 : slot3 - 1;
+            compute(f);                                                      // 4s: (s,0)
+            barrier();
+            load(sa + slot3 * C::A_SLOT, sw + (s & 1) * C::W_SLOT, ch1, f);  // 4s+1: (s,1)
+            dma_a_half(s - 1, slot3p);
+            barrier();
+            compute(f);                                                      // 4s+2: (s,1)
+            wait_vmcnt<C::APW>();
+            barrier();
+            load(sa + slot3n * C::A_SLOT, sw + ((s + 1) & 1) * C::W_SLOT, ch0, f);  // 4s+3: (s+1,0)
+            dma_w_half(s);
+            barrier();
+            slot3 = slot3n;
+        }
+    } else {
+        wait_vmcnt<C::APW>();  // A(0), W(0) landed: A(1) outstanding
+        barrier();
+        asm volatile("s_nop 4" ::: "memory");
+        barrier();
+        int slot3 = 0;
+        for (int s = 0; s < nk; ++s) {
+            const int slot3n = slot3 == 2 ? 0 : slot3 + 1, slot3p = slot3 == 0 ? 2 : slot3 - 1;
+            load(sa + slot3 * C::A_SLOT, sw + (s & 1) * C::W_SLOT, ch0, f);  // 4s: (s,0)
+            dma_w_half(s - 1);
+            barrier();
+            compute(f);                                                      // 4s+1: (s,0)
+            barrier();
+            load(sa + slot3 * C::A_SLOT, sw + (s & 1) * C::W_SLOT, ch1, f);  // 4s+2: (s,1)
+            dma_a_half(s - 1, slot3p);
+            wait_vmcnt<C::APW>();
+            barrier();
+            compute(f);                                                      // 4s+3: (s,1)
+            barrier();
+            slot3 = slot3n;
+        }
+    }
+    wait_vmcnt<0>();  // drain the trailing DMA before the block's LDS is released
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    tile_epilogue<C::FM, C::FN, OUT_Y, OUT_ACC>(epi, acc, bm0 + wm * C::WM + fr,
+                                                bn0 + wn * C::WN + 4 * fq);
+}
+
 // ------------------------------------------------------------ skinny GEMV
 // M <= 16 (decode). One workgroup per 16 output columns; the WAVES waves of a
 // workgroup split K, each streaming its K range of the 16 weight rows with
@@ -1203,10 +1375,28 @@ static int launch_l128(const int8_t *A, const int8_t *B, int64_t M, int64_t N, i
         gemm_l128_kernel<C, false, true><<<grid, nt, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
     return check_launch(name);
 }
+template <class C>
+static int launch_pp(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
+                     const Epilogue &epi, hipStream_t st, const char *name) {
+    const int64_t tm = ceil_div(M, C::BM), tn = ceil_div(N, C::BN);
+    RNN_REQUIRE(tm * tn <= 0x7fffffffLL, "%s: too many tiles", name);
+    RNN_REQUIRE(K % kL == 0, "%s: K must be a multiple of %d here", name, kL);
+    RNN_REQUIRE(l128_fits(M, N, K, false), "%s: operands of 4 GiB or more", name);
+    const unsigned grid = (unsigned)(tm * tn);
+    if (epi.y && epi.acc_out)
+        gemm_pp_kernel<C, true, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+    else if (epi.y)
+        gemm_pp_kernel<C, true, false><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+    else
+        gemm_pp_kernel<C, false, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+    return check_launch(name);
+}
 static int launch_dma_auto(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
                            const Epilogue &epi, hipStream_t st, const char *name) {
     if (M <= 128) return launch_dma<128, 128, 2, 2, 4>(A, B, M, N, K, epi, st, name);
-    if (l128_fits(M, N, K, false)) return launch_l128<L128W8>(A, B, M, N, K, epi, st, name);
+    if (l128_fits(M, N, K, false)) {
+        return launch_pp<PrefillCfg>(A, B, M, N, K, epi, st, name);
+    }
     return launch_dma<256, 224, 4, 2, 4>(A, B, M, N, K, epi, st, name);
 }
 
