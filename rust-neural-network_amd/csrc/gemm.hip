@@ -761,11 +761,18 @@ __device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
 // second half before its barrier; IL: MFMAs per DMA issue; KS: K groups (K
 // split inside the block, partial sums added in LDS); TER: the weights are
 // packed 2-bit ternary codes (TernaryTensor::packed rows, 32 bytes per row per
-// 128-K stage), decoded to int8 MFMA operands through an LDS table.
-template <int BM_, int BN_, int WGM_, int WGN_, int PRE, int IL, int KS_ = 1, bool TER_ = false>
+// 128-K stage), decoded to int8 MFMA operands through an LDS table. DEC
+// (ternary only, > 0): the early-word schedule -- the code words of both
+// halves of the next stage are read right after the barrier, the next
+// stage's first half is decoded DEC MFMAs after it and its second half at the
+// start of that stage, so no table lookup sits just before the MFMAs that use
+// it.
+template <int BM_, int BN_, int WGM_, int WGN_, int PRE, int IL, int KS_ = 1, bool TER_ = false,
+          int DEC_ = 0>
 struct L128Cfg {
     static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, KS = KS_;
     static constexpr bool TER = TER_;
+    static constexpr int DEC = DEC_;
     static constexpr int NW = WGM * WGN, NT = NW * 64;          // per K group
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
     static constexpr int W_ROW = TER ? kL / 4 : kL;             // weight bytes per row per stage
@@ -791,7 +798,11 @@ struct L128Cfg {
     static_assert(A_INS % NW == 0 && (W_EVEN || W_INS / NW == WPW - 1), "load split");
     static_assert(LDS_BYTES + LUT_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(KS == 1 || (KS - 1) * PART <= LDS_BYTES, "split-K partials fit in LDS");
-    static_assert(RD <= HALF && T0 + RD <= 2 * HALF, "fragment-read slots");
+    static_assert(DEC > 0 || (RD <= HALF && T0 + RD <= 2 * HALF), "fragment-read slots");
+    static_assert(DEC == 0 || (TER && FN + FM <= T0 && T0 + FM < 2 * HALF &&
+                               DEC >= 1 && T0 + DEC + FN <= 2 * HALF),
+                  "early-word slots: second-half decodes and activations before the barrier, "
+                  "the next stage's activations and decodes after it");
     // DMA op q of the sequence started at the barrier of stage s sits after
     // MFMA slot pos(q) (counted from stage s's first MFMA): ops with
     // pos < 2*HALF ("head") are issued in stage s, the rest ("tail") at
@@ -812,11 +823,14 @@ struct L128Cfg {
 // at a higher clock, but lose that to single-wave issue stalls: 1-2% slower
 // on the prefill shape.
 using PrefillCfg = L128Cfg<256, 224, 4, 2, 0, 1>;
-// Ternary: 128 x 64 tiles (512 x 4096 is 256 tiles, one per CU) of two K
-// groups of 4 waves (64 x 32 each): 8 waves per CU. The barrier opens the
-// second half (PRE = 0) so that the next stage's code words can be read and
-// decoded inside the half.
-using L128Ter = L128Cfg<128, 64, 2, 2, 0, 3, 2, true>;
+// Ternary: 64 x 128 tiles (512 x 4096 is 256 tiles, one per CU) of two K
+// groups of 4 waves (64 x 32 each): 8 waves per CU. Against 128 x 64 tiles a
+// block moves a third fewer bytes into LDS (64 activation rows per stage
+// instead of 128) and no weight word is decoded by two waves. The
+// early-word schedule decodes the next stage's first half 3 MFMAs after the
+// barrier. Measured on 512 x 4096 x 4096: 12.99 us against 13.63 us for
+// 128 x 64 tiles with the plain schedule.
+using L128Ter = L128Cfg<64, 128, 1, 4, 0, 3, 2, true, 3>;
 static_assert(L128Ter::window_ok(), "DMA window");
 
 template <class C, bool OUT_Y, bool OUT_ACC>
@@ -831,11 +845,6 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
     // the same object wait for all outstanding loads.
     __shared__ __attribute__((aligned(1024))) int8_t smem_all[C::LDS_BYTES + C::LUT_BYTES];
     uint32_t *const lut = reinterpret_cast<uint32_t *>(smem_all + C::LDS_BYTES);
-    if constexpr (C::TER) {
-        for (int t = threadIdx.x; t < 256 * kTerLutCopies; t += C::KS * C::NT)
-            lut[t] = ternary_lut_entry((uint32_t)(t / kTerLutCopies));
-        __syncthreads();
-    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -953,6 +962,13 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
 #pragma unroll
     for (int q = 0; q < C::NDMA; ++q)
         if (C::head(q)) dma_op(q, -1, 2);
+    // the decode table is built while the first loads are in flight (the
+    // barrier below publishes it)
+    if constexpr (C::TER) {
+        for (int t = threadIdx.x; t < 256 * kTerLutCopies; t += C::KS * C::NT)
+            lut[t] = ternary_lut_entry((uint32_t)(t / kTerLutCopies));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
     // A(0), W(0) of this wave landed: only A(1) and the head ops outstanding
     if (w_hi)
         wait_vmcnt<C::APW + C::head_ops(true)>();
@@ -963,7 +979,20 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
     asm volatile("s_nop 4" ::: "memory");  // AGPR writes of the zero-fill -> MFMA srcC
 
     F f0, f1;
-    static_for<C::RD>([&](auto uc) { read_slot(uc, sa, sw, ch0, wb0, f0); });
+    if constexpr (C::DEC > 0) {
+        // stage 0: the code words of both halves, the first half's
+        // activations and decodes (the second half decodes at its start)
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) read_w(sw, i, wb0, f0);
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) read_w(sw, i, wb1, f1);
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) read_a(sa, j, ch0, f0);
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) f0.b[i] = ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f0.w[i]);
+    } else {
+        static_for<C::RD>([&](auto uc) { read_slot(uc, sa, sw, ch0, wb0, f0); });
+    }
 
     int slot3 = 0;  // s % 3
     for (int s = 0; s < nk; ++s) {
@@ -989,13 +1018,35 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
                 constexpr int u = t - C::HALF;
                 mfma_i8_acc<true>(acc[u / C::FM][u % C::FM], f1.b[u / C::FM], f1.a[u % C::FM]);
             }
-            // second half of this stage -> f1 (weight fragments first: they
-            // were released earliest by the previous stage's MFMAs)
-            if constexpr (t < C::RD)
-                read_slot(std::integral_constant<int, t>{}, a_cur, w_cur, ch1, wb1, f1);
-            // first half of the next stage -> f0, after the barrier
-            if constexpr (t >= C::T0 && t < C::T0 + C::RD)
-                read_slot(std::integral_constant<int, t - C::T0>{}, a_nxt, w_nxt, ch0, wb0, f0);
+            if constexpr (C::DEC > 0) {
+                // early-word schedule: this stage's second half decodes its
+                // words (read after the previous barrier), then reads its
+                // activations; after the barrier, the next stage's words of
+                // both halves, its first-half activations and, DEC MFMAs in,
+                // its first-half decodes
+                if constexpr (t < C::FN)
+                    f1.b[t] = ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f1.w[t]);
+                else if constexpr (t < C::FN + C::FM)
+                    read_a(a_cur, t - C::FN, ch1, f1);
+                if constexpr (t == C::T0) {
+#pragma unroll
+                    for (int i = 0; i < C::FN; ++i) read_w(w_nxt, i, wb0, f0);
+#pragma unroll
+                    for (int i = 0; i < C::FN; ++i) read_w(w_nxt, i, wb1, f1);
+                }
+                if constexpr (t > C::T0 && t <= C::T0 + C::FM) read_a(a_nxt, t - C::T0 - 1, ch0, f0);
+                if constexpr (t >= C::T0 + C::DEC && t < C::T0 + C::DEC + C::FN)
+                    f0.b[t - C::T0 - C::DEC] =
+                        ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f0.w[t - C::T0 - C::DEC]);
+            } else {
+                // second half of this stage -> f1 (weight fragments first:
+                // they were released earliest by the previous stage's MFMAs)
+                if constexpr (t < C::RD)
+                    read_slot(std::integral_constant<int, t>{}, a_cur, w_cur, ch1, wb1, f1);
+                // first half of the next stage -> f0, after the barrier
+                if constexpr (t >= C::T0 && t < C::T0 + C::RD)
+                    read_slot(std::integral_constant<int, t - C::T0>{}, a_nxt, w_nxt, ch0, wb0, f0);
+            }
             // DMA: the tail of the sequence started at the previous barrier,
             // then the head of this stage's
             static_for<C::NDMA>([&](auto qc) {
