@@ -227,6 +227,24 @@ def test_w8a8_decode_gemv_full_size(dev, hip, m, k, n):
     assert np.array_equal(acc2, acc) and np.array_equal(y2, y)
 
 
+@pytest.mark.parametrize("m,k,n", [(2, 4096, 100), (3, 8192, 37), (4, 4096, 16), (5, 4096, 50),
+                                   (7, 8192, 200), (16, 12288, 33), (1, 12288, 4)])
+def test_w8a8_gemv_whole_line_variants(dev, hip, m, k, n):
+    """The whole-line GEMV (K % 4096 == 0): the LDS-staged activation path
+    (M <= 4) and the direct one (M > 4) with rows past M zeroed, ragged N,
+    several 1 KiB K chunks per wave (K = 8192, 12288), bias + ReLU, and the
+    accumulator-only output (no scales) -- int32 and fp32 bit-exact against
+    the oracle."""
+    aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=7 * m + n, outliers=0.01)
+    ye, acce = O.w8a8_linear(aq, sa, wq, sw, bias, True)
+    d = [to_dev(a, dev) for a in (aq, sa, wq, sw, bias)]
+    y, acc = hip.w8a8_linear(*d, relu=True, want_acc=True)
+    assert np.array_equal(host(acc), acce)
+    assert_f32_equal(host(y), ye)
+    _, acc2 = hip.w8a8_linear(d[0], None, d[2], None, None, want_y=False, want_acc=True)
+    assert np.array_equal(host(acc2), acce)
+
+
 def test_w8a8_prefill_full_size_sampled_rows(dev, hip):
     """BASELINE prefill config (2048 x 4096 x 14336): every output of 24
     sampled rows (covering all 16 row tiles) against the oracle, plus the
