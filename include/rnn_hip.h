@@ -172,6 +172,28 @@ int rnn_rotorquant_dequantize(const int8_t *codes, const float *scales,
                               int64_t rows, int64_t dim, const float *rotors,
                               float *y, void *stream);
 
+/* --------------------------------------------- f32 GEMM (BlasBackend) */
+
+/* C = alpha*op(A)*op(B) + beta*C, row-major with leading dimensions (row
+ * strides, in elements):
+ *   op(A) [m,k]: transa = 0 -> A stored [m,k], lda >= k;
+ *                transa = 1 -> A stored [k,m], lda >= m;
+ *   op(B) [k,n]: transb = 0 -> B stored [k,n], ldb >= n;
+ *                transb = 1 -> B stored [n,k], ldb >= k;
+ *   C [m,n], ldc >= n, read (unless beta == 0) and written in place.
+ * beta == 0 overwrites C without reading it (NaNs in C do not propagate);
+ * k == 0 or alpha == 0 gives C = beta*C; m == 0 or n == 0 is a no-op.
+ * Replaces BlasBackend::sgemm and blas::sgemm (src/blas.rs:712-734, contract
+ * :89-190, scale_c :191-207). Exception to the header's numeric rule: products
+ * are accumulated with fused multiply-adds (MFMA) in an order of the kernel's
+ * choosing, so results agree with the reference within the usual GEMM
+ * rounding bound (|err| <= ~k * 2^-24 * (|alpha| |A||B| + |beta C|)), not bit
+ * for bit -- as the reference's own blocked and small-matrix paths do with
+ * each other. */
+int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k,
+              float alpha, const float *a, int64_t lda, const float *b,
+              int64_t ldb, float beta, float *c, int64_t ldc, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

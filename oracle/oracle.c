@@ -583,3 +583,30 @@ void orc_rotorquant_rotors_from_seed(uint64_t seed, size_t n_groups, float *roto
         r[3] = mag * uc;
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* src/blas.rs:104-264 (sgemm contract, gemm_small order)              */
+/* ------------------------------------------------------------------ */
+void orc_sgemm(int transa, int transb, size_t m, size_t n, size_t k, float alpha,
+               const float *a, size_t lda, const float *b, size_t ldb, float beta,
+               float *c, size_t ldc) {
+    if (m == 0 || n == 0) return;
+    for (size_t i = 0; i < m; ++i) {
+        float *crow = c + i * ldc;
+        if (beta == 0.0f) {
+            for (size_t j = 0; j < n; ++j) crow[j] = 0.0f;
+        } else if (beta != 1.0f) {
+            for (size_t j = 0; j < n; ++j) crow[j] *= beta;
+        }
+        if (k == 0 || alpha == 0.0f) continue;
+        for (size_t p = 0; p < k; ++p) {
+            const float av = transa ? a[p * lda + i] : a[i * lda + p];
+            if (av == 0.0f) continue;
+            const float aav = alpha * av;
+            for (size_t j = 0; j < n; ++j) {
+                const float bv = transb ? b[j * ldb + p] : b[p * ldb + j];
+                crow[j] += aav * bv;
+            }
+        }
+    }
+}

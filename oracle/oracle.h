@@ -155,6 +155,19 @@ void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream,
 void orc_chacha20_block_ietf(const uint32_t key[8], uint32_t counter,
                              const uint32_t nonce[3], uint32_t out[16]);
 
+/* ---- f32 GEMM (BlasBackend contract) ---- */
+
+/* src/blas.rs:104-190 (sgemm contract, scale_c :191-207) with the small-matrix
+ * order of gemm_small (:214-264): per row i, C row *= beta (zeroed for beta
+ * == 0), then for p in k order, skipping op(A)[i][p] == 0,
+ * C[i][j] += (alpha*op(A)[i][p]) * op(B)[p][j], each product and sum rounded
+ * separately. k == 0 or alpha == 0 gives C = beta*C. The reference's blocked
+ * path (m*n*k >= 4096) sums in another order, so its results differ from this
+ * one by rounding only. transa/transb: 0 = as stored, 1 = transposed. */
+void orc_sgemm(int transa, int transb, size_t m, size_t n, size_t k, float alpha,
+               const float *a, size_t lda, const float *b, size_t ldb, float beta,
+               float *c, size_t ldc);
+
 #ifdef __cplusplus
 }
 #endif

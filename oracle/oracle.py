@@ -58,6 +58,8 @@ def lib():
             "orc_rotorquant_rotors_from_seed": [ctypes.c_uint64, _SZ, _P],
             "orc_chacha_block": [_P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _P],
             "orc_chacha20_block_ietf": [_P, ctypes.c_uint32, _P, _P],
+            "orc_sgemm": [ctypes.c_int, ctypes.c_int, _SZ, _SZ, _SZ, ctypes.c_float, _P, _SZ, _P, _SZ,
+                          ctypes.c_float, _P, _SZ],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -274,3 +276,68 @@ def chacha20_block_ietf(key_words, counter, nonce_words):
     out = np.empty(16, np.uint32)
     lib().orc_chacha20_block_ietf(_ptr(k), counter, _ptr(nn), _ptr(out))
     return out
+
+
+# ---------------------------------------------------------------- f32 GEMM
+def sgemm(transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc):
+    """src/blas.rs:104-264 (gemm_small order): returns the updated copy of c
+    (flat f32 storage with row stride ldc)."""
+    a = _c(a, np.float32).ravel()
+    b = _c(b, np.float32).ravel()
+    out = _c(c, np.float32).ravel().copy()
+    lib().orc_sgemm(int(transa), int(transb), m, n, k, float(alpha), _ptr(a), lda, _ptr(b), ldb,
+                    float(beta), _ptr(out), ldc)
+    return out
+
+
+def blas_rand_mat(seed: int, n: int):
+    """The reference's sgemm test generator (src/blas.rs tests, rand_mat):
+    s = s*1664525 + 1013904223 (mod 2^32), value = (s >> 8) / 2^24 - 0.5.
+    Returns (values f32 [n], next seed)."""
+    out = np.empty(n, np.float32)
+    s = seed & 0xFFFFFFFF
+    for i in range(n):
+        s = (s * 1664525 + 1013904223) & 0xFFFFFFFF
+        out[i] = np.float32(np.float32(s >> 8) / np.float32(16777216.0)) - np.float32(0.5)
+    return out, s
+
+
+# (name, transa, transb, m, n, k, seed, alpha, beta, tolerance of the reference's test)
+# from the reference's sgemm tests (src/blas.rs:1195-1512)
+BLAS_TEST_CASES = [
+    ("nn", 0, 0, 17, 19, 13, 1, 1.0, 0.0, 1e-3),
+    ("nt", 0, 1, 33, 29, 17, 2, 1.0, 0.0, 1e-3),
+    ("tn", 1, 0, 29, 33, 17, 3, 1.0, 0.0, 1e-3),
+    ("tt", 1, 1, 40, 35, 24, 4, 1.0, 0.0, 1e-3),
+    ("alpha_beta", 0, 0, 20, 20, 20, 5, 2.5, -1.5, 1e-3),
+    ("large_blocked", 0, 0, 200, 180, 160, 6, 1.0, 0.0, 0.1),
+]
+
+
+def blas_test_case(transa, transb, m, n, k, seed, beta):
+    """Operands of one BLAS_TEST_CASES entry, drawn in the reference's order
+    (A, then B, then C when beta != 0) with its storage shapes and leading
+    dimensions. Returns (a, lda, b, ldb, c0)."""
+    a, s = blas_rand_mat(seed, m * k)
+    b, s = blas_rand_mat(s, k * n)
+    c0 = blas_rand_mat(s, m * n)[0] if beta != 0.0 else np.zeros(m * n, np.float32)
+    lda = m if transa else k
+    ldb = k if transb else n
+    return a, lda, b, ldb, c0
+
+
+def sgemm_f64(transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc):
+    """The exact value in float64 and the rounding scale
+    |alpha| * (|op(A)| |op(B)|) + |beta C|, both [m, n]."""
+    def op(x, ld, rows, cols, trans):
+        # the logical [rows, cols] operand of storage x with row stride ld
+        x = np.asarray(x, np.float64).ravel()
+        if trans:  # stored [cols, rows]
+            return np.lib.stride_tricks.as_strided(x, shape=(cols, rows), strides=(ld * 8, 8)).T
+        return np.lib.stride_tricks.as_strided(x, shape=(rows, cols), strides=(ld * 8, 8))
+    A = op(a, lda, m, k, transa)
+    B = op(b, ldb, k, n, transb)
+    C = np.lib.stride_tricks.as_strided(np.asarray(c, np.float64).ravel(), shape=(m, n), strides=(ldc * 8, 8))
+    exact = alpha * (A @ B) + (beta * C if beta != 0.0 else 0.0)
+    scale = abs(alpha) * (np.abs(A) @ np.abs(B)) + (abs(beta) * np.abs(C) if beta != 0.0 else 0.0)
+    return exact, scale

@@ -1,0 +1,262 @@
+// sgemm.hip -- f32 GEMM for the BlasBackend plugin point of rust-nn
+// (src/blas.rs:712-734, contract at :89-190): C = alpha*op(A)*op(B) + beta*C,
+// row-major storage with leading dimensions, op = identity or transpose.
+//
+// Fast path: v_mfma_f32_16x16x4f32 on 128x128 block tiles of 4 waves (64x64
+// each), K staged 32 floats at a time through double-buffered LDS:
+//  * K-contiguous operands (A as stored, B transposed) are kept as 128-byte
+//    LDS rows (32 floats) whose 16-byte chunks are XOR-swizzled by
+//    (row >> 1) & 7. A lane reads one 16-byte chunk = 4 consecutive k and
+//    feeds them to 4 successive MFMAs: MFMA s of a 16-k super-step uses, in
+//    lane group q = lane/16, the k index 16*ss + 4*q + s. Both operands use the
+//    same k mapping, so the sum is the same as in k order up to rounding.
+//  * K-major operands (A transposed, B as stored) are kept as [k][row] tiles
+//    with a 132-float row pitch (the four lane groups' rows 4 apart land 16
+//    banks apart) and read 4 bytes per lane per MFMA.
+// The MFMA's A operand is the op(B) fragment (16 columns n), its B operand
+// the op(A) fragment (16 rows m), so a lane ends up with 4 consecutive n of
+// one m and writes them as one float4.
+// Other strides / alignments take a one-thread-per-output kernel.
+#include "common.hpp"
+
+namespace rnn {
+
+namespace {
+
+constexpr int kSgBM = 128, kSgBN = 128, kSgBK = 32;
+constexpr int kSgPitch = 132;                            // K-major tile row pitch (floats)
+constexpr int kSgRowTile = kSgBM * kSgBK;                 // 4096 floats (16 KiB)
+constexpr int kSgKTile = kSgBK * kSgPitch;                // 4224 floats (16.5 KiB)
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int sg_swz(int r) { return (r >> 1) & 7; }
+
+// One operand's tile of a stage: ROWS x 32 k (K-contiguous storage, KMAJ =
+// false) or 32 k x ROWS (K-major storage, KMAJ = true). Each of the 256
+// threads moves 4 float4 per stage.
+template <bool KMAJ>
+struct SgOperand {
+    static constexpr int TILE = KMAJ ? kSgKTile : kSgRowTile;
+    const float *p;
+    int64_t ld, rows, K;  // rows: M for A, N for B
+    int64_t r0;           // first row (m or n) of this block
+    f4 reg[4];
+
+    __device__ __forceinline__ void load(int64_t k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 256 * i;
+            int64_t r, k;
+            if (KMAJ) {          // k row f/32, 4 rows starting at 4*(f%32)
+                k = k0 + (f >> 5);
+                r = r0 + 4 * (f & 31);
+            } else {             // row f/8, k chunk f%8
+                r = r0 + (f >> 3);
+                k = k0 + 4 * (f & 7);
+            }
+            // the host guarantees that the contiguous dimension is a multiple
+            // of 4, so a float4 is either wholly inside or wholly outside
+            const bool ok = r < rows && k < K;
+            const float *src = KMAJ ? p + k * ld + r : p + r * ld + k;
+            reg[i] = ok ? *reinterpret_cast<const f4 *>(src) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    __device__ __forceinline__ void store(float *lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = tid + 256 * i;
+            float *dst;
+            if (KMAJ)
+                dst = lds + (f >> 5) * kSgPitch + 4 * (f & 31);
+            else {
+                const int r = f >> 3;
+                dst = lds + r * kSgBK + 4 * ((f & 7) ^ sg_swz(r));
+            }
+            *reinterpret_cast<f4 *>(dst) = reg[i];
+        }
+    }
+    // the 4 k values of super-step ss for fragment row `row` (tile-relative)
+    // in lane group q: k = 16*ss + 4*q + s, s = 0..3
+    __device__ __forceinline__ static f4 frag(const float *lds, int row, int q, int ss) {
+        if (KMAJ) {
+            const float *b = lds + (16 * ss + 4 * q) * kSgPitch + row;
+            return f4{b[0], b[kSgPitch], b[2 * kSgPitch], b[3 * kSgPitch]};
+        } else {
+            return *reinterpret_cast<const f4 *>(lds + row * kSgBK + 4 * ((4 * ss + q) ^ sg_swz(row)));
+        }
+    }
+};
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void sgemm_mfma_kernel(const float *__restrict__ A, int64_t lda,
+                                                         const float *__restrict__ B, int64_t ldb,
+                                                         float *__restrict__ C, int64_t ldc,
+                                                         int64_t M, int64_t N, int64_t K,
+                                                         float alpha, float beta, int tiles_m) {
+    using OA = SgOperand<TA>;    // op(A) rows m: K-major when A is transposed
+    using OB = SgOperand<!TB>;   // op(B) rows n: K-major when B is as stored ([k][n])
+    __shared__ __attribute__((aligned(16))) float smem[2 * (OA::TILE + OB::TILE)];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid & 1, wn = wid >> 1;
+    const int fr = lane & 15, q = lane >> 4;
+    const int tm = (int)blockIdx.x % tiles_m, tn = (int)blockIdx.x / tiles_m;
+    const int64_t m0 = (int64_t)tm * kSgBM, n0 = (int64_t)tn * kSgBN;
+
+    OA a{A, lda, M, K, m0, {}};
+    OB b{B, ldb, N, K, n0, {}};
+    f4 acc[4][4];  // [n tile][m tile]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int nst = (int)((K + kSgBK - 1) / kSgBK);
+    a.load(0, tid);
+    b.load(0, tid);
+    a.store(smem, tid);
+    b.store(smem + OA::TILE, tid);
+    __syncthreads();
+    for (int s = 0; s < nst; ++s) {
+        float *cur = smem + (s & 1) * (OA::TILE + OB::TILE);
+        float *nxt = smem + ((s + 1) & 1) * (OA::TILE + OB::TILE);
+        if (s + 1 < nst) {  // next stage's loads in flight during this stage's MFMAs
+            a.load((int64_t)(s + 1) * kSgBK, tid);
+            b.load((int64_t)(s + 1) * kSgBK, tid);
+        }
+#pragma unroll
+        for (int ss = 0; ss < kSgBK / 16; ++ss) {
+            f4 fa[4], fb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fa[j] = OA::frag(cur, wm * 64 + 16 * j + fr, q, ss);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fb[i] = OB::frag(cur + OA::TILE, wn * 64 + 16 * i + fr, q, ss);
+#pragma unroll
+            for (int k4 = 0; k4 < 4; ++k4)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[i][k4], fa[j][k4], acc[i][j], 0, 0, 0);
+        }
+        if (s + 1 < nst) {
+            a.store(nxt, tid);
+            b.store(nxt + OA::TILE, tid);
+        }
+        __syncthreads();
+    }
+
+    // lane: m = tile row + fr, n = tile column + 4*q + e (e = 0..3)
+    const bool vec_c = (ldc & 3) == 0 && (((uintptr_t)C) & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t m = m0 + wm * 64 + 16 * j + fr;
+            const int64_t n = n0 + wn * 64 + 16 * i + 4 * q;
+            if (m >= M || n >= N) continue;
+            float *cp = C + m * ldc + n;
+            f4 v = acc[i][j];
+            if (vec_c && n + 3 < N) {
+                f4 o = {alpha * v.x, alpha * v.y, alpha * v.z, alpha * v.w};
+                if (beta != 0.0f) {
+                    const f4 c = *reinterpret_cast<const f4 *>(cp);
+                    o = f4{o.x + beta * c.x, o.y + beta * c.y, o.z + beta * c.z, o.w + beta * c.w};
+                }
+                *reinterpret_cast<f4 *>(cp) = o;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (n + e >= N) break;
+                    const float o = alpha * v[e];
+                    cp[e] = beta != 0.0f ? o + beta * cp[e] : o;
+                }
+            }
+        }
+}
+
+// Any strides: one thread per output, k in order with fused multiply-adds.
+__global__ void sgemm_simple_kernel(int transa, int transb, const float *__restrict__ A, int64_t lda,
+                                    const float *__restrict__ B, int64_t ldb, float *__restrict__ C,
+                                    int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha,
+                                    float beta) {
+    const int64_t total = M * N;
+    for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = idx / N, n = idx % N;
+        float s = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            const float av = transa ? A[k * lda + m] : A[m * lda + k];
+            const float bv = transb ? B[n * ldb + k] : B[k * ldb + n];
+            s = fmaf(av, bv, s);
+        }
+        float *cp = C + m * ldc + n;
+        *cp = beta != 0.0f ? alpha * s + beta * *cp : alpha * s;
+    }
+}
+
+// C = beta*C (beta == 0: zeros, C is not read), for k == 0 or alpha == 0
+// (src/blas.rs:137-141, scale_c :191-207).
+__global__ void sgemm_scale_kernel(float *__restrict__ C, int64_t ldc, int64_t M, int64_t N,
+                                   float beta) {
+    const int64_t total = M * N;
+    for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        float *cp = C + (idx / N) * ldc + idx % N;
+        *cp = beta == 0.0f ? 0.0f : beta * *cp;
+    }
+}
+
+bool aligned16f(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+}  // namespace rnn
+
+using namespace rnn;
+
+extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k, float alpha,
+                         const float *a, int64_t lda, const float *b, int64_t ldb, float beta,
+                         float *c, int64_t ldc, void *stream) {
+    const char *name = "rnn_sgemm";
+    RNN_REQUIRE(m >= 0 && n >= 0 && k >= 0, "%s: negative size", name);
+    RNN_REQUIRE((transa == 0 || transa == 1) && (transb == 0 || transb == 1),
+                "%s: transa/transb must be 0 (as stored) or 1 (transposed)", name);
+    if (m == 0 || n == 0) return RNN_OK;
+    RNN_REQUIRE(c != nullptr, "%s: null C", name);
+    // leading dimensions: the row strides of the stored matrices (src/blas.rs:93-101)
+    RNN_REQUIRE(ldc >= n, "%s: ldc (%lld) < n (%lld)", name, (long long)ldc, (long long)n);
+    hipStream_t st = as_stream(stream);
+    const int cus = device_cu_count();
+    if (k == 0 || alpha == 0.0f) {
+        const int64_t blocks = std::min<int64_t>(ceil_div(m * n, 256), 8 * cus);
+        sgemm_scale_kernel<<<(unsigned)blocks, 256, 0, st>>>(c, ldc, m, n, beta);
+        return check_launch(name);
+    }
+    RNN_REQUIRE(a != nullptr && b != nullptr, "%s: null operand", name);
+    RNN_REQUIRE(lda >= (transa ? m : k), "%s: lda (%lld) < %s (%lld)", name, (long long)lda,
+                transa ? "m" : "k", (long long)(transa ? m : k));
+    RNN_REQUIRE(ldb >= (transb ? k : n), "%s: ldb (%lld) < %s (%lld)", name, (long long)ldb,
+                transb ? "k" : "n", (long long)(transb ? k : n));
+    // The MFMA path moves float4 along each operand's contiguous dimension.
+    const bool fast = (lda & 3) == 0 && (ldb & 3) == 0 && aligned16f(a) && aligned16f(b) &&
+                      (transa ? m % 4 == 0 : k % 4 == 0) && (transb ? k % 4 == 0 : n % 4 == 0);
+    if (!fast) {
+        const int64_t blocks = std::min<int64_t>(ceil_div(m * n, 256), 8 * cus);
+        sgemm_simple_kernel<<<(unsigned)blocks, 256, 0, st>>>(transa, transb, a, lda, b, ldb, c, ldc,
+                                                              m, n, k, alpha, beta);
+        return check_launch(name);
+    }
+    const int64_t tm = ceil_div(m, kSgBM), tn = ceil_div(n, kSgBN);
+    RNN_REQUIRE(tm * tn <= 0x7fffffffLL && tm < 0x7fffffffLL, "%s: too many tiles", name);
+    const unsigned grid = (unsigned)(tm * tn);
+    if (!transa && !transb)
+        sgemm_mfma_kernel<false, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+    else if (!transa && transb)
+        sgemm_mfma_kernel<false, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+    else if (transa && !transb)
+        sgemm_mfma_kernel<true, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+    else
+        sgemm_mfma_kernel<true, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+    return check_launch(name);
+}

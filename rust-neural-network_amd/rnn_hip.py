@@ -30,6 +30,10 @@ ALGO_TILED_DMA = 0x30
 TERNARY_ROWS = 0
 TERNARY_ABSMEAN = 1
 
+# blas::Transpose (src/blas.rs:72-77)
+NO_TRANS = 0
+TRANS = 1
+
 
 class RnnError(RuntimeError):
     def __init__(self, status: int, msg: str):
@@ -62,6 +66,8 @@ SIGNATURES = {
     "rnn_rotor_rotation_matrices": ([_P, _I64, _P, _P], _INT),
     "rnn_rotorquant_quantize": ([_P, _I64, _I64, _INT, _P, _P, _P, _P, _P], _INT),
     "rnn_rotorquant_dequantize": ([_P, _P, _I64, _I64, _P, _P, _P], _INT),
+    "rnn_sgemm": ([_INT, _INT, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P, _I64,
+                   ctypes.c_float, _P, _I64, _P], _INT),
 }
 
 _lib = None
@@ -303,3 +309,38 @@ def rotorquant_dequantize(codes, scales, dim, rotors, stream=None):
     _check(load().rnn_rotorquant_dequantize(_ptr(codes), _ptr(scales), rows, dim, _ptr(rotors),
                                             _ptr(y), _stream(stream)))
     return y
+
+
+# ------------------------------------------------------------------ f32 GEMM
+def sgemm(transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc, stream=None):
+    """blas::sgemm / BlasBackend::sgemm (src/blas.rs:104-118, :712-734):
+    C = alpha*op(A)*op(B) + beta*C on device storage `a`, `b`, `c` (f32
+    tensors holding the row-major matrices with row strides lda/ldb/ldc).
+    `transa`/`transb` are NO_TRANS or TRANS. C is updated in place."""
+    import torch
+    for t, nm in ((a, "a"), (b, "b"), (c, "c")):
+        _dev(t, torch.float32, nm)
+    _check(load().rnn_sgemm(int(transa), int(transb), m, n, k, float(alpha), _ptr(a), lda,
+                            _ptr(b), ldb, float(beta), _ptr(c), ldc, _stream(stream)))
+    return c
+
+
+def matmul(a, b, stream=None):
+    """blas::matmul (src/blas.rs:780-799): C = A.B for contiguous [m,k] @ [k,n]."""
+    import torch
+    _dev(a, torch.float32, "a"), _dev(b, torch.float32, "b")
+    m, k = a.shape
+    n = b.shape[1]
+    c = _empty((m, n), torch.float32, a)
+    return sgemm(NO_TRANS, NO_TRANS, m, n, k, 1.0, a, k, b, n, 0.0, c, n, stream)
+
+
+class HipBackend:
+    """The BlasBackend trait (src/blas.rs:712-734) on the GPU: name() and
+    sgemm() with the trait's argument order, operands on the device."""
+
+    def name(self) -> str:
+        return "hip-gfx950 (v_mfma_f32_16x16x4f32, 128x128 tiles)"
+
+    def sgemm(self, transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc):
+        return sgemm(transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc)

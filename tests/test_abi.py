@@ -68,6 +68,24 @@ def test_gemm_argument_rules(lib):
             H.RNN_ERR_UNSUPPORTED, "multiple of 16")
 
 
+def test_sgemm_argument_rules(lib):
+    """rnn_sgemm (BlasBackend::sgemm): the leading-dimension rules of the
+    reference's contract (src/blas.rs:93-101) and the transpose flags."""
+    def call(ta=0, tb=0, m=4, n=4, k=4, alpha=1.0, lda=4, ldb=4, ldc=4, c=FAKE):
+        return lib.rnn_sgemm(ta, tb, m, n, k, alpha, FAKE, lda, FAKE, ldb, 0.0, c, ldc, None)
+    _status(call(m=-1), H.RNN_ERR_INVALID_ARG, "negative")
+    _status(call(ta=2), H.RNN_ERR_INVALID_ARG, "transa/transb")
+    _status(call(ldc=3), H.RNN_ERR_INVALID_ARG, "ldc")
+    _status(call(c=None), H.RNN_ERR_INVALID_ARG, "null C")
+    _status(call(k=8, lda=7), H.RNN_ERR_INVALID_ARG, "lda")           # A [m,k]: lda >= k
+    _status(call(ta=1, m=8, lda=7, ldc=8), H.RNN_ERR_INVALID_ARG, "lda")  # A [k,m]: lda >= m
+    _status(call(n=8, ldb=7, ldc=8), H.RNN_ERR_INVALID_ARG, "ldb")    # B [k,n]: ldb >= n
+    _status(call(tb=1, k=8, lda=8, ldb=7), H.RNN_ERR_INVALID_ARG, "ldb")  # B [n,k]: ldb >= k
+    # m == 0 or n == 0 is a no-op, with no pointer needed
+    assert lib.rnn_sgemm(0, 0, 0, 4, 4, 1.0, None, 4, None, 4, 0.0, None, 4, None) == 0
+    assert lib.rnn_sgemm(0, 0, 4, 0, 4, 1.0, None, 4, None, 4, 0.0, None, 4, None) == 0
+
+
 def test_empty_shapes_are_noops(lib):
     assert lib.rnn_w8a8_linear(None, None, None, None, None, 0, 16, 4, 0, None, None, None) == 0
     assert lib.rnn_quant_rows_i8(None, 0, 5, None, None, None) == 0

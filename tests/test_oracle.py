@@ -421,3 +421,53 @@ def test_rotors_from_seed_are_unit_rotors():
     r = O.rotors_from_seed(0xC11FC0DE, 43)
     assert np.abs((r.astype(np.float64) ** 2).sum(axis=1) - 1).max() < 1e-5
     assert np.array_equal(r, O.rotors_from_seed(0xC11FC0DE, 43))
+
+
+# ------------------------------------------------------------------ f32 GEMM
+def _sgemm_bound(k, scale):
+    # |computed - exact| <= gamma_(k+2) * (|alpha| |A||B| + |beta C|), gamma_j = j u / (1 - j u)
+    u = 2.0 ** -24
+    return (k + 2) * u / (1 - (k + 2) * u) * scale + 1e-30
+
+
+def test_blas_rand_mat_matches_reference_recurrence():
+    # s = 1: first draws of the reference's rand_mat (src/blas.rs tests)
+    v, s = O.blas_rand_mat(1, 3)
+    seq, t = [], 1
+    for _ in range(3):
+        t = (t * 1664525 + 1013904223) % 2 ** 32
+        seq.append((t >> 8) / 2 ** 24 - 0.5)
+    assert np.array_equal(v, np.array(seq, np.float32)) and s == t
+
+
+@pytest.mark.parametrize("case", O.BLAS_TEST_CASES, ids=[c[0] for c in O.BLAS_TEST_CASES])
+def test_sgemm_reference_cases(case):
+    """The reference's sgemm tests (src/blas.rs:1195-1470): same generator,
+    shapes, strides, alpha/beta; within the reference's tolerance and within
+    the k-term rounding bound of the float64 product."""
+    _, ta, tb, m, n, k, seed, alpha, beta, tol = case
+    a, lda, b, ldb, c0 = O.blas_test_case(ta, tb, m, n, k, seed, beta)
+    c = O.sgemm(ta, tb, m, n, k, alpha, a, lda, b, ldb, beta, c0, n).reshape(m, n)
+    exact, scale = O.sgemm_f64(ta, tb, m, n, k, alpha, a, lda, b, ldb, beta, c0, n)
+    err = np.abs(c - exact)
+    assert err.max() < tol
+    assert np.all(err <= _sgemm_bound(k, scale))
+
+
+def test_sgemm_known_answers_and_edges():
+    # matmul_convenience_works (src/blas.rs:1514-1520)
+    c = O.sgemm(0, 0, 2, 2, 2, 1.0, [1, 2, 3, 4], 2, [5, 6, 7, 8], 2, 0.0, np.zeros(4), 2)
+    assert c.tolist() == [19.0, 22.0, 43.0, 50.0]
+    # sgemm_zero_and_small_edges (:1471-1512): k = 0 with beta = 0 zeroes C; 1x1
+    assert O.sgemm(0, 0, 2, 2, 0, 1.0, [0], 0, [0], 0, 0.0, np.full(4, 7.0), 2).tolist() == [0.0] * 4
+    assert O.sgemm(0, 0, 1, 1, 1, 1.0, [3.0], 1, [4.0], 1, 0.0, [0.0], 1).tolist() == [12.0]
+    # beta = 0 overwrites NaN; alpha = 0 gives beta*C; beta = 1 keeps C
+    nanc = np.full(4, np.nan, np.float32)
+    assert O.sgemm(0, 0, 2, 2, 1, 1.0, [1, 1], 1, [1, 1], 2, 0.0, nanc, 2).tolist() == [1.0] * 4
+    assert O.sgemm(0, 0, 2, 2, 3, 0.0, np.ones(6), 3, np.ones(6), 2, 2.0,
+                   np.arange(4.0), 2).tolist() == [0.0, 2.0, 4.0, 6.0]
+    # leading dimensions beyond the logical sizes: padding is read as nothing
+    # and left untouched in C
+    a = np.array([1, 2, 99, 3, 4, 99], np.float32)           # [2,2], lda 3
+    c = O.sgemm(0, 0, 2, 2, 2, 1.0, a, 3, [5, 6, 7, 8], 2, 0.0, np.full(6, -1.0), 3)
+    assert c.tolist() == [19.0, 22.0, -1.0, 43.0, 50.0, -1.0]
