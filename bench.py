@@ -6,7 +6,8 @@ TOPS (2*M*N*K int ops per step). The same JSON line carries the roofline of that
 kernel, the CPU baseline (the oracle's AVX-512 VNNI igemm path over the whole
 workload) and the other configurations as `components`: decode GEMV (GB/s, weight
 buffers rotated past the 256 MB MALL), ternary GEMM (TOPS; both timed by HIP-graph
-replay) and the RotorQuant K+V round trip (GB/s).
+replay), the RotorQuant K+V round trip (GB/s) and the f32 BlasBackend GEMM
+(TFLOP/s, beside torch.matmul's library GEMM on the same operands).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
 """
@@ -27,6 +28,7 @@ for _p in (os.path.join(ROOT, "rust-neural-network_amd"), os.path.join(ROOT, "or
 METRIC = "W8A8 GEMM TOPS (% int8 MFMA peak); GEMV & RotorQuant GB/s (% HBM peak)"
 PEAK_INT8_TOPS = 5033.0   # MI355X dense int8 MFMA (datasheet, no sparsity)
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -203,6 +205,35 @@ def bench_rotorquant(H, W, dev, steps):
             "launches_per_step": 2}
 
 
+# ---------------------------------------------------------------- f32 GEMM
+SGEMM_MNK = (4096, 4096, 4096)
+
+
+def bench_sgemm(H, dev, steps):
+    """rnn_sgemm (the BlasBackend::sgemm plugin point) on a 4096^3 f32
+    product, C = A*B with both operands as stored (no transpose), beside
+    torch.matmul (the ROCm library GEMM, TF32 off) on the same operands."""
+    import torch
+    m, n, k = SGEMM_MNK
+    a = gen_f32((m, k), 21, dev)
+    b = gen_f32((k, n), 22, dev)
+    c = torch.empty((m, n), dtype=torch.float32, device=dev)
+    n_iter = max(steps // 4, 20)
+    ms = timed(lambda: H.sgemm(H.NO_TRANS, H.NO_TRANS, m, n, k, 1.0, a, k, b, n, 0.0, c, n), n_iter, 10)
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        ms_lib = timed(lambda: torch.matmul(a, b, out=c), n_iter, 10)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    flops = 2.0 * m * n * k
+    tflops, tflops_lib = flops / (ms * 1e-3) / 1e12, flops / (ms_lib * 1e-3) / 1e12
+    return {"m": m, "n": n, "k": k, "trans": "nn", "us": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
+            "frac_fp32_mfma_peak": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+            "torch_matmul_TFLOP/s": round(tflops_lib, 1), "traffic": traffic_for("f32_sgemm"),
+            "kernel": "sgemm_mfma_kernel<false,false> (v_mfma_f32_16x16x4f32, 128x128 tiles)"}
+
+
 # ---------------------------------------------------------------- copy ceiling
 COPY_BYTES = 512 * 2**20
 
@@ -269,7 +300,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--only", default="all",
-                    choices=["all", "prefill", "gemv", "ternary", "rotorquant", "copy"])
+                    choices=["all", "prefill", "gemv", "ternary", "rotorquant", "sgemm", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -323,6 +354,9 @@ def main():
     if args.only in ("all", "rotorquant"):
         log("RotorQuant K+V [8,32,4096,128] 4-bit round trip")
         components["rotorquant_kv"] = bench_rotorquant(H, W, dev, args.steps)
+    if args.only in ("all", "sgemm"):
+        log("f32 GEMM 4096x4096x4096 (BlasBackend::sgemm)")
+        components["f32_sgemm"] = bench_sgemm(H, dev, args.steps)
     if args.only in ("all", "copy"):
         log("streaming copy ceiling: 512 MiB device-to-device")
         components["copy_ceiling"] = bench_copy(dev, args.steps)
