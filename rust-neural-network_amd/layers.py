@@ -1,0 +1,240 @@
+"""Layer-level mirrors of rust-nn's quantized inference types over the HIP
+library: `Int8Weights` / `Int8Linear` (src/int8.rs:11-172), `TernaryTensor` /
+`TernaryLinear` / `TernaryModel` (src/ternary.rs:81-362), and `Int8Model`, the
+int8 counterpart of `TernaryModel::from_model` that the reference does not have.
+
+Every tensor here is a torch device tensor; weights, codes and scales stay in
+HBM for the life of a layer, and a model's forward keeps its activations on the
+device between layers (quantize -> W8A8 GEMM with the ReLU fused -> quantize
+...). Each method names the reference method it mirrors and calls the C ABI
+through `rnn_hip`; nothing here computes on the CPU.
+
+`from_model` takes the flat parameter list of `Module::parameters()` (weights
+`[out, in]`, biases 1-D, in layer order), the reference's input to
+`TernaryModel::from_model`."""
+from __future__ import annotations
+
+import rnn_hip as H
+
+
+def pair_parameters(shapes):
+    """The weight/bias pairing of `TernaryModel::from_model`
+    (src/ternary.rs:291-329): a parameter is a layer's weight, and the next one
+    is its bias when it is 1-D. Returns (weight index, bias index or None)
+    pairs. Pure index logic over the parameter shapes, kept apart so that it
+    can be checked without a GPU."""
+    pairs, i = [], 0
+    while i < len(shapes):
+        b = i + 1 if i + 1 < len(shapes) and len(shapes[i + 1]) == 1 else None
+        pairs.append((i, b))
+        i += 2 if b is not None else 1
+    return pairs
+
+
+def _mean_abs_diff(a, b):
+    # quantization_error (src/int8.rs:102-112, src/ternary.rs:174-184): mean |a - b|
+    return float((a.reshape(-1) - b.reshape(-1)).abs().sum() / max(a.numel(), 1))
+
+
+# ------------------------------------------------------------------ int8
+class Int8Weights:
+    """src/int8.rs:11-18: int8 codes `[out, in]` and one f32 scale per row."""
+
+    def __init__(self, data, scales, shape):
+        self.data, self.scales, self.shape = data, scales, tuple(shape)
+
+    @classmethod
+    def quantize(cls, weight):
+        """Int8Weights::quantize (src/int8.rs:24-52)."""
+        q, s = H.quant_rows_i8(weight)
+        return cls(q, s, weight.shape)
+
+    def dequantize(self):
+        """Int8Weights::dequantize (src/int8.rs:55-65)."""
+        return H.int8_dequantize(self.data, self.scales)
+
+    def matmul_f32(self, activation, m):
+        """Int8Weights::matmul_f32 (src/int8.rs:70-88): activation `[m, in]`."""
+        return H.int8_matmul_f32(self.data, self.scales, activation.reshape(m, self.shape[1]))
+
+    def mem_bytes(self):
+        """src/int8.rs:91-93: int8 codes + f32 scales."""
+        return self.data.numel() + 4 * self.scales.numel()
+
+    def compression_ratio(self):
+        """src/int8.rs:96-99."""
+        return self.data.numel() * 4 / self.mem_bytes()
+
+    def quantization_error(self, original):
+        return _mean_abs_diff(original, self.dequantize())
+
+
+class Int8Linear:
+    """src/int8.rs:117-172. `forward` keeps the reference's semantics (the
+    activation quantized with the weight's row scale inside the output loop);
+    `forward_w8a8` is the per-row dynamic W8A8 path of the benchmark
+    configurations, with the ReLU optionally fused into the epilogue."""
+
+    def __init__(self, int8_weight, bias=None):
+        self.int8_weight, self.bias = int8_weight, bias
+
+    @classmethod
+    def from_linear(cls, weight, bias=None):
+        """Int8Linear::from_linear (src/int8.rs:124-131)."""
+        return cls(Int8Weights.quantize(weight), bias)
+
+    @property
+    def in_features(self):
+        return self.int8_weight.shape[1]
+
+    @property
+    def out_features(self):
+        return self.int8_weight.shape[0]
+
+    def forward(self, x):
+        """Int8Linear::forward (src/int8.rs:134-172): x `[batch, in]`."""
+        return H.int8_linear_forward(x, self.int8_weight.data, self.int8_weight.scales, self.bias)
+
+    def forward_w8a8(self, x, relu=False):
+        """y = (Σ q(x)·W_q · sa[m]) · sw[n] + b[n], ReLU fused when asked."""
+        aq, sa = H.quant_rows_i8(x)
+        y, _ = H.w8a8_linear(aq, sa, self.int8_weight.data, self.int8_weight.scales, self.bias,
+                             relu=relu)
+        return y
+
+
+class Int8Model:
+    """The int8 counterpart of `TernaryModel` (not in the reference): every
+    weight of a parameter list quantized per row, and a device-resident forward
+    that chains the W8A8 layers with the ReLU fused between them (the
+    784-256-128-10 MLP of the benchmark configurations)."""
+
+    def __init__(self, layers):
+        self.layers = list(layers)
+
+    @classmethod
+    def from_model(cls, params):
+        pairs = pair_parameters([tuple(p.shape) for p in params])
+        return cls(Int8Linear.from_linear(params[w], None if b is None else params[b])
+                   for w, b in pairs)
+
+    def forward(self, x, relu_between=True):
+        """W8A8 through every layer; ReLU after each layer but the last."""
+        for i, layer in enumerate(self.layers):
+            x = layer.forward_w8a8(x, relu=relu_between and i + 1 < len(self.layers))
+        return x
+
+    def mem_bytes(self):
+        return sum(l.int8_weight.mem_bytes() + (0 if l.bias is None else 4 * l.bias.numel())
+                   for l in self.layers)
+
+    def compression_ratio(self):
+        return sum(l.int8_weight.data.numel() for l in self.layers) * 4 / max(self.mem_bytes(), 1)
+
+
+# ------------------------------------------------------------------ ternary
+class TernaryTensor:
+    """src/ternary.rs:81-90: 2-bit codes packed 16 per 32-bit word, one f32
+    scale per row, the original shape and element count."""
+
+    def __init__(self, packed, scales, shape):
+        self.packed, self.scales, self.shape = packed, scales, tuple(shape)
+        self.numel = self.shape[0] * self.shape[1]
+
+    @classmethod
+    def quantize(cls, tensor, mode=H.TERNARY_ROWS):
+        """TernaryTensor::quantize (src/ternary.rs:97-137); `mode` =
+        TERNARY_ABSMEAN selects the benchmark configuration's absmean rule."""
+        packed, scales = H.ternary_quantize(tensor, mode)
+        return cls(packed, scales, tensor.shape)
+
+    def dequantize(self):
+        """TernaryTensor::dequantize (src/ternary.rs:140-161)."""
+        return H.ternary_dequantize(self.packed, self.numel, self.scales,
+                                    self.shape[1]).reshape(self.shape)
+
+    def mem_bytes(self):
+        """src/ternary.rs:164-166: packed words + f32 scales."""
+        return 4 * self.packed.numel() + 4 * self.scales.numel()
+
+    def compression_ratio(self):
+        return self.numel * 4 / max(self.mem_bytes(), 1)
+
+    def quantization_error(self, original):
+        return _mean_abs_diff(original, self.dequantize())
+
+    def value_counts(self):
+        """src/ternary.rs:194-200: counts of +1, -1 and 0."""
+        t = H.ternary_unpack(self.packed, self.numel)
+        return int((t == 1).sum()), int((t == -1).sum()), int((t == 0).sum())
+
+    def sparsity(self):
+        """src/ternary.rs:187-191: fraction of exact zeros."""
+        return self.value_counts()[2] / max(self.numel, 1)
+
+
+class TernaryLinear:
+    """src/ternary.rs:209-279. `forward` is the reference's sequential f32
+    sum (bit-exact); `forward_int8` is the benchmark configuration's int8
+    ternary GEMM over per-row quantized activations."""
+
+    def __init__(self, ternary_weight, bias=None):
+        self.ternary_weight, self.bias = ternary_weight, bias
+        self.out_features, self.in_features = ternary_weight.shape
+
+    @classmethod
+    def from_linear(cls, weight, bias=None, mode=H.TERNARY_ROWS):
+        """TernaryLinear::from_linear (src/ternary.rs:218-232)."""
+        return cls(TernaryTensor.quantize(weight, mode), bias)
+
+    def forward(self, x):
+        """TernaryLinear::forward (src/ternary.rs:239-279): x `[batch, in]`."""
+        return H.ternary_linear_forward(x, self.ternary_weight.packed, self.ternary_weight.scales,
+                                        self.out_features, self.bias)
+
+    def forward_int8(self, x, relu=False):
+        aq, sa = H.quant_rows_i8(x)
+        y, _ = H.ternary_gemm(aq, sa, self.ternary_weight.packed, self.ternary_weight.scales,
+                              self.out_features, self.bias, relu=relu)
+        return y
+
+
+class TernaryModel:
+    """src/ternary.rs:285-362."""
+
+    def __init__(self, layers):
+        self.layers = list(layers)
+
+    @classmethod
+    def from_model(cls, params, mode=H.TERNARY_ROWS):
+        """TernaryModel::from_model (src/ternary.rs:291-329)."""
+        pairs = pair_parameters([tuple(p.shape) for p in params])
+        return cls(TernaryLinear.from_linear(params[w], None if b is None else params[b], mode)
+                   for w, b in pairs)
+
+    def mem_bytes(self):
+        """src/ternary.rs:332-337."""
+        return sum(l.ternary_weight.mem_bytes() + (0 if l.bias is None else 4 * l.bias.numel())
+                   for l in self.layers)
+
+    def compression_ratio(self):
+        """src/ternary.rs:340-344."""
+        return sum(l.ternary_weight.numel for l in self.layers) * 4 / max(self.mem_bytes(), 1)
+
+    def avg_sparsity(self):
+        """src/ternary.rs:347-356."""
+        if not self.layers:
+            return 0.0
+        return sum(l.ternary_weight.sparsity() for l in self.layers) / len(self.layers)
+
+    def forward_first_layer(self, x):
+        """src/ternary.rs:359-361."""
+        return self.layers[0].forward(x)
+
+    def forward(self, x, relu_between=True):
+        """The whole stack on the device through the int8 ternary GEMM, ReLU
+        fused after each layer but the last (not in the reference, which only
+        runs the first layer)."""
+        for i, layer in enumerate(self.layers):
+            x = layer.forward_int8(x, relu=relu_between and i + 1 < len(self.layers))
+        return x

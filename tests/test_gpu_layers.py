@@ -1,0 +1,91 @@
+"""GPU parity of the layer mirrors (`layers.py`): Int8Weights / Int8Linear
+(src/int8.rs:11-172), TernaryTensor / TernaryLinear / TernaryModel
+(src/ternary.rs:81-362) and the device-resident Int8Model chain, against the
+oracle on the same inputs (fp32 outputs bit for bit)."""
+import numpy as np
+import pytest
+
+import layers as L
+import oracle as O
+import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def mlp_params(seed0=10):
+    """Module::parameters() of the 784-256-128-10 MLP: weight, bias per layer."""
+    params = []
+    for i, (fi, fo) in enumerate(zip(W.MLP_LAYERS[:-1], W.MLP_LAYERS[1:])):
+        params += [W.weights(fo, fi, seed=seed0 + i), W.weights(1, fo, seed=20 + i)[0]]
+    return params
+
+
+def test_int8_model_chain_matches_oracle(dev):
+    params = mlp_params()
+    model = L.Int8Model.from_model([to_dev(p, dev) for p in params])
+    assert len(model.layers) == 3
+    x = W.activations(W.MLP_BATCH, W.MLP_LAYERS[0], seed=1)
+    got = host(model.forward(to_dev(x, dev)))
+    h = x
+    for i in range(3):
+        wq, sw = O.quant_rows_i8(params[2 * i])
+        aq, sa = O.quant_rows_i8(h)
+        h, _ = O.w8a8_linear(aq, sa, wq, sw, params[2 * i + 1], i < 2)
+    np.testing.assert_array_equal(got, h)
+    # mem_bytes: int8 codes + f32 row scales + f32 biases (src/int8.rs:91-93)
+    n_w = sum(p.size for p in params[0::2])
+    rows = sum(p.shape[0] for p in params[0::2])
+    assert model.mem_bytes() == n_w + 4 * rows + 4 * sum(p.size for p in params[1::2])
+
+
+def test_int8_linear_reference_forward_and_weights(dev):
+    w = W.weights(48, 80, seed=3)
+    b = W.weights(1, 48, seed=4)[0]
+    x = W.activations(6, 80, seed=5)
+    lin = L.Int8Linear.from_linear(to_dev(w, dev), to_dev(b, dev))
+    wq, sw = O.quant_rows_i8(w)
+    np.testing.assert_array_equal(host(lin.int8_weight.data), wq)
+    np.testing.assert_array_equal(host(lin.forward(to_dev(x, dev))), O.int8_linear_forward(x, wq, sw, b))
+    np.testing.assert_array_equal(host(lin.int8_weight.matmul_f32(to_dev(x, dev), 6)),
+                                  O.int8_matmul_f32(wq, sw, x))
+    np.testing.assert_array_equal(host(lin.int8_weight.dequantize()), O.int8_dequantize(wq, sw))
+    assert lin.int8_weight.compression_ratio() == pytest.approx(48 * 80 * 4 / (48 * 80 + 4 * 48))
+
+
+def test_ternary_model_from_model(dev):
+    # a bias-less layer between two biased ones exercises the pairing rule
+    shapes = [(64, 96), (64,), (32, 64), (16, 32), (16,)]
+    params = [W.weights(*s, seed=30 + i) if len(s) == 2 else W.weights(1, s[0], seed=30 + i)[0]
+              for i, s in enumerate(shapes)]
+    model = L.TernaryModel.from_model([to_dev(p, dev) for p in params])
+    assert [l.bias is None for l in model.layers] == [False, True, False]
+    x = W.activations(5, 96, seed=7)
+    t, s = O.ternary_quantize_rows(params[0])
+    packed = O.pack_ternary(t)
+    got = host(model.forward_first_layer(to_dev(x, dev)))
+    np.testing.assert_array_equal(got, O.ternary_linear_f32(x, packed, s, 64, params[1]))
+    first = model.layers[0].ternary_weight
+    pos, neg, zero = first.value_counts()
+    assert (pos, neg, zero) == (int((t == 1).sum()), int((t == -1).sum()), int((t == 0).sum()))
+    assert first.sparsity() == zero / t.size
+    # src/ternary.rs:164-166, 332-337: words + row scales (+ biases)
+    exp = sum(4 * ((p.size + 15) // 16) + 4 * p.shape[0] for p in (params[0], params[2], params[3]))
+    exp += 4 * (64 + 16)
+    assert model.mem_bytes() == exp
+    # the whole stack through the int8 ternary GEMM, ReLU between layers
+    h = x
+    for i, (w_i, b_i) in enumerate([(0, 1), (2, None), (3, 4)]):
+        tq, ts = O.ternary_quantize_rows(params[w_i])
+        aq, sa = O.quant_rows_i8(h)
+        h, _ = O.ternary_gemm_i8(aq, sa, O.pack_ternary(tq), ts, params[w_i].shape[0],
+                                 None if b_i is None else params[b_i], i < 2)
+    np.testing.assert_array_equal(host(model.forward(to_dev(x, dev))), h)
