@@ -157,6 +157,47 @@ def bench_gemv(H, W, dev, steps):
     return out
 
 
+# ---------------------------------------------------------------- QuantizedLinear GEMV
+QT_SHAPES = [(1, 4096, 11008), (4, 4096, 11008), (1, 4096, 4096)]
+QT_FORMATS = [("INT4_g128", 3, 128), ("GGUF_Q4_0", 6, 32), ("GGUF_Q8_0", 8, 32), ("BF16", 1, 0)]
+
+
+def bench_qt_gemv(H, dev, steps):
+    """QuantizedLinear::forward (src/quantize.rs:744-754) at decode shapes:
+    the fused GEMV that decodes INT4/GGUF/BF16 weights in registers. Bytes per
+    launch = weight codes + f32 scales + x (4 m k) + y (4 m n); weights
+    rotate over copies past the MALL as for the W8A8 GEMV."""
+    import torch
+    out = {}
+    for name, fmt, gs in QT_FORMATS:
+        for (m, k, n) in QT_SHAPES:
+            if name == "BF16" and (m, n) != (1, 11008):
+                continue
+            nb, ns, g = H.qt_layout(fmt, n * k, gs)
+            wbytes = nb + 4 * ns
+            copies = max(2, -(-640 * 2**20 // wbytes))
+            ds, ss = [], []
+            for i in range(copies):
+                d, s_, _ = H.qt_quantize(fmt, gen_f32((n, k), 300 + i, dev, 0.02), gs)
+                ds.append(d)
+                ss.append(s_ if s_.numel() else torch.zeros(1, device=dev))
+            x = gen_f32((m, k), 9, dev)
+            y = torch.empty((m, n), dtype=torch.float32, device=dev)
+            n_launch = copies * max(1, -(-max(steps, 100) // copies))
+            ms = graph_timed(lambda i: H.qt_linear_forward(fmt, x, ds[i % copies], ss[i % copies],
+                                                           g, n, y=y, algo=H.ALGO_GEMV), n_launch)
+            nbytes = wbytes + 4 * m * k + 4 * m * n
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out[f"{name}_m{m}_k{k}_n{n}"] = {
+                "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+                "weight_copies": copies, "launches_timed": n_launch,
+                "timing": "HIP graph replay, events / launches"}
+            del ds, ss
+            torch.cuda.empty_cache()
+    return out
+
+
 # ---------------------------------------------------------------- ternary
 def bench_ternary(H, W, dev, steps):
     import torch
@@ -300,7 +341,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--only", default="all",
-                    choices=["all", "prefill", "gemv", "ternary", "rotorquant", "sgemm", "copy"])
+                    choices=["all", "prefill", "gemv", "qt_gemv", "ternary", "rotorquant", "sgemm",
+                             "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -348,6 +390,9 @@ def main():
     if args.only in ("all", "gemv"):
         log("decode GEMV: 6 shapes")
         components["w8a8_decode_gemv"] = bench_gemv(H, W, dev, args.steps)
+    if args.only in ("all", "qt_gemv"):
+        log("QuantizedLinear GEMV: INT4/GGUF/BF16 weights, decode shapes")
+        components["quantized_linear_gemv"] = bench_qt_gemv(H, dev, args.steps)
     if args.only in ("all", "ternary"):
         log("ternary GEMM 512x4096x4096")
         components["ternary_gemm"] = bench_ternary(H, W, dev, args.steps)

@@ -194,6 +194,62 @@ int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k,
               float alpha, const float *a, int64_t lda, const float *b,
               int64_t ldb, float beta, float *c, int64_t ldc, void *stream);
 
+/* ------------------------------------- QuantizedTensor formats (next row) */
+
+/* QuantFormat (src/quantize.rs:37-56), in the reference's declaration order.
+ * Storage is QuantizedTensor::{data, scales, group_size} byte for byte:
+ * FP16/BF16 2 bytes per element (little-endian), no scales; INT8/GGUF_Q8 one
+ * int8 code per element; INT4/NF4/NVFP4/GGUF_Q4(K) 4-bit codes, each group
+ * packed on its own, low nibble first; one f32 scale per group (GGUF: per
+ * block of min(group, 32)). */
+#define RNN_QF_FP16 0
+#define RNN_QF_BF16 1
+#define RNN_QF_INT8 2
+#define RNN_QF_INT4 3
+#define RNN_QF_NF4 4
+#define RNN_QF_NVFP4 5
+#define RNN_QF_GGUF_Q4 6
+#define RNN_QF_GGUF_Q4K 7 /* stored as Q4_0, as the reference does (:241-243) */
+#define RNN_QF_GGUF_Q8 8
+
+/* Host-side sizes of QuantizedTensor::quantize(n elements, group_size)
+ * (src/quantize.rs:231-250): data bytes, scales.len() and the stored
+ * group_size field (0 means the whole tensor; GGUF caps it at 32). No GPU
+ * work. */
+int rnn_qt_layout(int format, int64_t n, int64_t group_size, int64_t *data_bytes,
+                  int64_t *n_scales, int64_t *stored_group);
+
+/* QuantizedTensor::quantize (src/quantize.rs:231-250, per-format :296-625)
+ * of x [n] (a tensor's flat row-major data): data and scales sized by
+ * rnn_qt_layout. Codes and scales are bit-exact (IEEE division, half-away
+ * rounding, first-minimum NF4/E2M1 search, truncating f32->f16 and the
+ * wrapping bf16 rounding of :639-703). */
+int rnn_qt_quantize(int format, const float *x, int64_t n, int64_t group_size,
+                    uint8_t *data, float *scales, void *stream);
+
+/* QuantizedTensor::dequantize (src/quantize.rs:252-269, :324-632) into out
+ * [n]; `group` is the stored group_size field. 4-bit formats other than GGUF
+ * read byte i/2 of the whole tensor and scales[min(i/group, n_scales-1)], as
+ * the reference does. Bit-exact. */
+int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
+                      const float *scales, int64_t n_scales, int64_t group,
+                      int64_t n, float *out, void *stream);
+
+/* QuantizedLinear::forward (src/quantize.rs:744-754): y [m, out_f] =
+ * x [m, in_f] . W^T (+ bias[out_f]) with W = the dequantized [out_f, in_f]
+ * weight. AUTO: for m <= 16 with INT4/INT8/GGUF/FP16/BF16 weights, in_f % 32
+ * == 0, group % 32 == 0 and 16-byte aligned x and data, a fused GEMV that
+ * decodes the codes in registers (weights read once); otherwise dequantize
+ * into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV forces the
+ * former (error if it does not fit), RNN_ALGO_TILED the latter. f32 sums in
+ * the kernel's own order: within the rnn_sgemm rounding bound of the
+ * reference, not bit for bit. */
+int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,
+                          const uint8_t *data, int64_t data_bytes,
+                          const float *scales, int64_t n_scales, int64_t group,
+                          int64_t out_f, const float *bias, float *y,
+                          unsigned flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

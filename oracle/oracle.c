@@ -610,3 +610,268 @@ void orc_sgemm(int transa, int transb, size_t m, size_t n, size_t k, float alpha
         }
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* src/quantize.rs: QuantizedTensor (multi-format weight quantization)  */
+/* ------------------------------------------------------------------ */
+
+/* src/quantize.rs:96-114 */
+static const float NF4_LUT[16] = {
+    -1.0f, -0.6961928f, -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f,
+    -0.091050036f, 0.0f, 0.0795803f, 0.1609302f, 0.2461123f, 0.33791524f,
+    0.44070983f, 0.562617f, 0.72295684f, 1.0f};
+/* src/quantize.rs:138-144 (index 8 is -0.0) */
+static const float NVFP4_LUT[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,
+                                    4.0f,  6.0f,  -0.0f, -0.5f, -1.0f, -1.5f,
+                                    -2.0f, -3.0f, -4.0f, -6.0f};
+
+/* src/quantize.rs:117-129: first index of the strictly smallest |v - x|. */
+static uint8_t nf4_index(float x) {
+    uint8_t best = 0;
+    float best_d = INFINITY;
+    for (int i = 0; i < 16; ++i) {
+        float d = fabsf(NF4_LUT[i] - x);
+        if (d < best_d) { best_d = d; best = (uint8_t)i; }
+    }
+    return best;
+}
+
+/* src/quantize.rs:146-161 */
+static uint8_t nvfp4_index(float x) {
+    static const float mags[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    float ax = fabsf(x);
+    uint8_t sign = x < 0.0f ? 8 : 0;
+    uint8_t best = 0;
+    float best_d = INFINITY;
+    for (int i = 0; i < 8; ++i) {
+        float d = fabsf(mags[i] - ax);
+        if (d < best_d) { best_d = d; best = (uint8_t)i; }
+    }
+    return sign | best;
+}
+
+/* src/quantize.rs:639-666 (truncating; release-mode integer semantics) */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
+    uint32_t mant = bits & 0x7FFFFFu;
+    if (exp == 0xFF) return sign | 0x7C00u | (mant != 0 ? 0x200u : 0u);
+    int32_t new_exp = exp - 127 + 15;
+    if (new_exp >= 31) return sign | 0x7C00u;
+    if (new_exp <= 0) {
+        if (14 - new_exp >= 24) return sign;
+        uint32_t m = mant | 0x800000u;
+        uint32_t shift = (uint32_t)(14 - new_exp);
+        return sign | (uint16_t)(m >> shift);
+    }
+    return sign | (uint16_t)((uint32_t)new_exp << 10) | (uint16_t)(mant >> 13);
+}
+
+/* src/quantize.rs:668-695. The subnormal loop decrements an unsigned
+ * exponent below zero for mantissas under 0x200; release Rust wraps, and the
+ * `as i32` then gives the intended negative value, so this follows the
+ * release arithmetic (debug builds would panic on that overflow). */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t exp = ((uint32_t)h >> 10) & 0x1Fu;
+    uint32_t mant = (uint32_t)h & 0x3FFu;
+    uint32_t val;
+    if (exp == 0) {
+        if (mant == 0) {
+            val = sign;
+        } else {
+            uint32_t e = 1, m = mant;
+            while ((m & 0x400u) == 0) { m <<= 1; e -= 1; }
+            m &= 0x3FFu;
+            val = sign | ((uint32_t)(127 - 15 + (int32_t)e) << 23) | (m << 13);
+        }
+    } else if (exp == 31) {
+        val = sign | 0x7F800000u | (mant << 13);
+    } else {
+        val = sign | ((exp + 112) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &val, 4);
+    return f;
+}
+
+/* src/quantize.rs:697-703: bits + ((bits>>16)&1) + 0x7FFF, wrapping (release). */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    uint32_t r = bits + ((bits >> 16) & 1u) + 0x7FFFu;
+    return (uint16_t)(r >> 16);
+}
+
+/* src/quantize.rs:705-708 */
+float orc_bf16_to_f32(uint16_t b) {
+    uint32_t v = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &v, 4);
+    return f;
+}
+
+/* Array forms (the results stay bit patterns in memory; a float returned by
+ * value through a foreign-function layer may have its signalling NaNs
+ * quieted on the way). */
+void orc_f32_to_f16_array(const float *x, size_t n, uint16_t *h) {
+    for (size_t i = 0; i < n; ++i) h[i] = orc_f32_to_f16(x[i]);
+}
+void orc_f16_to_f32_array(const uint16_t *h, size_t n, float *x) {
+    for (size_t i = 0; i < n; ++i) x[i] = orc_f16_to_f32(h[i]);
+}
+void orc_f32_to_bf16_array(const float *x, size_t n, uint16_t *h) {
+    for (size_t i = 0; i < n; ++i) h[i] = orc_f32_to_bf16(x[i]);
+}
+void orc_bf16_to_f32_array(const uint16_t *h, size_t n, float *x) {
+    for (size_t i = 0; i < n; ++i) x[i] = orc_bf16_to_f32(h[i]);
+}
+
+static int qf_is4(int fmt) {
+    return fmt == ORC_QF_INT4 || fmt == ORC_QF_NF4 || fmt == ORC_QF_NVFP4 ||
+           fmt == ORC_QF_GGUF_Q4 || fmt == ORC_QF_GGUF_Q4K;
+}
+
+/* Storage of QuantizedTensor::quantize (src/quantize.rs:231-250): the group
+ * (or GGUF block, min(group,32), :515/:558) every format uses, with
+ * group_size 0 meaning the whole tensor (:235). */
+size_t orc_qt_layout(int fmt, size_t n, size_t group_size, size_t *n_scales,
+                     size_t *stored_group) {
+    if (fmt == ORC_QF_FP16 || fmt == ORC_QF_BF16) {
+        *n_scales = 0;
+        *stored_group = 0;
+        return 2 * n;
+    }
+    size_t g = group_size == 0 ? n : group_size;
+    if (fmt == ORC_QF_GGUF_Q4 || fmt == ORC_QF_GGUF_Q4K || fmt == ORC_QF_GGUF_Q8)
+        g = g < 32 ? g : 32;
+    *stored_group = g;
+    if (g == 0) { *n_scales = 0; return 0; }
+    size_t ng = (n + g - 1) / g;
+    *n_scales = ng;
+    if (!qf_is4(fmt)) return n;
+    if (ng == 0) return 0;
+    size_t last = n - (ng - 1) * g;
+    return (ng - 1) * ((g + 1) / 2) + (last + 1) / 2;
+}
+
+/* src/quantize.rs:296-322 (INT8), :334-375 (INT4), :398-438 (NF4),
+ * :456-496 (NVFP4), :514-536 with :171-190 (GGUF Q4_0), :556-583 (GGUF Q8_0),
+ * :589-602 (FP16), :612-625 (BF16). 4-bit formats pack each group on its own
+ * (low nibble first, a zero high nibble after an odd count). */
+void orc_qt_quantize(int fmt, const float *x, size_t n, size_t group_size,
+                     uint8_t *data, float *scales) {
+    if (fmt == ORC_QF_FP16 || fmt == ORC_QF_BF16) {
+        for (size_t i = 0; i < n; ++i) {
+            uint16_t h = fmt == ORC_QF_FP16 ? orc_f32_to_f16(x[i]) : orc_f32_to_bf16(x[i]);
+            data[2 * i] = (uint8_t)(h & 0xFF);
+            data[2 * i + 1] = (uint8_t)(h >> 8);
+        }
+        return;
+    }
+    size_t ns, g;
+    orc_qt_layout(fmt, n, group_size, &ns, &g);
+    size_t off = 0;
+    for (size_t gi = 0; gi < ns; ++gi) {
+        size_t start = gi * g, end = start + g < n ? start + g : n;
+        float max_abs = 0.0f;
+        for (size_t i = start; i < end; ++i) max_abs = fmaxf(max_abs, fabsf(x[i]));
+        float s;
+        switch (fmt) {
+        case ORC_QF_INT8: case ORC_QF_GGUF_Q8:
+            s = max_abs > 0.0f ? max_abs / 127.0f : 1.0f; break;
+        case ORC_QF_INT4: s = max_abs > 0.0f ? max_abs / 7.0f : 1.0f; break;
+        case ORC_QF_NF4: s = max_abs > 0.0f ? max_abs : 1.0f; break;
+        case ORC_QF_NVFP4: s = max_abs > 0.0f ? max_abs / 6.0f : 1.0f; break;
+        default: /* GGUF Q4_0, :174-176 */
+            s = max_abs / -8.0f;
+            if (s == 0.0f) s = 1.0f;
+            break;
+        }
+        scales[gi] = s;
+        if (!qf_is4(fmt)) {
+            for (size_t i = start; i < end; ++i)
+                data[i] = (uint8_t)f32_to_i8_sat(clampf_rs(roundf(x[i] / s), -128.0f, 127.0f));
+            continue;
+        }
+        for (size_t i = start; i < end; i += 2) {
+            uint8_t c[2] = {0, 0};
+            for (size_t t = 0; t < 2 && i + t < end; ++t) {
+                float v = x[i + t] / s;
+                switch (fmt) {
+                case ORC_QF_NF4: c[t] = nf4_index(v); break;
+                case ORC_QF_NVFP4: c[t] = nvfp4_index(v); break;
+                default: /* INT4 and Q4_0: round, clamp to [-8,7], low 4 bits */
+                    c[t] = (uint8_t)f32_to_i8_sat(clampf_rs(roundf(v), -8.0f, 7.0f)) & 0xF;
+                    break;
+                }
+            }
+            data[off++] = (uint8_t)(c[0] | (c[1] << 4));
+        }
+    }
+}
+
+static float nib_signed(uint8_t nib) { return (float)((nib & 0x8) ? (int)nib - 16 : (int)nib); }
+
+/* src/quantize.rs:252-269 and the per-format dequantizers :324-332 (INT8,
+ * GGUF Q8_0 :585-587), :377-396 (INT4), :440-454 (NF4), :498-512 (NVFP4),
+ * :538-554 with :192-211 (GGUF Q4_0), :604-610 (FP16), :627-632 (BF16).
+ * INT4/NF4/NVFP4 index bytes as data[i/2] over the whole tensor and scales as
+ * scales[min(i/group, n_scales-1)] (:326, :380, :442, :500), exactly as the
+ * reference does; GGUF Q4_0 walks its blocks with a running byte offset. */
+void orc_qt_dequantize(int fmt, const uint8_t *data, const float *scales,
+                       size_t n_scales, size_t group, size_t n, float *out) {
+    if (fmt == ORC_QF_FP16 || fmt == ORC_QF_BF16) {
+        for (size_t i = 0; i < n; ++i) {
+            uint16_t h = (uint16_t)(data[2 * i] | (data[2 * i + 1] << 8));
+            out[i] = fmt == ORC_QF_FP16 ? orc_f16_to_f32(h) : orc_bf16_to_f32(h);
+        }
+        return;
+    }
+    if (fmt == ORC_QF_GGUF_Q4 || fmt == ORC_QF_GGUF_Q4K) {
+        size_t off = 0;
+        for (size_t b = 0; b * group < n; ++b) {
+            size_t start = b * group, end = start + group < n ? start + group : n;
+            float s = scales[b];
+            for (size_t i = 0; i < end - start; ++i) {
+                uint8_t byte = data[off + i / 2];
+                uint8_t nib = (i % 2 == 0) ? (byte & 0xF) : ((byte >> 4) & 0xF);
+                out[start + i] = nib_signed(nib) * s;
+            }
+            off += (end - start + 1) / 2;
+        }
+        return;
+    }
+    if (n_scales == 0 || group == 0) return; /* the reference panics here */
+    for (size_t i = 0; i < n; ++i) {
+        size_t gi = i / group;
+        float s = scales[gi < n_scales - 1 ? gi : n_scales - 1];
+        if (fmt == ORC_QF_INT8 || fmt == ORC_QF_GGUF_Q8) {
+            out[i] = (float)(int8_t)data[i] * s;
+            continue;
+        }
+        uint8_t byte = data[i / 2];
+        uint8_t nib = (i % 2 == 0) ? (byte & 0xF) : ((byte >> 4) & 0xF);
+        if (fmt == ORC_QF_INT4) out[i] = nib_signed(nib) * s;
+        else if (fmt == ORC_QF_NF4) out[i] = NF4_LUT[nib] * s;
+        else out[i] = NVFP4_LUT[nib] * s;
+    }
+}
+
+/* QuantizedLinear::forward (src/quantize.rs:744-754): W = dequantize()
+ * [out_f, in_f], y = x.matmul(W^T) (blas sgemm, restated by orc_sgemm), then
+ * y + bias broadcast over rows. */
+void orc_qt_linear_forward(int fmt, const float *x, size_t m, size_t in_f,
+                           const uint8_t *data, const float *scales, size_t n_scales,
+                           size_t group, size_t out_f, const float *bias, float *y) {
+    size_t nw = out_f * in_f;
+    float *w = (float *)malloc(sizeof(float) * (nw > 0 ? nw : 1));
+    orc_qt_dequantize(fmt, data, scales, n_scales, group, out_f * in_f, w);
+    orc_sgemm(0, 1, m, out_f, in_f, 1.0f, x, in_f, w, in_f, 0.0f, y, out_f);
+    free(w);
+    if (bias)
+        for (size_t i = 0; i < m; ++i)
+            for (size_t j = 0; j < out_f; ++j) y[i * out_f + j] = y[i * out_f + j] + bias[j];
+}

@@ -168,6 +168,48 @@ void orc_sgemm(int transa, int transb, size_t m, size_t n, size_t k, float alpha
                const float *a, size_t lda, const float *b, size_t ldb, float beta,
                float *c, size_t ldc);
 
+/* ---- QuantizedTensor formats (src/quantize.rs) ---- */
+
+/* QuantFormat (src/quantize.rs:37-56), in the reference's declaration order. */
+enum {
+    ORC_QF_FP16 = 0, ORC_QF_BF16 = 1, ORC_QF_INT8 = 2, ORC_QF_INT4 = 3,
+    ORC_QF_NF4 = 4, ORC_QF_NVFP4 = 5, ORC_QF_GGUF_Q4 = 6, ORC_QF_GGUF_Q4K = 7,
+    ORC_QF_GGUF_Q8 = 8
+};
+
+/* Half/bfloat conversions of src/quantize.rs:639-708 (f32_to_f16 truncates;
+ * f32_to_bf16 adds with wrap-around as release Rust does). */
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t b);
+/* The same over arrays (bit patterns, signalling NaNs included, kept as is). */
+void orc_f32_to_f16_array(const float *x, size_t n, uint16_t *h);
+void orc_f16_to_f32_array(const uint16_t *h, size_t n, float *x);
+void orc_f32_to_bf16_array(const float *x, size_t n, uint16_t *h);
+void orc_bf16_to_f32_array(const uint16_t *h, size_t n, float *x);
+
+/* Bytes of QuantizedTensor::data for n elements; *n_scales and
+ * *stored_group receive scales.len() and the group_size field
+ * (src/quantize.rs:231-250, :515, :558). */
+size_t orc_qt_layout(int fmt, size_t n, size_t group_size, size_t *n_scales,
+                     size_t *stored_group);
+
+/* QuantizedTensor::quantize (src/quantize.rs:231-250 and :296-625). */
+void orc_qt_quantize(int fmt, const float *x, size_t n, size_t group_size,
+                     uint8_t *data, float *scales);
+
+/* QuantizedTensor::dequantize (src/quantize.rs:252-269 and :324-632); group is
+ * the stored group_size field. */
+void orc_qt_dequantize(int fmt, const uint8_t *data, const float *scales,
+                       size_t n_scales, size_t group, size_t n, float *out);
+
+/* QuantizedLinear::forward (src/quantize.rs:744-754): dequantize, x.W^T with
+ * orc_sgemm's order, then + bias (may be NULL). */
+void orc_qt_linear_forward(int fmt, const float *x, size_t m, size_t in_f,
+                           const uint8_t *data, const float *scales, size_t n_scales,
+                           size_t group, size_t out_f, const float *bias, float *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,6 +58,18 @@ def lib():
             "orc_rotorquant_rotors_from_seed": [ctypes.c_uint64, _SZ, _P],
             "orc_chacha_block": [_P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _P],
             "orc_chacha20_block_ietf": [_P, ctypes.c_uint32, _P, _P],
+            "orc_f32_to_f16": [ctypes.c_float],
+            "orc_f16_to_f32": [ctypes.c_uint16],
+            "orc_f32_to_bf16": [ctypes.c_float],
+            "orc_bf16_to_f32": [ctypes.c_uint16],
+            "orc_f32_to_f16_array": [_P, _SZ, _P],
+            "orc_f16_to_f32_array": [_P, _SZ, _P],
+            "orc_f32_to_bf16_array": [_P, _SZ, _P],
+            "orc_bf16_to_f32_array": [_P, _SZ, _P],
+            "orc_qt_layout": [ctypes.c_int, _SZ, _SZ, _P, _P],
+            "orc_qt_quantize": [ctypes.c_int, _P, _SZ, _SZ, _P, _P],
+            "orc_qt_dequantize": [ctypes.c_int, _P, _P, _SZ, _SZ, _SZ, _P],
+            "orc_qt_linear_forward": [ctypes.c_int, _P, _SZ, _SZ, _P, _P, _SZ, _SZ, _SZ, _P, _P],
             "orc_sgemm": [ctypes.c_int, ctypes.c_int, _SZ, _SZ, _SZ, ctypes.c_float, _P, _SZ, _P, _SZ,
                           ctypes.c_float, _P, _SZ],
         }
@@ -66,6 +78,11 @@ def lib():
             fn.argtypes = args
             fn.restype = None
         L.orc_igemm.restype = ctypes.c_int
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_f32_to_bf16.restype = ctypes.c_uint16
+        L.orc_bf16_to_f32.restype = ctypes.c_float
+        L.orc_qt_layout.restype = _SZ
         L.orc_ternary_quantize_absmean.restype = ctypes.c_float
         _lib = L
     return _lib
@@ -341,3 +358,78 @@ def sgemm_f64(transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc):
     exact = alpha * (A @ B) + (beta * C if beta != 0.0 else 0.0)
     scale = abs(alpha) * (np.abs(A) @ np.abs(B)) + (abs(beta) * np.abs(C) if beta != 0.0 else 0.0)
     return exact, scale
+
+
+# ---------------------------------------------------------------- QuantizedTensor
+# QuantFormat (src/quantize.rs:37-56), declaration order
+QF_FP16, QF_BF16, QF_INT8, QF_INT4, QF_NF4, QF_NVFP4, QF_GGUF_Q4, QF_GGUF_Q4K, QF_GGUF_Q8 = range(9)
+QF_NAMES = {QF_FP16: "FP16", QF_BF16: "BF16", QF_INT8: "INT8", QF_INT4: "INT4", QF_NF4: "NF4",
+            QF_NVFP4: "NVFP4", QF_GGUF_Q4: "GGUF_Q4", QF_GGUF_Q4K: "GGUF_Q4K",
+            QF_GGUF_Q8: "GGUF_Q8"}
+# QuantFormat::bits (src/quantize.rs:60-71)
+QF_BITS = {QF_FP16: 16, QF_BF16: 16, QF_INT8: 8, QF_GGUF_Q8: 8, QF_INT4: 4, QF_NF4: 4,
+           QF_NVFP4: 4, QF_GGUF_Q4: 4, QF_GGUF_Q4K: 4}
+
+
+def _conv(name, x, in_dtype, out_dtype):
+    x = _c(x, in_dtype).ravel()
+    out = np.empty(x.size, out_dtype)
+    getattr(lib(), name)(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def f32_to_f16(x):
+    """src/quantize.rs:639-666 over an array (uint16 bit patterns)."""
+    return _conv("orc_f32_to_f16_array", x, np.float32, np.uint16)
+
+
+def f16_to_f32(h):
+    """src/quantize.rs:668-695 over an array."""
+    return _conv("orc_f16_to_f32_array", h, np.uint16, np.float32)
+
+
+def f32_to_bf16(x):
+    """src/quantize.rs:697-703 over an array."""
+    return _conv("orc_f32_to_bf16_array", x, np.float32, np.uint16)
+
+
+def bf16_to_f32(h):
+    """src/quantize.rs:705-708 over an array."""
+    return _conv("orc_bf16_to_f32_array", h, np.uint16, np.float32)
+
+
+def qt_layout(fmt, n, group_size):
+    """(data bytes, scales.len(), stored group_size) of QuantizedTensor::quantize."""
+    ns, g = (ctypes.c_size_t * 1)(), (ctypes.c_size_t * 1)()
+    nb = lib().orc_qt_layout(fmt, n, group_size, ctypes.addressof(ns), ctypes.addressof(g))
+    return int(nb), int(ns[0]), int(g[0])
+
+
+def qt_quantize(fmt, x, group_size):
+    """QuantizedTensor::quantize (src/quantize.rs:231-250). Returns
+    (data uint8, scales f32, stored group_size)."""
+    x = _c(x, np.float32).ravel()
+    nb, ns, g = qt_layout(fmt, x.size, group_size)
+    data = np.zeros(nb, np.uint8)
+    scales = np.zeros(ns, np.float32)
+    lib().orc_qt_quantize(fmt, _ptr(x), x.size, group_size, _ptr(data), _ptr(scales))
+    return data, scales, g
+
+
+def qt_dequantize(fmt, data, scales, group, n):
+    """QuantizedTensor::dequantize (src/quantize.rs:252-269), flat f32 [n]."""
+    data, scales = _c(data, np.uint8), _c(scales, np.float32)
+    out = np.empty(n, np.float32)
+    lib().orc_qt_dequantize(fmt, _ptr(data), _ptr(scales), scales.size, group, n, _ptr(out))
+    return out
+
+
+def qt_linear_forward(fmt, x, data, scales, group, out_f, bias=None):
+    """QuantizedLinear::forward (src/quantize.rs:744-754)."""
+    x, data, scales = _c(x, np.float32), _c(data, np.uint8), _c(scales, np.float32)
+    bias = None if bias is None else _c(bias, np.float32)
+    m, in_f = x.shape
+    y = np.empty((m, out_f), np.float32)
+    lib().orc_qt_linear_forward(fmt, _ptr(x), m, in_f, _ptr(data), _ptr(scales), scales.size,
+                                group, out_f, _ptr(bias), _ptr(y))
+    return y

@@ -1,0 +1,587 @@
+// qformat.hip -- QuantizedTensor (src/quantize.rs): quantize / dequantize of
+// every QuantFormat, and QuantizedLinear::forward with the weights decoded on
+// the fly.
+//
+// Storage follows QuantizedTensor::{data, scales, group_size} byte for byte:
+// 8-bit codes one per byte, 4-bit codes packed per group (low nibble first),
+// f16/bf16 as little-endian u16 pairs, f32 scales per group (GGUF: per block
+// of min(group, 32)). Codes, scales and dequantized values are bit-exact with
+// the reference; the linear forward sums in f32 in its own order.
+#include "common.hpp"
+#include "numerics.hpp"
+
+namespace rnn {
+
+enum QKind { KIND_I4 = 0, KIND_I8 = 1, KIND_F16 = 2, KIND_BF16 = 3 };
+
+__host__ __device__ inline bool qf_is4(int f) {
+    return f == RNN_QF_INT4 || f == RNN_QF_NF4 || f == RNN_QF_NVFP4 || f == RNN_QF_GGUF_Q4 ||
+           f == RNN_QF_GGUF_Q4K;
+}
+__host__ __device__ inline bool qf_is_gguf(int f) {
+    return f == RNN_QF_GGUF_Q4 || f == RNN_QF_GGUF_Q4K || f == RNN_QF_GGUF_Q8;
+}
+
+// src/quantize.rs:96-114 and :138-144 (index 8 of the E2M1 table is -0.0).
+__constant__ float kNF4[16] = {-1.0f, -0.6961928f, -0.52507305f, -0.3949175f,
+                               -0.28444138f, -0.18477343f, -0.091050036f, 0.0f,
+                               0.0795803f, 0.1609302f, 0.2461123f, 0.33791524f,
+                               0.44070983f, 0.562617f, 0.72295684f, 1.0f};
+__constant__ float kE2M1[16] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f,
+                                -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+// Scale of a group from its max|x| (src/quantize.rs:307, :345, :408, :466,
+// :174-176, :567).
+__device__ inline float group_scale(int f, float max_abs) {
+    switch (f) {
+    case RNN_QF_INT8: case RNN_QF_GGUF_Q8: return max_abs > 0.0f ? max_abs / 127.0f : 1.0f;
+    case RNN_QF_INT4: return max_abs > 0.0f ? max_abs / 7.0f : 1.0f;
+    case RNN_QF_NF4: return max_abs > 0.0f ? max_abs : 1.0f;
+    case RNN_QF_NVFP4: return max_abs > 0.0f ? max_abs / 6.0f : 1.0f;
+    default: {
+        const float s = max_abs / -8.0f;  // Q4_0: signed range [-8, 7]
+        return s == 0.0f ? 1.0f : s;
+    }
+    }
+}
+
+// Code of one value (src/quantize.rs:117-129, :146-161, :181-186, :350-353).
+__device__ inline uint8_t code4(int f, float v, float s) {
+    const float t = v / s;
+    if (f == RNN_QF_NF4) {
+        uint8_t best = 0;
+        float bd = INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float d = fabsf(kNF4[i] - t);
+            if (d < bd) { bd = d; best = (uint8_t)i; }
+        }
+        return best;
+    }
+    if (f == RNN_QF_NVFP4) {
+        const float a = fabsf(t);
+        uint8_t best = 0;
+        float bd = INFINITY;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float d = fabsf(kE2M1[i] - a);
+            if (d < bd) { bd = d; best = (uint8_t)i; }
+        }
+        return (uint8_t)((t < 0.0f ? 8 : 0) | best);
+    }
+    return (uint8_t)(to_i8_rs(clamp_rs(roundf(t), -8.0f, 7.0f)) & 0xF);
+}
+
+// src/quantize.rs:639-666 (truncating f32 -> f16).
+__device__ inline uint16_t f32_to_f16_rs(float f) {
+    const uint32_t bits = __float_as_uint(f);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
+    const uint32_t mant = bits & 0x7FFFFFu;
+    if (exp == 0xFF) return sign | 0x7C00u | (mant != 0 ? 0x200u : 0u);
+    const int32_t ne = exp - 127 + 15;
+    if (ne >= 31) return sign | 0x7C00u;
+    if (ne <= 0) {
+        if (14 - ne >= 24) return sign;
+        return sign | (uint16_t)((mant | 0x800000u) >> (uint32_t)(14 - ne));
+    }
+    return sign | (uint16_t)((uint32_t)ne << 10) | (uint16_t)(mant >> 13);
+}
+
+// src/quantize.rs:668-695 with release integer semantics: a subnormal with
+// s leading zeros below bit 10 gets exponent 113 - s.
+__device__ inline float f16_to_f32_rs(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1Fu;
+    const uint32_t mant = h & 0x3FFu;
+    uint32_t v;
+    if (exp == 0) {
+        if (mant == 0) {
+            v = sign;
+        } else {
+            const int s = __clz(mant) - 21;  // shifts until bit 10 is set
+            v = sign | ((uint32_t)(113 - s) << 23) | (((mant << s) & 0x3FFu) << 13);
+        }
+    } else if (exp == 31) {
+        v = sign | 0x7F800000u | (mant << 13);
+    } else {
+        v = sign | ((exp + 112) << 23) | (mant << 13);
+    }
+    return __uint_as_float(v);
+}
+
+// src/quantize.rs:697-703 (wrapping add, as release Rust).
+__device__ inline uint16_t f32_to_bf16_rs(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (uint16_t)((b + ((b >> 16) & 1u) + 0x7FFFu) >> 16);
+}
+
+// ------------------------------------------------------------ quantize
+
+__global__ void qt_half_quant_kernel(int f, const float *__restrict__ x, int64_t n,
+                                     uint16_t *__restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = f == RNN_QF_FP16 ? f32_to_f16_rs(x[i]) : f32_to_bf16_rs(x[i]);
+}
+
+// Stores the codes of elements [start, end) of one group with scale s: one
+// byte per element, or one byte per pair for 4-bit formats at byte offset
+// `off` (each group packed on its own, src/quantize.rs:355-365).
+__device__ inline void emit_codes(int f, const float *__restrict__ x, int64_t start, int64_t end,
+                                  float s, int64_t off, uint8_t *__restrict__ data, int64_t t0,
+                                  int64_t stride) {
+    if (!qf_is4(f)) {
+        for (int64_t i = start + t0; i < end; i += stride) data[i] = (uint8_t)quant_i8(x[i], s);
+        return;
+    }
+    const int64_t nb = (end - start + 1) / 2;
+    for (int64_t b = t0; b < nb; b += stride) {
+        const int64_t i = start + 2 * b;
+        const uint8_t lo = code4(f, x[i], s);
+        const uint8_t hi = i + 1 < end ? code4(f, x[i + 1], s) : (uint8_t)0;
+        data[off + b] = (uint8_t)(lo | (hi << 4));
+    }
+}
+
+// Groups of up to kSmallGroup elements: one wave per group finds max|x|
+// (order-free, equal to the reference's sequential fold), then writes the
+// scale and the codes.
+constexpr int64_t kSmallGroup = 8192;
+
+__global__ __launch_bounds__(256) void qt_quant_group_kernel(
+    int f, const float *__restrict__ x, int64_t n, int64_t g, int64_t ng,
+    uint8_t *__restrict__ data, float *__restrict__ scales) {
+    const int64_t gi = blockIdx.x * 4 + threadIdx.x / 64;
+    const int lane = threadIdx.x % 64;
+    if (gi >= ng) return;
+    const int64_t start = gi * g, end = start + g < n ? start + g : n;
+    float m = 0.0f;
+    for (int64_t i = start + lane; i < end; i += 64) m = fmaxf(m, fabsf(x[i]));
+    m = wave_max(m);
+    const float s = group_scale(f, m);
+    if (lane == 0) scales[gi] = s;
+    emit_codes(f, x, start, end, s, gi * ((g + 1) / 2), data, lane, 64);
+}
+
+// Larger groups: max|x| per group through an atomic max on the bit patterns
+// of non-negative floats (kept in `scales`, zeroed first), then codes, then
+// max -> scale in place.
+constexpr int64_t kChunk = 4096;
+
+__global__ void qt_zero_kernel(uint32_t *__restrict__ p, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+__global__ __launch_bounds__(256) void qt_group_max_kernel(const float *__restrict__ x, int64_t n,
+                                                           int64_t g, int64_t chunks_per_group,
+                                                           uint32_t *__restrict__ maxbits) {
+    const int64_t gi = blockIdx.x / chunks_per_group, c = blockIdx.x % chunks_per_group;
+    const int64_t gend = gi * g + g < n ? gi * g + g : n;
+    const int64_t start = gi * g + c * kChunk;
+    const int64_t end = start + kChunk < gend ? start + kChunk : gend;
+    float m = 0.0f;
+    for (int64_t i = start + threadIdx.x; i < end; i += 256) m = fmaxf(m, fabsf(x[i]));
+    __shared__ float red[4];
+    m = block_max<256>(m, red);  // NaN inputs drop out here, as in f32::max
+    if (threadIdx.x == 0 && start < end) atomicMax(maxbits + gi, __float_as_uint(m));
+}
+
+__global__ __launch_bounds__(256) void qt_big_codes_kernel(int f, const float *__restrict__ x,
+                                                           int64_t n, int64_t g,
+                                                           int64_t chunks_per_group,
+                                                           const float *__restrict__ maxv,
+                                                           uint8_t *__restrict__ data) {
+    const int64_t gi = blockIdx.x / chunks_per_group, c = blockIdx.x % chunks_per_group;
+    const int64_t gstart = gi * g, gend = gstart + g < n ? gstart + g : n;
+    const int64_t start = gstart + c * kChunk;  // kChunk is even: pairs stay whole
+    const int64_t end = start + kChunk < gend ? start + kChunk : gend;
+    if (start >= end) return;
+    const float s = group_scale(f, maxv[gi]);
+    emit_codes(f, x, start, end, s, gi * ((g + 1) / 2) + c * (kChunk / 2), data, threadIdx.x, 256);
+}
+
+__global__ void qt_finish_scales_kernel(int f, float *__restrict__ scales, int64_t ng) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < ng;
+         i += (int64_t)gridDim.x * blockDim.x)
+        scales[i] = group_scale(f, scales[i]);
+}
+
+// ------------------------------------------------------------ dequantize
+
+// One element per thread: src/quantize.rs:324-332, :377-396, :440-454,
+// :498-512 (data[i/2], scales[min(i/group, ns-1)]), :538-554 (GGUF Q4_0 block
+// offsets), :604-610, :627-632.
+__global__ void qt_dequant_kernel(int f, const uint8_t *__restrict__ data,
+                                  const float *__restrict__ scales, int64_t ns, int64_t g,
+                                  int64_t n, float *__restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float v;
+        if (f == RNN_QF_FP16 || f == RNN_QF_BF16) {
+            const uint32_t h = (uint32_t)data[2 * i] | ((uint32_t)data[2 * i + 1] << 8);
+            v = f == RNN_QF_FP16 ? f16_to_f32_rs(h) : __uint_as_float(h << 16);
+        } else if (f == RNN_QF_GGUF_Q4 || f == RNN_QF_GGUF_Q4K) {
+            const int64_t b = i / g, j = i - b * g;
+            const uint8_t byte = data[b * ((g + 1) / 2) + j / 2];
+            const int nib = (j & 1) ? (byte >> 4) : (byte & 0xF);
+            v = (float)((nib ^ 8) - 8) * scales[b];
+        } else {
+            const int64_t gi = i / g;
+            const float s = scales[gi < ns - 1 ? gi : ns - 1];
+            if (f == RNN_QF_INT8 || f == RNN_QF_GGUF_Q8) {
+                v = (float)(int8_t)data[i] * s;
+            } else {
+                const uint8_t byte = data[i / 2];
+                const int nib = (i & 1) ? (byte >> 4) : (byte & 0xF);
+                if (f == RNN_QF_INT4) v = (float)((nib ^ 8) - 8) * s;
+                else if (f == RNN_QF_NF4) v = kNF4[nib] * s;
+                else v = kE2M1[nib] * s;
+            }
+        }
+        out[i] = v;
+    }
+}
+
+// ------------------------------------------------------------ fused GEMV
+
+// QuantizedLinear::forward (src/quantize.rs:744-754) for few rows of x:
+// y[m, o] = sum_k x[m, k] * W[o, k] + bias[o] with W decoded from its codes
+// in registers. Each wave owns R consecutive output rows; per 2048-wide K
+// slice, lane l holds x[m, 32 l .. 32 l + 31] for the MT rows of x in
+// registers and streams the matching 32 codes of each of its rows (16, 32 or
+// 64 bytes, non-temporal: every weight byte is read once). The 32 products of
+// a chunk are summed first and scaled once by the group's scale (the group
+// size is a multiple of 32, so a chunk never spans two groups); the wave then
+// reduces its R x MT partial sums across lanes.
+template <int KIND>
+struct ChunkLoad {
+    static constexpr int NV = KIND == KIND_I4 ? 1 : (KIND == KIND_I8 ? 2 : 4);  // uint4 per chunk
+    static constexpr int BYTES_PER_32 = 16 * NV;
+};
+
+template <int KIND>
+__device__ inline void decode32(const v4i *raw, float *v) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(raw);
+    if (KIND == KIND_I4) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[8 * d + i] = (float)(((int32_t)(w[d] << (28 - 4 * i))) >> 28);
+    } else if (KIND == KIND_I8) {
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[4 * d + i] = (float)(int8_t)(w[d] >> (8 * i));
+    } else if (KIND == KIND_F16) {
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            v[2 * d] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w[d] & 0xFFFFu));
+            v[2 * d + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w[d] >> 16));
+        }
+    } else {
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            v[2 * d] = __uint_as_float(w[d] << 16);
+            v[2 * d + 1] = __uint_as_float(w[d] & 0xFFFF0000u);
+        }
+    }
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <int KIND, int MT, int R, bool SCALED, bool BIAS>
+__global__ __launch_bounds__(256) void qt_gemv_kernel(
+    const float *__restrict__ x, int mrows, int64_t K, const uint8_t *__restrict__ data,
+    const float *__restrict__ scales, int64_t ns, int64_t g, int64_t N,
+    const float *__restrict__ bias, float *__restrict__ y) {
+    using CL = ChunkLoad<KIND>;
+    const int lane = threadIdx.x % 64;
+    const int64_t r0 = (blockIdx.x * 4 + threadIdx.x / 64) * (int64_t)R;
+    if (r0 >= N) return;
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+
+    for (int64_t kb = 0; kb < K; kb += 2048) {
+        const int64_t kc = kb + 32 * lane;
+        const bool act = kc < K;
+        const int64_t kk = act ? kc : kb;  // idle lanes re-read a valid chunk
+        v4i raw[R][CL::NV];
+        float sc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t row = r0 + r < N ? r0 + r : N - 1;
+            const int64_t flat = row * K + kk;
+            const v4i *p = reinterpret_cast<const v4i *>(data + flat * CL::BYTES_PER_32 / 32);
+#pragma unroll
+            for (int j = 0; j < CL::NV; ++j) raw[r][j] = __builtin_nontemporal_load(p + j);
+            if (SCALED) {
+                const int64_t gi = flat / g;
+                sc[r] = scales[gi < ns - 1 ? gi : ns - 1];
+            }
+        }
+        float xr[MT][32];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int mr = m < mrows ? m : 0;
+            const float4 *xp = reinterpret_cast<const float4 *>(x + (int64_t)mr * K + kk);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 t = xp[j];
+                xr[m][4 * j] = t.x, xr[m][4 * j + 1] = t.y, xr[m][4 * j + 2] = t.z,
+                xr[m][4 * j + 3] = t.w;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float v[32];
+            decode32<KIND>(raw[r], v);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float p = xr[m][0] * v[0];
+#pragma unroll
+                for (int j = 1; j < 32; ++j) p = __builtin_fmaf(xr[m][j], v[j], p);
+                p = act ? p : 0.0f;
+                acc[r][m] = SCALED ? __builtin_fmaf(sc[r], p, acc[r][m]) : acc[r][m] + p;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = r0 + r;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float s = wave_sum(acc[r][m]);
+            if (lane == r * MT + m && row < N && m < mrows) {
+                if (BIAS) s = s + bias[row];
+                y[(int64_t)m * N + row] = s;
+            }
+        }
+    }
+}
+
+__global__ void qt_bias_kernel(float *__restrict__ y, int64_t m, int64_t n,
+                               const float *__restrict__ bias) {
+    const int64_t total = m * n;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = y[i] + bias[i % n];
+}
+
+int grid_for(int64_t work, int per_block) {
+    return (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(work, per_block),
+                                                       (int64_t)8 * device_cu_count()));
+}
+
+}  // namespace rnn
+
+using namespace rnn;
+
+extern "C" int rnn_qt_layout(int format, int64_t n, int64_t group_size, int64_t *data_bytes,
+                             int64_t *n_scales, int64_t *stored_group) {
+    RNN_REQUIRE(format >= RNN_QF_FP16 && format <= RNN_QF_GGUF_Q8, "rnn_qt_layout: bad format %d",
+                format);
+    RNN_REQUIRE(n >= 0 && group_size >= 0, "rnn_qt_layout: negative size");
+    RNN_REQUIRE(data_bytes && n_scales && stored_group, "rnn_qt_layout: null pointer");
+    if (format == RNN_QF_FP16 || format == RNN_QF_BF16) {
+        *data_bytes = 2 * n, *n_scales = 0, *stored_group = 0;
+        return RNN_OK;
+    }
+    int64_t g = group_size == 0 ? n : group_size;
+    if (qf_is_gguf(format)) g = std::min<int64_t>(g, 32);
+    // group_size 0 on an empty tensor divides by zero in the reference
+    // (n.div_ceil(0), src/quantize.rs:298)
+    RNN_REQUIRE(g > 0, "rnn_qt_layout: group size 0 with n = 0");
+    const int64_t ng = ceil_div(n, g);
+    *stored_group = g, *n_scales = ng;
+    if (!qf_is4(format)) *data_bytes = n;
+    else *data_bytes = ng == 0 ? 0 : (ng - 1) * ((g + 1) / 2) + (n - (ng - 1) * g + 1) / 2;
+    return RNN_OK;
+}
+
+extern "C" int rnn_qt_quantize(int format, const float *x, int64_t n, int64_t group_size,
+                               uint8_t *data, float *scales, void *stream) {
+    int64_t nb, ng, g;
+    RNN_TRY(rnn_qt_layout(format, n, group_size, &nb, &ng, &g));
+    if (n == 0) return RNN_OK;
+    RNN_REQUIRE(x && data, "rnn_qt_quantize: null pointer");
+    hipStream_t st = as_stream(stream);
+    if (format == RNN_QF_FP16 || format == RNN_QF_BF16) {
+        qt_half_quant_kernel<<<grid_for(n, 256), 256, 0, st>>>(format, x, n,
+                                                               reinterpret_cast<uint16_t *>(data));
+        return check_launch("rnn_qt_quantize");
+    }
+    RNN_REQUIRE(scales != nullptr, "rnn_qt_quantize: null scales");
+    if (g <= kSmallGroup) {
+        RNN_REQUIRE(ceil_div(ng, 4) <= 0x7fffffff, "rnn_qt_quantize: too many groups");
+        qt_quant_group_kernel<<<(unsigned)ceil_div(ng, 4), 256, 0, st>>>(format, x, n, g, ng, data,
+                                                                        scales);
+        return check_launch("rnn_qt_quantize");
+    }
+    const int64_t cpg = ceil_div(g, kChunk);
+    RNN_REQUIRE(ng * cpg <= 0x7fffffff, "rnn_qt_quantize: tensor too large");
+    qt_zero_kernel<<<grid_for(ng, 256), 256, 0, st>>>(reinterpret_cast<uint32_t *>(scales), ng);
+    qt_group_max_kernel<<<(unsigned)(ng * cpg), 256, 0, st>>>(
+        x, n, g, cpg, reinterpret_cast<uint32_t *>(scales));
+    qt_big_codes_kernel<<<(unsigned)(ng * cpg), 256, 0, st>>>(format, x, n, g, cpg, scales, data);
+    qt_finish_scales_kernel<<<grid_for(ng, 256), 256, 0, st>>>(format, scales, ng);
+    return check_launch("rnn_qt_quantize");
+}
+
+static int check_tensor(const char *name, int format, const uint8_t *data, int64_t data_bytes,
+                        const float *scales, int64_t n_scales, int64_t group, int64_t n) {
+    RNN_REQUIRE(format >= RNN_QF_FP16 && format <= RNN_QF_GGUF_Q8, "%s: bad format %d", name,
+                format);
+    RNN_REQUIRE(n >= 0 && data_bytes >= 0 && n_scales >= 0 && group >= 0, "%s: negative size",
+                name);
+    if (n == 0) return RNN_OK;
+    RNN_REQUIRE(data != nullptr, "%s: null data", name);
+    if (format == RNN_QF_FP16 || format == RNN_QF_BF16) {
+        RNN_REQUIRE(data_bytes >= 2 * n, "%s: data holds %lld bytes, needs %lld", name,
+                    (long long)data_bytes, (long long)(2 * n));
+        return RNN_OK;
+    }
+    // the reference indexes scales[] and data[] without checks and panics on
+    // a short array; here the same conditions are errors
+    RNN_REQUIRE(group > 0, "%s: group size 0", name);
+    RNN_REQUIRE(scales != nullptr && n_scales > 0, "%s: no scales", name);
+    int64_t need;
+    if (format == RNN_QF_GGUF_Q4 || format == RNN_QF_GGUF_Q4K) {
+        RNN_REQUIRE(n_scales >= ceil_div(n, group), "%s: %lld scales for %lld blocks", name,
+                    (long long)n_scales, (long long)ceil_div(n, group));
+        const int64_t nbk = ceil_div(n, group);
+        need = (nbk - 1) * ((group + 1) / 2) + (n - (nbk - 1) * group + 1) / 2;
+    } else {
+        need = qf_is4(format) ? (n + 1) / 2 : n;
+    }
+    RNN_REQUIRE(data_bytes >= need, "%s: data holds %lld bytes, needs %lld", name,
+                (long long)data_bytes, (long long)need);
+    return RNN_OK;
+}
+
+extern "C" int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
+                                 const float *scales, int64_t n_scales, int64_t group, int64_t n,
+                                 float *out, void *stream) {
+    RNN_TRY(check_tensor("rnn_qt_dequantize", format, data, data_bytes, scales, n_scales, group, n));
+    if (n == 0) return RNN_OK;
+    RNN_REQUIRE(out != nullptr, "rnn_qt_dequantize: null out");
+    qt_dequant_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(format, data, scales,
+                                                                       n_scales, group, n, out);
+    return check_launch("rnn_qt_dequantize");
+}
+
+template <int KIND, int MT, int R, bool SCALED>
+static void launch_gemv(const float *x, int mrows, int64_t K, const uint8_t *data,
+                        const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
+                        float *y, hipStream_t st) {
+    const unsigned blocks = (unsigned)ceil_div(ceil_div(N, R), 4);
+    if (bias)
+        qt_gemv_kernel<KIND, MT, R, SCALED, true><<<blocks, 256, 0, st>>>(x, mrows, K, data, scales,
+                                                                          ns, g, N, bias, y);
+    else
+        qt_gemv_kernel<KIND, MT, R, SCALED, false><<<blocks, 256, 0, st>>>(x, mrows, K, data, scales,
+                                                                           ns, g, N, bias, y);
+}
+
+template <int KIND, bool SCALED>
+static void gemv_chunk(int mt, const float *x, int64_t K, const uint8_t *data, const float *scales,
+                       int64_t ns, int64_t g, int64_t N, const float *bias, float *y,
+                       hipStream_t st) {
+    constexpr int R4 = KIND == KIND_I4 || KIND == KIND_I8 ? 4 : 2;
+    if (mt == 1) launch_gemv<KIND, 1, 8, SCALED>(x, 1, K, data, scales, ns, g, N, bias, y, st);
+    else if (mt == 2) launch_gemv<KIND, 2, 8, SCALED>(x, 2, K, data, scales, ns, g, N, bias, y, st);
+    else launch_gemv<KIND, 4, R4, SCALED>(x, mt, K, data, scales, ns, g, N, bias, y, st);
+}
+
+// The fused path takes formats whose codes decode without a table, K a
+// multiple of 32, 16-byte aligned x and data, and (for scaled formats) a
+// group that is a multiple of 32.
+static int gemv_kind(int format) {
+    switch (format) {
+    case RNN_QF_INT4: case RNN_QF_GGUF_Q4: case RNN_QF_GGUF_Q4K: return KIND_I4;
+    case RNN_QF_INT8: case RNN_QF_GGUF_Q8: return KIND_I8;
+    case RNN_QF_FP16: return KIND_F16;
+    case RNN_QF_BF16: return KIND_BF16;
+    default: return -1;
+    }
+}
+
+extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,
+                                     const uint8_t *data, int64_t data_bytes, const float *scales,
+                                     int64_t n_scales, int64_t group, int64_t out_f,
+                                     const float *bias, float *y, unsigned flags, void *stream) {
+    const char *name = "rnn_qt_linear_forward";
+    RNN_REQUIRE(m >= 0 && in_f >= 0 && out_f >= 0, "%s: negative size", name);
+    RNN_TRY(check_tensor(name, format, data, data_bytes, scales, n_scales, group, out_f * in_f));
+    const unsigned algo = flags & RNN_ALGO_MASK;
+    RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_GEMV || algo == RNN_ALGO_TILED,
+                "%s: bad algo 0x%x", name, algo);
+    if (m == 0 || out_f == 0) return RNN_OK;
+    RNN_REQUIRE(y != nullptr && (in_f == 0 || x != nullptr), "%s: null pointer", name);
+    hipStream_t st = as_stream(stream);
+    if (in_f == 0) {  // empty sum: y = 0 (+ bias)
+        qt_zero_kernel<<<grid_for(m * out_f, 256), 256, 0, st>>>(reinterpret_cast<uint32_t *>(y),
+                                                                   m * out_f);
+        if (bias) qt_bias_kernel<<<grid_for(m * out_f, 256), 256, 0, st>>>(y, m, out_f, bias);
+        return check_launch(name);
+    }
+    const int kind = gemv_kind(format);
+    const bool scaled = format != RNN_QF_FP16 && format != RNN_QF_BF16;
+    const bool fits = kind >= 0 && in_f % 32 == 0 && (!scaled || group % 32 == 0) &&
+                      ((uintptr_t)x % 16) == 0 && ((uintptr_t)data % 16) == 0 &&
+                      ceil_div(ceil_div(out_f, 2), 4) <= 0x7fffffff;
+    const bool gemv = algo == RNN_ALGO_GEMV || (algo == RNN_ALGO_AUTO && m <= 16 && fits);
+    if (gemv) {
+        RNN_REQUIRE(fits, "%s: the fused GEMV needs an INT4/INT8/GGUF/FP16/BF16 format, in_f %% 32 "
+                    "== 0, group %% 32 == 0 and 16-byte aligned x and data", name);
+        for (int64_t m0 = 0; m0 < m; m0 += 4) {
+            const int mt = (int)std::min<int64_t>(4, m - m0);
+            const float *xs = x + m0 * in_f;
+            float *ys = y + m0 * out_f;
+            switch (kind) {
+            case KIND_I4:
+                gemv_chunk<KIND_I4, true>(mt, xs, in_f, data, scales, n_scales, group, out_f, bias,
+                                          ys, st);
+                break;
+            case KIND_I8:
+                gemv_chunk<KIND_I8, true>(mt, xs, in_f, data, scales, n_scales, group, out_f, bias,
+                                          ys, st);
+                break;
+            case KIND_F16:
+                gemv_chunk<KIND_F16, false>(mt, xs, in_f, data, scales, n_scales, 1, out_f, bias,
+                                            ys, st);
+                break;
+            default:
+                gemv_chunk<KIND_BF16, false>(mt, xs, in_f, data, scales, n_scales, 1, out_f, bias,
+                                             ys, st);
+                break;
+            }
+            RNN_TRY(check_launch(name));
+        }
+        return RNN_OK;
+    }
+    // Otherwise: W = dequantize() into stream-ordered scratch, y = x . W^T on
+    // the f32 MFMA GEMM, then + bias -- the reference's own three steps.
+    void *w = nullptr;
+    RNN_TRY(check_hip(hipMallocAsync(&w, sizeof(float) * out_f * in_f, st), name));
+    int rc = rnn_qt_dequantize(format, data, data_bytes, scales, n_scales, group, out_f * in_f,
+                               static_cast<float *>(w), stream);
+    if (rc == RNN_OK)
+        rc = rnn_sgemm(0, 1, m, out_f, in_f, 1.0f, x, in_f, static_cast<const float *>(w), in_f,
+                       0.0f, y, out_f, stream);
+    if (rc == RNN_OK && bias) {
+        qt_bias_kernel<<<grid_for(m * out_f, 256), 256, 0, st>>>(y, m, out_f, bias);
+        rc = check_launch(name);
+    }
+    const int rf = check_hip(hipFreeAsync(w, st), name);
+    return rc != RNN_OK ? rc : rf;
+}

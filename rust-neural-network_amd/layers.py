@@ -1,7 +1,9 @@
 """Layer-level mirrors of rust-nn's quantized inference types over the HIP
 library: `Int8Weights` / `Int8Linear` (src/int8.rs:11-172), `TernaryTensor` /
-`TernaryLinear` / `TernaryModel` (src/ternary.rs:81-362), and `Int8Model`, the
-int8 counterpart of `TernaryModel::from_model` that the reference does not have.
+`TernaryLinear` / `TernaryModel` (src/ternary.rs:81-362), `QuantizedTensor` /
+`QuantizedLinear` / `QuantizedModel` (src/quantize.rs:214-816), and
+`Int8Model`, the int8 counterpart of `TernaryModel::from_model` that the
+reference does not have.
 
 Every tensor here is a torch device tensor; weights, codes and scales stay in
 HBM for the life of a layer, and a model's forward keeps its activations on the
@@ -238,3 +240,129 @@ class TernaryModel:
         for i, layer in enumerate(self.layers):
             x = layer.forward_int8(x, relu=relu_between and i + 1 < len(self.layers))
         return x
+
+
+# ------------------------------------------------------------------ QuantizedTensor
+QF_NAMES = {H.QF_FP16: "FP16", H.QF_BF16: "BF16", H.QF_INT8: "INT8", H.QF_INT4: "INT4",
+            H.QF_NF4: "NF4 (NormalFloat 4-bit)", H.QF_NVFP4: "NVFP4 (NVIDIA FP4 E2M1)",
+            H.QF_GGUF_Q4: "GGUF Q4_0", H.QF_GGUF_Q4K: "GGUF Q4_K", H.QF_GGUF_Q8: "GGUF Q8_0"}
+
+
+def qf_bits(fmt):
+    """QuantFormat::bits (src/quantize.rs:60-71)."""
+    if fmt in (H.QF_FP16, H.QF_BF16):
+        return 16
+    if fmt in (H.QF_INT8, H.QF_GGUF_Q8):
+        return 8
+    return 4
+
+
+def qf_compression_ratio(fmt):
+    """QuantFormat::compression_ratio (src/quantize.rs:73-75)."""
+    return 32.0 / qf_bits(fmt)
+
+
+def pair_parameters_quantized(n_params):
+    """The pairing of `QuantizedModel::from_model` (src/quantize.rs:758-789):
+    parameter i is a weight and parameter i+1, whatever its shape, its bias;
+    a trailing weight has none. Returns (weight index, bias index or None)."""
+    pairs, i = [], 0
+    while i < n_params:
+        b = i + 1 if i + 1 < n_params else None
+        pairs.append((i, b))
+        i += 2 if b is not None else 1
+    return pairs
+
+
+class QuantizedTensor:
+    """src/quantize.rs:214-227: `format`, packed `data` bytes, per-group
+    `scales`, original `shape`, and the stored `group_size` (the GGUF block)."""
+
+    def __init__(self, fmt, data, scales, shape, group_size):
+        self.format, self.data, self.scales = fmt, data, scales
+        self.shape, self.group_size = tuple(shape), group_size
+
+    @classmethod
+    def quantize(cls, tensor, fmt, group_size):
+        """QuantizedTensor::quantize (src/quantize.rs:231-250)."""
+        data, scales, g = H.qt_quantize(fmt, tensor.contiguous(), group_size)
+        return cls(fmt, data, scales, tensor.shape, g)
+
+    def numel(self):
+        n = 1
+        for d in self.shape:
+            n *= d
+        return n
+
+    def dequantize(self):
+        """QuantizedTensor::dequantize (src/quantize.rs:252-269)."""
+        return H.qt_dequantize(self.format, self.data, self.scales, self.group_size,
+                               self.numel()).reshape(self.shape)
+
+    def mem_bytes(self):
+        """src/quantize.rs:271-274."""
+        return self.data.numel() + 4 * self.scales.numel()
+
+    def compression_ratio(self):
+        """src/quantize.rs:276-280."""
+        return self.numel() * 4 / self.mem_bytes()
+
+    def quantization_error(self, original):
+        """src/quantize.rs:282-293."""
+        return _mean_abs_diff(original, self.dequantize())
+
+
+class QuantizedLinear:
+    """src/quantize.rs:718-754: a quantized weight `[out, in]` and optional
+    f32 bias. `forward` decodes the weight inside the GEMV (or dequantizes
+    once and runs the f32 GEMM for many rows)."""
+
+    def __init__(self, weight, bias, in_features, out_features):
+        self.weight, self.bias = weight, bias
+        self.in_features, self.out_features = in_features, out_features
+
+    @classmethod
+    def from_linear(cls, weight, bias, fmt, group_size):
+        """QuantizedLinear::from_linear (src/quantize.rs:727-741)."""
+        return cls(QuantizedTensor.quantize(weight, fmt, group_size), bias, weight.shape[1],
+                   weight.shape[0])
+
+    def forward(self, x):
+        """QuantizedLinear::forward (src/quantize.rs:744-754)."""
+        w = self.weight
+        return H.qt_linear_forward(w.format, x.reshape(-1, self.in_features).contiguous(),
+                                   w.data, w.scales, w.group_size, self.out_features, self.bias)
+
+
+class QuantizedModel:
+    """src/quantize.rs:712-816."""
+
+    def __init__(self, layers, fmt):
+        self._layers, self.format = layers, fmt
+
+    @classmethod
+    def from_model(cls, params, fmt, group_size):
+        """QuantizedModel::from_model (src/quantize.rs:758-789) over
+        `Module::parameters()`."""
+        layers = []
+        for wi, bi in pair_parameters_quantized(len(params)):
+            w = params[wi]
+            q = QuantizedTensor.quantize(w, fmt, group_size)
+            bias = None if bi is None else params[bi].reshape(-1).contiguous()
+            out_f = w.shape[0] if w.dim() > 0 else 0
+            in_f = w.shape[1] if w.dim() > 1 else 0
+            layers.append(QuantizedLinear(q, bias, in_f, out_f))
+        return cls(layers, fmt)
+
+    def layers(self):
+        return self._layers
+
+    def mem_bytes(self):
+        """src/quantize.rs:791-797."""
+        return sum(l.weight.mem_bytes() + (0 if l.bias is None else 4 * l.bias.numel())
+                   for l in self._layers)
+
+    def compression_ratio(self):
+        """src/quantize.rs:799-807."""
+        elems = sum(l.weight.numel() for l in self._layers)
+        return elems * 4 / max(self.mem_bytes(), 1)

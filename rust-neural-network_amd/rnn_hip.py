@@ -30,6 +30,9 @@ ALGO_TILED_DMA = 0x30
 TERNARY_ROWS = 0
 TERNARY_ABSMEAN = 1
 
+# QuantFormat (src/quantize.rs:37-56), declaration order
+QF_FP16, QF_BF16, QF_INT8, QF_INT4, QF_NF4, QF_NVFP4, QF_GGUF_Q4, QF_GGUF_Q4K, QF_GGUF_Q8 = range(9)
+
 # blas::Transpose (src/blas.rs:72-77)
 NO_TRANS = 0
 TRANS = 1
@@ -66,6 +69,11 @@ SIGNATURES = {
     "rnn_rotor_rotation_matrices": ([_P, _I64, _P, _P], _INT),
     "rnn_rotorquant_quantize": ([_P, _I64, _I64, _INT, _P, _P, _P, _P, _P], _INT),
     "rnn_rotorquant_dequantize": ([_P, _P, _I64, _I64, _P, _P, _P], _INT),
+    "rnn_qt_layout": ([_INT, _I64, _I64, _P, _P, _P], _INT),
+    "rnn_qt_quantize": ([_INT, _P, _I64, _I64, _P, _P, _P], _INT),
+    "rnn_qt_dequantize": ([_INT, _P, _I64, _P, _I64, _I64, _I64, _P, _P], _INT),
+    "rnn_qt_linear_forward": ([_INT, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P,
+                               _UINT, _P], _INT),
     "rnn_sgemm": ([_INT, _INT, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P, _I64,
                    ctypes.c_float, _P, _I64, _P], _INT),
 }
@@ -344,3 +352,52 @@ class HipBackend:
 
     def sgemm(self, transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc):
         return sgemm(transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc)
+
+
+# ------------------------------------------------------------------ QuantizedTensor
+def qt_layout(fmt, n, group_size):
+    """(data bytes, scales.len(), stored group_size) of QuantizedTensor::quantize
+    (src/quantize.rs:231-250)."""
+    out = (ctypes.c_int64 * 3)()
+    base = ctypes.addressof(out)
+    _check(load().rnn_qt_layout(fmt, n, group_size, ctypes.c_void_p(base),
+                                ctypes.c_void_p(base + 8), ctypes.c_void_p(base + 16)))
+    return int(out[0]), int(out[1]), int(out[2])
+
+
+def qt_quantize(fmt, x, group_size, stream=None):
+    """QuantizedTensor::quantize of the flat data of device tensor x. Returns
+    (data uint8 [bytes], scales f32 [groups], stored group_size)."""
+    import torch
+    _dev(x, torch.float32, "x")
+    n = x.numel()
+    nb, ns, g = qt_layout(fmt, n, group_size)
+    data = _empty((nb,), torch.uint8, x)
+    scales = _empty((ns,), torch.float32, x)
+    _check(load().rnn_qt_quantize(fmt, _ptr(x), n, group_size, _ptr(data), _ptr(scales),
+                                  _stream(stream)))
+    return data, scales, g
+
+
+def qt_dequantize(fmt, data, scales, group, n, stream=None):
+    """QuantizedTensor::dequantize (src/quantize.rs:252-269): flat f32 [n]."""
+    import torch
+    _dev(data, torch.uint8, "data"), _dev(scales, torch.float32, "scales")
+    out = _empty((n,), torch.float32, data)
+    _check(load().rnn_qt_dequantize(fmt, _ptr(data), data.numel(), _ptr(scales), scales.numel(),
+                                    group, n, _ptr(out), _stream(stream)))
+    return out
+
+
+def qt_linear_forward(fmt, x, data, scales, group, out_f, bias=None, algo=ALGO_AUTO, y=None,
+                      stream=None):
+    """QuantizedLinear::forward (src/quantize.rs:744-754): x [m, in] -> y [m, out]."""
+    import torch
+    _dev(x, torch.float32, "x"), _dev(data, torch.uint8, "data")
+    _dev(scales, torch.float32, "scales"), _dev(bias, torch.float32, "bias")
+    m, in_f = x.shape
+    y = y if y is not None else _empty((m, out_f), torch.float32, x)
+    _check(load().rnn_qt_linear_forward(fmt, _ptr(x), m, in_f, _ptr(data), data.numel(),
+                                        _ptr(scales), scales.numel(), group, out_f, _ptr(bias),
+                                        _ptr(y), algo, _stream(stream)))
+    return y

@@ -1,0 +1,238 @@
+"""GPU parity of the QuantizedTensor formats (src/quantize.rs) through the C
+ABI against the oracle.
+
+- quantize: data bytes and scales bit-exact, every format, ragged groups
+  (odd sizes, a short last group, group 0 = whole tensor, groups above the
+  one-wave-per-group limit), zero groups, NaN/Inf/signed zero, half and
+  bfloat edge values;
+- dequantize: bit-exact on the oracle's codes, including a shortened scales
+  array (scales[min(i/group, len-1)]) and the odd-group 4-bit layout;
+- QuantizedLinear::forward: f32 sums in the kernel's own order, so the bar is
+  the GEMM rounding bound |got - exact| <= gamma_(k+2) * sum |x||W| (+ |b| u)
+  around the float64 product of the oracle's dequantized weight (gamma_j =
+  j u / (1 - j u), u = 2^-24); both the fused GEMV and the dequantize +
+  f32 GEMM path are forced on the same inputs.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ALL = [O.QF_FP16, O.QF_BF16, O.QF_INT8, O.QF_INT4, O.QF_NF4, O.QF_NVFP4, O.QF_GGUF_Q4,
+       O.QF_GGUF_Q4K, O.QF_GGUF_Q8]
+GEMV_FMTS = [O.QF_INT4, O.QF_INT8, O.QF_GGUF_Q4, O.QF_GGUF_Q8, O.QF_FP16, O.QF_BF16]
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def weights(n, seed, scale=0.02):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(n) * scale).astype(np.float32)
+
+
+def special(n, seed):
+    """Normal data with zero runs, NaN, +-Inf, signed zeros, huge/tiny values
+    and exact code midpoints."""
+    x = weights(n, seed, 1.0)
+    rng = np.random.default_rng(seed + 1)
+    idx = rng.choice(n, size=min(n, 40), replace=False)
+    vals = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 3e38, -3e38, 1e-40, -1e-42, 65504.0,
+                     65520.0, 6e-8, 0.5, -0.5, 1.5, 2.5], np.float32)
+    x[idx] = vals[np.arange(idx.size) % vals.size]
+    if n >= 96:
+        x[32:64] = 0.0
+    return x
+
+
+def check_quantize(hip, dev, fmt, x, gs):
+    d, s, g = hip.qt_quantize(fmt, to_dev(x, dev), gs)
+    de, se, ge = O.qt_quantize(fmt, x, gs)
+    assert g == ge
+    assert np.array_equal(host(d), de), f"{O.QF_NAMES[fmt]}: codes differ"
+    assert np.array_equal(host(s).view(np.uint32), se.view(np.uint32)), "scales differ"
+    out = host(hip.qt_dequantize(fmt, d, s, g, x.size))
+    exp = O.qt_dequantize(fmt, de, se, ge, x.size)
+    assert np.array_equal(out.view(np.uint32), exp.view(np.uint32)), "dequantize differs"
+
+
+@pytest.mark.parametrize("fmt", ALL, ids=[O.QF_NAMES[f] for f in ALL])
+@pytest.mark.parametrize("n,gs", [(4096, 32), (4096, 128), (1000, 33), (999, 7), (77, 0),
+                                  (1, 0), (5, 64), (20000, 10000), (30001, 0), (65, 64)])
+def test_quantize_dequantize_parity(dev, hip, fmt, n, gs):
+    check_quantize(hip, dev, fmt, weights(n, n * 13 + gs), gs)
+
+
+@pytest.mark.parametrize("fmt", ALL, ids=[O.QF_NAMES[f] for f in ALL])
+def test_quantize_special_values(dev, hip, fmt):
+    for n, gs in ((4096, 32), (333, 11), (9000, 0)):
+        check_quantize(hip, dev, fmt, special(n, n + gs), gs)
+
+
+def test_half_conversions_every_pattern(dev, hip):
+    """FP16/BF16 dequantize of all 65,536 bit patterns, and quantize of their
+    f32 values plus random floats of every magnitude."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    for fmt in (O.QF_FP16, O.QF_BF16):
+        out = host(hip.qt_dequantize(fmt, to_dev(h.view(np.uint8), dev),
+                                     to_dev(np.zeros(1, np.float32), dev), 0, h.size))
+        exp = O.qt_dequantize(fmt, h.view(np.uint8), np.zeros(0, np.float32), 0, h.size)
+        assert np.array_equal(out.view(np.uint32), exp.view(np.uint32))
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(50000) * 10.0 ** rng.uniform(-45, 38, 50000)).astype(np.float32)
+    x = np.concatenate([x, h.view(np.float16).astype(np.float32),
+                        np.array([0x7F800001, 0xFFFFFFFF, 0x7FC00000], np.uint32).view(np.float32)])
+    for fmt in (O.QF_FP16, O.QF_BF16):
+        check_quantize(hip, dev, fmt, x, 0)
+
+
+def test_dequantize_short_scales_and_odd_groups(dev, hip):
+    """scales[min(i/group, len-1)] with a caller-shortened scales array, and
+    the odd-group INT4 layout read through data[i/2] (src/quantize.rs:377-396)."""
+    x = weights(1001, 5, 1.0)
+    for fmt in (O.QF_INT8, O.QF_INT4, O.QF_NF4, O.QF_NVFP4):
+        d, s, g = O.qt_quantize(fmt, x, 33)
+        for ns in (s.size, 5, 1):
+            out = host(hip.qt_dequantize(fmt, to_dev(d, dev), to_dev(s[:ns], dev), g, x.size))
+            exp = O.qt_dequantize(fmt, d, s[:ns], g, x.size)
+            assert np.array_equal(out.view(np.uint32), exp.view(np.uint32))
+
+
+def test_argument_errors(dev, hip):
+    import torch
+    x = torch.zeros(64, device=dev)
+    with pytest.raises(hip.RnnError):
+        hip.qt_quantize(99, x, 32)
+    d, s, g = hip.qt_quantize(O.QF_INT4, x, 32)
+    with pytest.raises(hip.RnnError):          # data shorter than the tensor needs
+        hip.qt_dequantize(O.QF_INT4, d[:10], s, g, 64)
+    with pytest.raises(hip.RnnError):          # no scales
+        hip.qt_dequantize(O.QF_INT4, d, s[:0], g, 64)
+    xr = torch.zeros((2, 48), device=dev)
+    d, s, g = hip.qt_quantize(O.QF_INT4, torch.zeros(48 * 8, device=dev), 48)
+    with pytest.raises(hip.RnnError):          # forced GEMV: in_f % 32 != 0
+        hip.qt_linear_forward(O.QF_INT4, xr, d, s, g, 8, algo=hip.ALGO_GEMV)
+    with pytest.raises(hip.RnnError):          # NF4 has no fused GEMV
+        hip.qt_linear_forward(O.QF_NF4, torch.zeros((1, 64), device=dev), d, s, g, 3,
+                              algo=hip.ALGO_GEMV)
+
+
+# ------------------------------------------------------------------ linear forward
+def gemm_check(got, x, wdeq, bias):
+    xd, wd = x.astype(np.float64), wdeq.astype(np.float64)
+    exact = xd @ wd.T
+    scale = np.abs(xd) @ np.abs(wd).T
+    if bias is not None:
+        exact = exact + bias
+        scale = scale + np.abs(bias)
+    k = x.shape[1]
+    u = 2.0 ** -24
+    lim = (k + 2) * u / (1 - (k + 2) * u) * scale + 1e-30
+    err = np.abs(got.astype(np.float64) - exact)
+    assert np.all(err <= lim), f"max err {err.max():.3g}, worst excess {(err - lim).max():.3g}"
+
+
+@pytest.mark.parametrize("fmt", GEMV_FMTS, ids=[O.QF_NAMES[f] for f in GEMV_FMTS])
+@pytest.mark.parametrize("m,k,n,gs", [(1, 4096, 1000, 128), (3, 2048, 257, 32), (4, 64, 9, 64),
+                                      (8, 4096, 512, 32), (16, 2080, 130, 32), (2, 6144, 40, 0),
+                                      (5, 96, 1, 32)])
+def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
+    rng = np.random.default_rng(m * 1000 + k + n)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[:, :7] *= 20.0                                          # outlier channels
+    b = rng.standard_normal(n).astype(np.float32)
+    g0 = gs if gs else n * k
+    if fmt not in (O.QF_FP16, O.QF_BF16) and g0 % 32:
+        pytest.skip("group not a multiple of 32")
+    d, s, g = O.qt_quantize(fmt, w, gs)
+    wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
+    dd, sd, xd = to_dev(d, dev), to_dev(s if s.size else np.zeros(1, np.float32), dev), to_dev(x, dev)
+    for bias in (None, b):
+        bd = None if bias is None else to_dev(bias, dev)
+        for algo in (hip.ALGO_GEMV, hip.ALGO_TILED):
+            if algo == hip.ALGO_GEMV and m > 16:
+                continue
+            y = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd, algo=algo))
+            gemm_check(y, x, wdeq, bias)
+        auto = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd))
+        gemm_check(auto, x, wdeq, bias)
+
+
+@pytest.mark.parametrize("fmt", [O.QF_NF4, O.QF_NVFP4, O.QF_INT4],
+                         ids=["NF4", "NVFP4", "INT4-odd-group"])
+def test_linear_forward_dequant_path(dev, hip, fmt):
+    """Formats and groups outside the fused GEMV (table formats, a group that
+    is not a multiple of 32) take dequantize + f32 GEMM, for m = 1 and 40."""
+    rng = np.random.default_rng(fmt)
+    n, k = 70, 200
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    gs = 33 if fmt == O.QF_INT4 else 64
+    d, s, g = O.qt_quantize(fmt, w, gs)
+    wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
+    b = rng.standard_normal(n).astype(np.float32)
+    for m in (1, 40):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = host(hip.qt_linear_forward(fmt, to_dev(x, dev), to_dev(d, dev), to_dev(s, dev), g, n,
+                                       to_dev(b, dev)))
+        gemm_check(y, x, wdeq, b)
+        assert np.abs(y - O.qt_linear_forward(fmt, x, d, s, g, n, b)).max() < 1e-3
+
+
+def test_linear_forward_decode_config_sampled(dev, hip):
+    """The bench workload: INT4 group 128 and GGUF Q4_0/Q8_0 weights
+    [11008, 4096], x [1, 4096] and [4, 4096]; every output checked."""
+    rng = np.random.default_rng(77)
+    n, k = 11008, 4096
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    for fmt, gs in ((O.QF_INT4, 128), (O.QF_GGUF_Q4, 32), (O.QF_GGUF_Q8, 32)):
+        d, s, g = O.qt_quantize(fmt, w, gs)
+        dq, sq, _ = hip.qt_quantize(fmt, to_dev(w, dev), gs)
+        assert np.array_equal(host(dq), d) and np.array_equal(host(sq), s)
+        wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
+        for m in (1, 4):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            y = host(hip.qt_linear_forward(fmt, to_dev(x, dev), dq, sq, g, n))
+            gemm_check(y, x, wdeq, None)
+
+
+def test_quantized_layers(dev, hip):
+    """QuantizedTensor / QuantizedLinear / QuantizedModel mirrors
+    (src/quantize.rs:214-816): sizes, ratios, the from_model pairing and a
+    forward through each layer."""
+    import torch
+    import layers as L
+    rng = np.random.default_rng(3)
+    params = [rng.standard_normal((128, 64)).astype(np.float32) * 0.05,
+              rng.standard_normal(128).astype(np.float32),
+              rng.standard_normal((64, 128)).astype(np.float32) * 0.05,
+              rng.standard_normal(64).astype(np.float32)]
+    tp = [to_dev(p, dev) for p in params]
+    qm = L.QuantizedModel.from_model(tp, O.QF_INT4, 32)
+    assert len(qm.layers()) == 2
+    nbytes = sum(O.qt_layout(O.QF_INT4, p.size, 32)[0] + 4 * O.qt_layout(O.QF_INT4, p.size, 32)[1]
+                 for p in params[::2])
+    assert qm.mem_bytes() == nbytes + 4 * (128 + 64)
+    assert qm.compression_ratio() > 4.0                  # quantized_model_compression
+    x = rng.standard_normal((2, 64)).astype(np.float32)
+    h = x
+    for i, layer in enumerate(qm.layers()):
+        y = host(layer.forward(to_dev(h, dev)))
+        d, s, g = O.qt_quantize(O.QF_INT4, params[2 * i], 32)
+        wdeq = O.qt_dequantize(O.QF_INT4, d, s, g, params[2 * i].size).reshape(params[2 * i].shape)
+        gemm_check(y, h, wdeq, params[2 * i + 1])
+        h = y
+    qt = L.QuantizedTensor.quantize(tp[0], O.QF_NF4, 64)
+    assert qt.dequantize().shape == (128, 64)
+    assert abs(qt.compression_ratio() - 128 * 64 * 4 / (128 * 64 / 2 + 4 * 128)) < 1e-9
+    assert qt.quantization_error(tp[0]) < 0.05 * 0.2
+    ql = L.QuantizedLinear.from_linear(tp[2], None, O.QF_INT8, 0)   # quantized_linear_forward
+    assert tuple(ql.forward(torch.zeros((2, 128), device=dev)).shape) == (2, 64)

@@ -21,3 +21,14 @@ def test_pairs_without_bias_and_trailing_weight():
 def test_a_leading_1d_parameter_is_taken_as_a_weight():
     # the reference treats parameter i as a weight whatever its rank
     assert L.pair_parameters([(3,), (3,), (2, 3)]) == [(0, 1), (2, None)]
+
+
+def test_quantized_model_pairing():
+    """QuantizedModel::from_model (src/quantize.rs:762-787) takes parameter
+    i+1 as the bias of weight i whatever its shape, stepping by two; a
+    trailing weight has no bias."""
+    from layers import pair_parameters_quantized as P
+    assert P(4) == [(0, 1), (2, 3)]
+    assert P(3) == [(0, 1), (2, None)]
+    assert P(1) == [(0, None)]
+    assert P(0) == []
