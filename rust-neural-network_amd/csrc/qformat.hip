@@ -249,122 +249,299 @@ __global__ void qt_dequant_kernel(int f, const uint8_t *__restrict__ data,
 
 // QuantizedLinear::forward (src/quantize.rs:744-754) for few rows of x:
 // y[m, o] = sum_k x[m, k] * W[o, k] + bias[o] with W decoded from its codes
-// in registers. Each wave owns R consecutive output rows; per 2048-wide K
-// slice, lane l holds x[m, 32 l .. 32 l + 31] for the MT rows of x in
-// registers and streams the matching 32 codes of each of its rows (16, 32 or
-// 64 bytes, non-temporal: every weight byte is read once). The 32 products of
-// a chunk are summed first and scaled once by the group's scale (the group
-// size is a multiple of 32, so a chunk never spans two groups); the wave then
-// reduces its R x MT partial sums across lanes.
+// in registers.
+//
+// A workgroup of 4 waves owns 4R consecutive output rows, a wave R of them.
+// K is walked in slices of 2048 elements. In a slice each lane takes NV
+// 16-byte pieces of every row: piece j at byte j*1024 + 16*lane of the
+// slice, so one load instruction reads 1 KiB of whole cache lines
+// (non-temporal: each weight byte is read once). The slice of x (MT rows) is
+// staged once per workgroup in a double-buffered LDS ring, and the next
+// slice's weights are in flight while the current slice is computed. The EP
+// products of a piece are summed first and scaled once by the group's scale
+// (a piece never spans two groups: group % EP == 0). At the end the wave
+// reduces its R*MT partial sums with a halving butterfly.
 template <int KIND>
-struct ChunkLoad {
-    static constexpr int NV = KIND == KIND_I4 ? 1 : (KIND == KIND_I8 ? 2 : 4);  // uint4 per chunk
-    static constexpr int BYTES_PER_32 = 16 * NV;
+struct Fmt {
+    static constexpr int NV = KIND == KIND_I4 ? 1 : (KIND == KIND_I8 ? 2 : 4);  // pieces per lane
+    static constexpr int EP = 32 / NV;               // elements per 16-byte piece
+    static constexpr int PIECE_STRIDE = 1024 * EP / 16;  // elements between a lane's pieces
 };
 
+constexpr int kSlice = 2048;  // elements of K per slice (64 lanes x 32)
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Decodes one 16-byte piece into EP floats. INT4 nibbles are moved into the
+// high half of a byte, where the sign-extending byte conversion reads them
+// as exactly 16*q; the caller multiplies the piece's sum by 1/16.
 template <int KIND>
-__device__ inline void decode32(const v4i *raw, float *v) {
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(raw);
+__device__ __attribute__((always_inline)) inline void decode_piece(const v4i raw, float *v) {
     if (KIND == KIND_I4) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t w = (uint32_t)raw[d];
+            const uint32_t lo = (w << 4) & 0xF0F0F0F0u, hi = w & 0xF0F0F0F0u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                v[8 * d + 2 * b] = (float)(int8_t)(lo >> (8 * b));
+                v[8 * d + 2 * b + 1] = (float)(int8_t)(hi >> (8 * b));
+            }
+        }
+    } else if (KIND == KIND_I8) {
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[8 * d + i] = (float)(((int32_t)(w[d] << (28 - 4 * i))) >> 28);
-    } else if (KIND == KIND_I8) {
-#pragma unroll
-        for (int d = 0; d < 8; ++d)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[4 * d + i] = (float)(int8_t)(w[d] >> (8 * i));
+            for (int b = 0; b < 4; ++b) v[4 * d + b] = (float)(int8_t)((uint32_t)raw[d] >> (8 * b));
     } else if (KIND == KIND_F16) {
 #pragma unroll
-        for (int d = 0; d < 16; ++d) {
-            v[2 * d] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w[d] & 0xFFFFu));
-            v[2 * d + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w[d] >> 16));
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t w = (uint32_t)raw[d];
+            v[2 * d] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
+            v[2 * d + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
         }
     } else {
 #pragma unroll
-        for (int d = 0; d < 16; ++d) {
-            v[2 * d] = __uint_as_float(w[d] << 16);
-            v[2 * d + 1] = __uint_as_float(w[d] & 0xFFFF0000u);
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t w = (uint32_t)raw[d];
+            v[2 * d] = __uint_as_float(w << 16);
+            v[2 * d + 1] = __uint_as_float(w & 0xFFFF0000u);
         }
     }
 }
 
-__device__ inline float wave_sum(float v) {
+// Register state of one slice: the pieces of R rows and their scales.
+template <int KIND, int R>
+struct SliceRegs {
+    v4i raw[R][Fmt<KIND>::NV];
+    float sc[R][Fmt<KIND>::NV];
+};
+
+// Group index of element e of a row: rows hold whole groups (K % g == 0,
+// gbase = row * (K / g), per-piece term e / g) or groups hold whole rows
+// (g % K == 0, gbase = row / (g / K), per-piece term 0). Both avoid a 64-bit
+// division per load.
+template <int KIND, int R, bool SCALED>
+__device__ __attribute__((always_inline)) inline void load_slice(SliceRegs<KIND, R> &s, const uint8_t *__restrict__ data,
+                                  const float *__restrict__ scales, int64_t ns,
+                                  const int64_t (&gbase)[R], uint32_t g, bool rows_hold_groups,
+                                  int64_t K, int64_t N, int64_t r0, int64_t kb, int lane) {
+    using F = Fmt<KIND>;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    for (int j = 0; j < F::NV; ++j) {
+        int64_t e = kb + j * F::PIECE_STRIDE + lane * F::EP;
+        e = e < K ? e : kb;  // pieces past K (last slice) re-read a valid one
+        const uint32_t ge = SCALED && rows_hold_groups ? (uint32_t)e / g : 0u;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int64_t row = r0 + r < N ? r0 + r : N - 1;
+            const int64_t flat = row * K + e;
+            s.raw[r][j] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i *>(data + flat * 16 / F::EP));
+            if (SCALED) {
+                const int64_t gi = gbase[r] + ge;
+                s.sc[r][j] = scales[gi < ns - 1 ? gi : ns - 1];
+            }
+        }
+    }
 }
 
-template <int KIND, int MT, int R, bool SCALED, bool BIAS>
+// LDS layout of an x slice: the EP floats that lane l reads for piece j
+// start at j * PIECE_STRIDE + l * EP, and their float4 number q is stored at
+// slot q ^ swz(l), which spreads the lanes of one LDS pass over all banks
+// (lane strides of 128, 64 or 32 bytes would otherwise collide 8, 4 or 2
+// ways).
+template <int KIND>
+__device__ __attribute__((always_inline)) inline int x_swz(int lane) {
+    constexpr int EP = Fmt<KIND>::EP;
+    return (lane * EP / 64) & (EP / 4 - 1);
+}
+
+// Slot in the swizzled slice of the float4 holding slice elements [4p, 4p+4).
+template <int KIND>
+__device__ __attribute__((always_inline)) inline int x_slot(int p) {
+    using F = Fmt<KIND>;
+    const int o = 4 * p;
+    const int j = o / F::PIECE_STRIDE, w = o % F::PIECE_STRIDE;
+    const int lane = w / F::EP, q = (w % F::EP) / 4;
+    return j * F::PIECE_STRIDE + lane * F::EP + 4 * (q ^ x_swz<KIND>(lane));
+}
+
+// x[:, kb .. kb + 2048) of MT rows for an LDS buffer, 16 bytes per thread
+// per row of x.
+template <int MT>
+__device__ __attribute__((always_inline)) inline void stage_x_load(f4v (&t)[MT], const float *__restrict__ x, int mrows,
+                                    int64_t K, int64_t kb) {
+    const int64_t e = kb + 4 * (int64_t)threadIdx.x;  // 256 threads x 4 = 1024 ... x2 below
+    // Past K the load re-reads a valid address (no branch around it); those
+    // values reach only pieces whose sums compute_slice discards.
+    const int64_t ec = e < K ? e : 0;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int mr = m < mrows ? m : 0;
+        t[m] = *reinterpret_cast<const f4v *>(x + (int64_t)mr * K + ec);
+    }
+}
+
+template <int KIND, int MT, int R, bool SCALED>
+__device__ __attribute__((always_inline)) inline void compute_slice(const SliceRegs<KIND, R> &s, const float *__restrict__ xs,
+                                     int64_t K, int64_t kb, int lane, float (&acc)[R][MT]) {
+    using F = Fmt<KIND>;
+#pragma unroll
+    for (int j = 0; j < F::NV; ++j) {
+        const int off = j * F::PIECE_STRIDE + lane * F::EP;
+        const bool act = kb + off < K;
+        float xr[MT][F::EP];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int q = 0; q < F::EP / 4; ++q) {
+                const f4v t = *reinterpret_cast<const f4v *>(
+                    xs + m * kSlice + off + 4 * (q ^ x_swz<KIND>(lane)));
+                xr[m][4 * q] = t.x, xr[m][4 * q + 1] = t.y, xr[m][4 * q + 2] = t.z,
+                xr[m][4 * q + 3] = t.w;
+            }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            // one row at a time: without the barrier the scheduler decodes
+            // every row up front and the values of all rows stay live
+            __builtin_amdgcn_sched_barrier(0);
+            float v[F::EP];
+            decode_piece<KIND>(s.raw[r][j], v);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float p = xr[m][0] * v[0];
+#pragma unroll
+                for (int e = 1; e < F::EP; ++e) p = __builtin_fmaf(xr[m][e], v[e], p);
+                if (KIND == KIND_I4) p = p * 0.0625f;  // the codes were read as 16*q
+                p = act ? p : 0.0f;
+                acc[r][m] = SCALED ? __builtin_fmaf(s.sc[r][j], p, acc[r][m]) : acc[r][m] + p;
+            }
+        }
+    }
+}
+
+// SFIX = 1 or 2: K takes exactly that many slices and the body is straight
+// line; 0: any K, slices walked two at a time in a loop.
+template <int KIND, int MT, int R, bool SCALED, bool BIAS, int SFIX>
 __global__ __launch_bounds__(256) void qt_gemv_kernel(
     const float *__restrict__ x, int mrows, int64_t K, const uint8_t *__restrict__ data,
-    const float *__restrict__ scales, int64_t ns, int64_t g, int64_t N,
+    const float *__restrict__ scales, int64_t ns, uint32_t g, uint32_t kg, uint32_t rpg, int64_t N,
     const float *__restrict__ bias, float *__restrict__ y) {
-    using CL = ChunkLoad<KIND>;
+    // g: the group size; kg = K / g when rows hold whole groups, else 0 and
+    // rpg = g / K rows per group (both computed on the host)
+    constexpr int V = R * MT;
+    static_assert((V & (V - 1)) == 0 && V <= 64, "R*MT must be a power of two <= 64");
+    __shared__ __attribute__((aligned(16))) float xs[2][MT * kSlice];
     const int lane = threadIdx.x % 64;
-    const int64_t r0 = (blockIdx.x * 4 + threadIdx.x / 64) * (int64_t)R;
-    if (r0 >= N) return;
+    const int64_t r0 = (blockIdx.x * 4 + threadIdx.x / 64) * (int64_t)R;  // rows past N: clamped
     float acc[R][MT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 
-    for (int64_t kb = 0; kb < K; kb += 2048) {
-        const int64_t kc = kb + 32 * lane;
-        const bool act = kc < K;
-        const int64_t kk = act ? kc : kb;  // idle lanes re-read a valid chunk
-        v4i raw[R][CL::NV];
-        float sc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int64_t row = r0 + r < N ? r0 + r : N - 1;
-            const int64_t flat = row * K + kk;
-            const v4i *p = reinterpret_cast<const v4i *>(data + flat * CL::BYTES_PER_32 / 32);
-#pragma unroll
-            for (int j = 0; j < CL::NV; ++j) raw[r][j] = __builtin_nontemporal_load(p + j);
-            if (SCALED) {
-                const int64_t gi = flat / g;
-                sc[r] = scales[gi < ns - 1 ? gi : ns - 1];
-            }
-        }
-        float xr[MT][32];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const int mr = m < mrows ? m : 0;
-            const float4 *xp = reinterpret_cast<const float4 *>(x + (int64_t)mr * K + kk);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float4 t = xp[j];
-                xr[m][4 * j] = t.x, xr[m][4 * j + 1] = t.y, xr[m][4 * j + 2] = t.z,
-                xr[m][4 * j + 3] = t.w;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float v[32];
-            decode32<KIND>(raw[r], v);
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                float p = xr[m][0] * v[0];
-#pragma unroll
-                for (int j = 1; j < 32; ++j) p = __builtin_fmaf(xr[m][j], v[j], p);
-                p = act ? p : 0.0f;
-                acc[r][m] = SCALED ? __builtin_fmaf(sc[r], p, acc[r][m]) : acc[r][m] + p;
-            }
-        }
-    }
+    const int64_t S = (K + kSlice - 1) / kSlice;
+    const int slot0 = x_slot<KIND>(threadIdx.x), slot1 = x_slot<KIND>(threadIdx.x + 256);
+    const bool rows_hold_groups = kg != 0;
+    int64_t gbase[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int64_t row = r0 + r;
+        const uint32_t row = (uint32_t)(r0 + r < N ? r0 + r : N - 1);
+        gbase[r] = !SCALED ? 0 : (rows_hold_groups ? (int64_t)row * kg : (int64_t)(row / rpg));
+    }
+    // Two slices in flight: slices s and s+1 sit in register sets A and B
+    // and LDS buffers 0 and 1. While A is computed, the loads of slice s+2
+    // go out; while B is computed, those of slice s+3. x is always issued
+    // before weights, so waiting for x (to write it to LDS) never waits for
+    // weight loads: the memory counter completes in issue order.
+    SliceRegs<KIND, R> A, B;
+    f4v tx[2][2][MT];
+    auto ld = [&](SliceRegs<KIND, R> &w, int64_t kb) {
+        load_slice<KIND, R, SCALED>(w, data, scales, ns, gbase, g, rows_hold_groups, K, N, r0, kb,
+                                    lane);
+    };
+    auto stx = [&](int b, f4v (&t)[2][MT]) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            float s = wave_sum(acc[r][m]);
-            if (lane == r * MT + m && row < N && m < mrows) {
-                if (BIAS) s = s + bias[row];
-                y[(int64_t)m * N + row] = s;
+            *reinterpret_cast<f4v *>(&xs[b][m * kSlice + slot0]) = t[0][m];
+            *reinterpret_cast<f4v *>(&xs[b][m * kSlice + slot1]) = t[1][m];
+        }
+    };
+    stage_x_load<MT>(tx[0][0], x, mrows, K, 0);
+    stage_x_load<MT>(tx[0][1], x, mrows, K, 1024);
+    if (SFIX != 1) {
+        stage_x_load<MT>(tx[1][0], x, mrows, K, kSlice);
+        stage_x_load<MT>(tx[1][1], x, mrows, K, kSlice + 1024);
+    }
+    ld(A, 0);
+    if (SFIX != 1) ld(B, kSlice);
+    stx(0, tx[0]);
+    if (SFIX != 1) stx(1, tx[1]);
+    __syncthreads();
+    if (SFIX != 0) {
+        // Straight line (the slice count is a template constant): the
+        // compiler waits for exactly the loads each row needs. Where loads
+        // are conditional or sit behind a loop back-edge it waits for every
+        // outstanding load first, so slice 0 would wait for slice 1's data.
+        compute_slice<KIND, MT, R, SCALED>(A, xs[0], K, 0, lane, acc);
+        if (SFIX == 2) compute_slice<KIND, MT, R, SCALED>(B, xs[1], K, kSlice, lane, acc);
+    } else
+    for (int64_t s = 0; s < S; s += 2) {
+        const int64_t kb = s * kSlice;
+        compute_slice<KIND, MT, R, SCALED>(A, xs[0], K, kb, lane, acc);
+        const bool n2 = s + 2 < S, n3 = s + 3 < S;
+        if (n2) {
+            stage_x_load<MT>(tx[0][0], x, mrows, K, kb + 2 * kSlice);
+            stage_x_load<MT>(tx[0][1], x, mrows, K, kb + 2 * kSlice + 1024);
+        }
+        if (n3) {
+            stage_x_load<MT>(tx[1][0], x, mrows, K, kb + 3 * kSlice);
+            stage_x_load<MT>(tx[1][1], x, mrows, K, kb + 3 * kSlice + 1024);
+        }
+        if (n2) ld(A, kb + 2 * kSlice);
+        if (s + 1 < S) compute_slice<KIND, MT, R, SCALED>(B, xs[1], K, kb + kSlice, lane, acc);
+        if (n3) ld(B, kb + 3 * kSlice);
+        if (!n2) break;
+        __syncthreads();  // every wave is done reading both buffers
+        stx(0, tx[0]);
+        if (n3) stx(1, tx[1]);
+        __syncthreads();
+    }
+
+    // Halving butterfly: at distance d, the lanes with bit d set keep the
+    // upper half of their values and the others the lower half, each adding
+    // the partner's copy; once one value is left the remaining steps sum it.
+    // Lane l ends with value index l >> (6 - log2 V).
+    float v[V];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) v[r * MT + m] = acc[r][m];
+#pragma unroll
+    for (int d = 32, cnt = V; d >= 1; d >>= 1) {
+        if (cnt > 1) {
+            const int half = cnt / 2;
+            const bool up = (lane & d) != 0;
+#pragma unroll
+            for (int i = 0; i < half; ++i) {
+                const float keep = up ? v[half + i] : v[i];
+                const float send = up ? v[i] : v[half + i];
+                v[i] = keep + __shfl_xor(send, d, 64);
             }
+            cnt = half;
+        } else {
+            v[0] += __shfl_xor(v[0], d, 64);
+        }
+    }
+    constexpr int LOG_V = V == 1 ? 0 : (V == 2 ? 1 : (V == 4 ? 2 : (V == 8 ? 3 : (V == 16 ? 4 : (V == 32 ? 5 : 6)))));
+    if ((lane & ((64 >> LOG_V) - 1)) == 0) {
+        const int idx = lane >> (6 - LOG_V);
+        const int r = idx / MT, m = idx % MT;
+        const int64_t row = r0 + r;
+        if (row < N && m < mrows) {
+            float o = v[0];
+            if (BIAS) o = o + bias[row];
+            y[(int64_t)m * N + row] = o;
         }
     }
 }
@@ -479,27 +656,45 @@ extern "C" int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_b
     return check_launch("rnn_qt_dequantize");
 }
 
+template <int KIND, int MT, int R, bool SCALED, bool BIAS>
+static void launch_gemv_b(unsigned blocks, const float *x, int mrows, int64_t K,
+                          const uint8_t *data, const float *scales, int64_t ns, uint32_t g,
+                          uint32_t kg, uint32_t rpg, int64_t N, const float *bias, float *y,
+                          hipStream_t st) {
+    if (K <= kSlice)
+        qt_gemv_kernel<KIND, MT, R, SCALED, BIAS, 1><<<blocks, 256, 0, st>>>(
+            x, mrows, K, data, scales, ns, g, kg, rpg, N, bias, y);
+    else if (K <= 2 * kSlice)
+        qt_gemv_kernel<KIND, MT, R, SCALED, BIAS, 2><<<blocks, 256, 0, st>>>(
+            x, mrows, K, data, scales, ns, g, kg, rpg, N, bias, y);
+    else
+        qt_gemv_kernel<KIND, MT, R, SCALED, BIAS, 0><<<blocks, 256, 0, st>>>(
+            x, mrows, K, data, scales, ns, g, kg, rpg, N, bias, y);
+}
+
 template <int KIND, int MT, int R, bool SCALED>
 static void launch_gemv(const float *x, int mrows, int64_t K, const uint8_t *data,
                         const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
                         float *y, hipStream_t st) {
     const unsigned blocks = (unsigned)ceil_div(ceil_div(N, R), 4);
+    const uint32_t kg = K % g == 0 ? (uint32_t)(K / g) : 0u;
+    const uint32_t rpg = kg ? 1u : (uint32_t)(g / K);
     if (bias)
-        qt_gemv_kernel<KIND, MT, R, SCALED, true><<<blocks, 256, 0, st>>>(x, mrows, K, data, scales,
-                                                                          ns, g, N, bias, y);
+        launch_gemv_b<KIND, MT, R, SCALED, true>(blocks, x, mrows, K, data, scales, ns,
+                                                 (uint32_t)g, kg, rpg, N, bias, y, st);
     else
-        qt_gemv_kernel<KIND, MT, R, SCALED, false><<<blocks, 256, 0, st>>>(x, mrows, K, data, scales,
-                                                                           ns, g, N, bias, y);
+        launch_gemv_b<KIND, MT, R, SCALED, false>(blocks, x, mrows, K, data, scales, ns,
+                                                  (uint32_t)g, kg, rpg, N, bias, y, st);
 }
 
 template <int KIND, bool SCALED>
 static void gemv_chunk(int mt, const float *x, int64_t K, const uint8_t *data, const float *scales,
                        int64_t ns, int64_t g, int64_t N, const float *bias, float *y,
                        hipStream_t st) {
-    constexpr int R4 = KIND == KIND_I4 || KIND == KIND_I8 ? 4 : 2;
-    if (mt == 1) launch_gemv<KIND, 1, 8, SCALED>(x, 1, K, data, scales, ns, g, N, bias, y, st);
-    else if (mt == 2) launch_gemv<KIND, 2, 8, SCALED>(x, 2, K, data, scales, ns, g, N, bias, y, st);
-    else launch_gemv<KIND, 4, R4, SCALED>(x, mt, K, data, scales, ns, g, N, bias, y, st);
+    constexpr int R = KIND == KIND_I4 ? 4 : 2;  // rows per wave (wider pieces hold more registers)
+    if (mt == 1) launch_gemv<KIND, 1, R, SCALED>(x, 1, K, data, scales, ns, g, N, bias, y, st);
+    else if (mt == 2) launch_gemv<KIND, 2, R, SCALED>(x, 2, K, data, scales, ns, g, N, bias, y, st);
+    else launch_gemv<KIND, 4, 2, SCALED>(x, mt, K, data, scales, ns, g, N, bias, y, st);
 }
 
 // The fused path takes formats whose codes decode without a table, K a
@@ -536,13 +731,16 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
     }
     const int kind = gemv_kind(format);
     const bool scaled = format != RNN_QF_FP16 && format != RNN_QF_BF16;
-    const bool fits = kind >= 0 && in_f % 32 == 0 && (!scaled || group % 32 == 0) &&
+    const bool fits = kind >= 0 && in_f % 32 == 0 &&
+                      (!scaled || (group % (kind == KIND_I4 ? 32 : 16) == 0 && group <= 0xffffffffLL &&
+                                   (in_f % group == 0 || group % in_f == 0))) &&
                       ((uintptr_t)x % 16) == 0 && ((uintptr_t)data % 16) == 0 &&
-                      ceil_div(ceil_div(out_f, 2), 4) <= 0x7fffffff;
+                      out_f <= 0x7fffffffLL;
     const bool gemv = algo == RNN_ALGO_GEMV || (algo == RNN_ALGO_AUTO && m <= 16 && fits);
     if (gemv) {
         RNN_REQUIRE(fits, "%s: the fused GEMV needs an INT4/INT8/GGUF/FP16/BF16 format, in_f %% 32 "
-                    "== 0, group %% 32 == 0 and 16-byte aligned x and data", name);
+                    "== 0, group %% 32 == 0 (INT4, Q4) or %% 16 == 0 (INT8, Q8), groups that divide or "
+                    "are divided by in_f, and 16-byte aligned x and data", name);
         for (int64_t m0 = 0; m0 < m; m0 += 4) {
             const int mt = (int)std::min<int64_t>(4, m - m0);
             const float *xs = x + m0 * in_f;
