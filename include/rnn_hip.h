@@ -250,6 +250,40 @@ int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,
                           int64_t out_f, const float *bias, float *y,
                           unsigned flags, void *stream);
 
+/* ------------------------------- RotorQuant KV cache + attention (next row) */
+
+/* Elements of one page array (codes or scales) for `bh` sequences of `seq`
+ * positions at head dim `dim`: bh * ceil(seq/64)*64 * ceil(dim/3). Host only. */
+int rnn_rotorquant_kv_page_elems(int64_t bh, int64_t seq, int64_t dim, int64_t *elems);
+
+/* Lays the codes and scales of rnn_rotorquant_quantize (rows = bh*seq vectors
+ * of one K or V cache, codes int8 [rows, 3*ceil(dim/3)], scales f32 [rows,
+ * ceil(dim/3)]) out as a KV-cache page: per sequence, tiles of 64 positions;
+ * in a tile, position j of group g at ((tile*16 + j/4)*ng + g)*4 + j%4; codes
+ * as u16 words of three 4-bit two's-complement codes (c0 | c1<<4 | c2<<8),
+ * scales f32. Positions past seq are zero. bits 2..4. No counterpart in the
+ * reference, which keeps only the reconstruction (src/quant.rs:116-121
+ * describes RotorQuant as a KV-cache quantizer). */
+int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, int64_t bh,
+                           int64_t seq, int64_t dim, int bits, uint16_t *page_codes,
+                           float *page_scales, void *stream);
+
+/* Tensor::flash_attention (src/tensor.rs:618-672) of queries q [bh, nq, dim]
+ * over the K and V caches held as pages (rnn_rotorquant_kv_pack), equal to
+ * the reference's attention over the RotorQuant reconstructions
+ * (rnn_rotorquant_dequantize) of K and V, without forming them: scores are
+ * s_g ((R_g q_g) . c_g) summed over groups and V is accumulated in the
+ * rotated domain. out [bh, nq, dim]; dim <= 192; scale multiplies q.k as in
+ * the reference. f32 sums in the kernel's own order: within a floating-point
+ * bound of the reference, not bit for bit. Pages 16-byte (scales) and 8-byte
+ * (codes) aligned. */
+int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t nq,
+                                const uint16_t *k_codes, const float *k_scales,
+                                const uint16_t *v_codes, const float *v_scales,
+                                const float *k_rotors, const float *v_rotors,
+                                int64_t seq, int64_t dim, float scale, float *out,
+                                void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -875,3 +875,39 @@ void orc_qt_linear_forward(int fmt, const float *x, size_t m, size_t in_f,
         for (size_t i = 0; i < m; ++i)
             for (size_t j = 0; j < out_f; ++j) y[i * out_f + j] = y[i * out_f + j] + bias[j];
 }
+
+/* ------------------------------------------------------------------ */
+/* src/tensor.rs:618-672 Tensor::flash_attention                        */
+/* ------------------------------------------------------------------ */
+/* Online softmax per query row, sequential over keys, every product and sum
+ * rounded on its own (no contraction), exp through libm expf as f32::exp.
+ * The reference takes q, k, v of one shape [batch, seq, dim]; nq and skv are
+ * kept apart here so that a decode query (nq = 1) over a cache of skv keys
+ * follows the same expressions; nq == skv is the reference function. */
+void orc_flash_attention(const float *q, const float *k, const float *v, size_t batch,
+                         size_t nq, size_t skv, size_t dim, float scale, float *out) {
+    float *acc = (float *)malloc((dim ? dim : 1) * sizeof(float));
+    for (size_t b = 0; b < batch; ++b) {
+        for (size_t i = 0; i < nq; ++i) {
+            const float *qr = q + (b * nq + i) * dim;
+            float row_max = -INFINITY, row_sum = 0.0f;
+            for (size_t t = 0; t < dim; ++t) acc[t] = 0.0f;
+            for (size_t j = 0; j < skv; ++j) {
+                const float *kr = k + (b * skv + j) * dim, *vr = v + (b * skv + j) * dim;
+                float s = 0.0f;
+                for (size_t t = 0; t < dim; ++t) s += qr[t] * kr[t];
+                s *= scale;
+                float m_new = fmaxf(row_max, s);
+                float exp_old = expf(row_max - m_new);
+                float p = expf(s - m_new);
+                row_sum = exp_old * row_sum + p;
+                for (size_t t = 0; t < dim; ++t) acc[t] = exp_old * acc[t] + p * vr[t];
+                row_max = m_new;
+            }
+            float inv = row_sum > 0.0f ? 1.0f / row_sum : 0.0f;
+            float *o = out + (b * nq + i) * dim;
+            for (size_t t = 0; t < dim; ++t) o[t] = acc[t] * inv;
+        }
+    }
+    free(acc);
+}

@@ -210,6 +210,15 @@ void orc_qt_linear_forward(int fmt, const float *x, size_t m, size_t in_f,
                            const uint8_t *data, const float *scales, size_t n_scales,
                            size_t group, size_t out_f, const float *bias, float *y);
 
+/* ---- attention (src/tensor.rs:618-672) ---- */
+
+/* Tensor::flash_attention: out[b,i] = softmax_j(scale * q[b,i].k[b,j]) . v[b,j]
+ * by the reference's sequential online softmax (expf, no contraction). q is
+ * [batch, nq, dim], k and v [batch, skv, dim]; nq == skv is the reference's
+ * own signature, nq = 1 a decode step over a cache of skv keys. */
+void orc_flash_attention(const float *q, const float *k, const float *v, size_t batch,
+                         size_t nq, size_t skv, size_t dim, float scale, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,7 @@ def lib():
             "orc_qt_quantize": [ctypes.c_int, _P, _SZ, _SZ, _P, _P],
             "orc_qt_dequantize": [ctypes.c_int, _P, _P, _SZ, _SZ, _SZ, _P],
             "orc_qt_linear_forward": [ctypes.c_int, _P, _SZ, _SZ, _P, _P, _SZ, _SZ, _SZ, _P, _P],
+            "orc_flash_attention": [_P, _P, _P, _SZ, _SZ, _SZ, _SZ, ctypes.c_float, _P],
             "orc_sgemm": [ctypes.c_int, ctypes.c_int, _SZ, _SZ, _SZ, ctypes.c_float, _P, _SZ, _P, _SZ,
                           ctypes.c_float, _P, _SZ],
         }
@@ -433,3 +434,15 @@ def qt_linear_forward(fmt, x, data, scales, group, out_f, bias=None):
     lib().orc_qt_linear_forward(fmt, _ptr(x), m, in_f, _ptr(data), _ptr(scales), scales.size,
                                 group, out_f, _ptr(bias), _ptr(y))
     return y
+
+
+# ---------------------------------------------------------------- attention
+def flash_attention(q, k, v, scale):
+    """Tensor::flash_attention (src/tensor.rs:618-672): q [batch, nq, dim],
+    k, v [batch, skv, dim] (nq == skv is the reference's signature)."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    b, nq, dim = q.shape
+    skv = k.shape[1]
+    out = np.empty((b, nq, dim), np.float32)
+    lib().orc_flash_attention(_ptr(q), _ptr(k), _ptr(v), b, nq, skv, dim, float(scale), _ptr(out))
+    return out

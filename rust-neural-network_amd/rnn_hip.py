@@ -74,6 +74,10 @@ SIGNATURES = {
     "rnn_qt_dequantize": ([_INT, _P, _I64, _P, _I64, _I64, _I64, _P, _P], _INT),
     "rnn_qt_linear_forward": ([_INT, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P,
                                _UINT, _P], _INT),
+    "rnn_rotorquant_kv_page_elems": ([_I64, _I64, _I64, _P], _INT),
+    "rnn_rotorquant_kv_pack": ([_P, _P, _I64, _I64, _I64, _INT, _P, _P, _P], _INT),
+    "rnn_rotorquant_kv_attention": ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                     ctypes.c_float, _P, _P], _INT),
     "rnn_sgemm": ([_INT, _INT, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P, _I64,
                    ctypes.c_float, _P, _I64, _P], _INT),
 }
@@ -401,3 +405,43 @@ def qt_linear_forward(fmt, x, data, scales, group, out_f, bias=None, algo=ALGO_A
                                         _ptr(scales), scales.numel(), group, out_f, _ptr(bias),
                                         _ptr(y), algo, _stream(stream)))
     return y
+
+
+# ------------------------------------------------------------------ RotorQuant KV cache
+def rotorquant_kv_page_elems(bh, seq, dim):
+    out = (ctypes.c_int64 * 1)()
+    _check(load().rnn_rotorquant_kv_page_elems(bh, seq, dim, ctypes.c_void_p(ctypes.addressof(out))))
+    return int(out[0])
+
+
+def rotorquant_kv_pack(codes, scales, bh, seq, dim, bits, stream=None):
+    """Codes/scales of rotorquant_quantize (rows = bh*seq) -> a KV-cache page
+    (u16 codes as int16, f32 scales), both flat [page elements]."""
+    import torch
+    _dev(codes, torch.int8, "codes"), _dev(scales, torch.float32, "scales")
+    n = rotorquant_kv_page_elems(bh, seq, dim)
+    pc = _empty((n,), torch.int16, codes)
+    ps = _empty((n,), torch.float32, codes)
+    _check(load().rnn_rotorquant_kv_pack(_ptr(codes), _ptr(scales), bh, seq, dim, bits, _ptr(pc),
+                                         _ptr(ps), _stream(stream)))
+    return pc, ps
+
+
+def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, out=None,
+                            stream=None):
+    """Tensor::flash_attention (src/tensor.rs:618-672) of q [bh, nq, dim] over
+    K and V pages (rotorquant_kv_pack). Returns out [bh, nq, dim]."""
+    import torch
+    _dev(q, torch.float32, "q")
+    for t, nm in ((k_page[0], "k codes"), (v_page[0], "v codes")):
+        _dev(t, torch.int16, nm)
+    for t, nm in ((k_page[1], "k scales"), (v_page[1], "v scales"), (k_rotors, "k rotors"),
+                  (v_rotors, "v rotors")):
+        _dev(t, torch.float32, nm)
+    bh, nq, dim = q.shape
+    out = out if out is not None else _empty((bh, nq, dim), torch.float32, q)
+    _check(load().rnn_rotorquant_kv_attention(_ptr(q), bh, nq, _ptr(k_page[0]), _ptr(k_page[1]),
+                                              _ptr(v_page[0]), _ptr(v_page[1]), _ptr(k_rotors),
+                                              _ptr(v_rotors), seq, dim, float(scale), _ptr(out),
+                                              _stream(stream)))
+    return out
