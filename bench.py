@@ -246,6 +246,50 @@ def bench_rotorquant(H, W, dev, steps):
             "launches_per_step": 2}
 
 
+def bench_rq_attention(H, W, dev, steps):
+    """Decode attention over the RotorQuant KV cache (the RotorQuant config's
+    K and V, [8, 32, 4096, 128], 4-bit, as pages): one query per (batch,
+    head). Bytes per launch = both pages (6 bytes per position and group) +
+    q + out. Beside it, torch's f32 scaled_dot_product_attention over the
+    reconstructed K and V (what a cache without the codes would read), timed
+    the same way, for context."""
+    import torch
+    c = W.ROTORQUANT
+    b, h, seq, dim, bits = c["batch"], c["heads"], c["seq"], c["head_dim"], c["bits"]
+    bh, ng = b * h, (dim + 2) // 3
+    pages, rots, recon = [], [], []
+    for seed in (11, 12):
+        x = gen_f32((bh * seq, dim), seed, dev)
+        ch = torch.as_tensor(W.kv_outlier_channels(dim, seed), device=dev)
+        x[:, ch] *= 10.0
+        r = torch.from_numpy(W.rotors(ng, seed)).to(dev)
+        _, codes, scales = H.rotorquant_quantize(x, r, bits, want_y=False, want_codes=True)
+        pages.append(H.rotorquant_kv_pack(codes, scales, bh, seq, dim, bits))
+        recon.append(H.rotorquant_dequantize(codes, scales, dim, r).view(b, h, seq, dim))
+        rots.append(r)
+        del x, codes, scales
+    q = gen_f32((bh, 1, dim), 13, dev)
+    out = torch.empty_like(q)
+    scale = 1.0 / dim ** 0.5
+
+    def step():
+        H.rotorquant_kv_attention(q, pages[0], pages[1], rots[0], rots[1], seq, scale, out=out)
+
+    ms = timed(step, max(steps // 2, 20), 10)
+    nbytes = sum(p[0].numel() * 2 + p[1].numel() * 4 for p in pages) + 2 * q.numel() * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    qf = q.view(b, h, 1, dim)
+    ms_f32 = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
+        qf, recon[0], recon[1], scale=scale), max(steps // 2, 20), 10)
+    del recon
+    torch.cuda.empty_cache()
+    return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+            "bytes": nbytes, "kernel": "rq_kv_attn_kernel (scores and V in the rotated domain)",
+            "f32_kv_sdpa_us": round(ms_f32 * 1e3, 2),
+            "f32_kv_bytes": 2 * bh * seq * dim * 4,
+            "shape": {"batch": b, "heads": h, "seq": seq, "head_dim": dim, "bits": bits, "nq": 1}}
+
+
 # ---------------------------------------------------------------- f32 GEMM
 SGEMM_MNK = (4096, 4096, 4096)
 
@@ -341,8 +385,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--only", default="all",
-                    choices=["all", "prefill", "gemv", "qt_gemv", "ternary", "rotorquant", "sgemm",
-                             "copy"])
+                    choices=["all", "prefill", "gemv", "qt_gemv", "ternary", "rotorquant", "rq_attention",
+                             "sgemm", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -399,6 +443,9 @@ def main():
     if args.only in ("all", "rotorquant"):
         log("RotorQuant K+V [8,32,4096,128] 4-bit round trip")
         components["rotorquant_kv"] = bench_rotorquant(H, W, dev, args.steps)
+    if args.only in ("all", "rq_attention"):
+        log("attention over the RotorQuant KV cache [8,32,4096,128], 4-bit, one query per head")
+        components["rotorquant_kv_attention"] = bench_rq_attention(H, W, dev, args.steps)
     if args.only in ("all", "sgemm"):
         log("f32 GEMM 4096x4096x4096 (BlasBackend::sgemm)")
         components["f32_sgemm"] = bench_sgemm(H, dev, args.steps)
