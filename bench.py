@@ -258,13 +258,13 @@ def bench_rq_attention(H, W, dev, steps):
     b, h, seq, dim, bits = c["batch"], c["heads"], c["seq"], c["head_dim"], c["bits"]
     bh, ng = b * h, (dim + 2) // 3
     pages, rots, recon = [], [], []
-    for seed in (11, 12):
+    for seed, kind in ((11, H.RQ_PAGE_K), (12, H.RQ_PAGE_V)):
         x = gen_f32((bh * seq, dim), seed, dev)
         ch = torch.as_tensor(W.kv_outlier_channels(dim, seed), device=dev)
         x[:, ch] *= 10.0
         r = torch.from_numpy(W.rotors(ng, seed)).to(dev)
         _, codes, scales = H.rotorquant_quantize(x, r, bits, want_y=False, want_codes=True)
-        pages.append(H.rotorquant_kv_pack(codes, scales, bh, seq, dim, bits))
+        pages.append(H.rotorquant_kv_pack(codes, scales, bh, seq, dim, bits, kind))
         recon.append(H.rotorquant_dequantize(codes, scales, dim, r).view(b, h, seq, dim))
         rots.append(r)
         del x, codes, scales
@@ -276,7 +276,10 @@ def bench_rq_attention(H, W, dev, steps):
         H.rotorquant_kv_attention(q, pages[0], pages[1], rots[0], rots[1], seq, scale, out=out)
 
     ms = timed(step, max(steps // 2, 20), 10)
-    nbytes = sum(p[0].numel() * 2 + p[1].numel() * 4 for p in pages) + 2 * q.numel() * 4
+    # bytes the kernel reads: K pages pad each position to 8 groups of codes
+    # and 4 of scales, V pages hold exactly ng of each
+    npos = bh * -(-seq // 64) * 64
+    nbytes = npos * (2 * 8 * -(-ng // 8) + 4 * 4 * -(-ng // 4)) + npos * 6 * ng + 2 * q.numel() * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
     qf = q.view(b, h, 1, dim)
     ms_f32 = timed(lambda: torch.nn.functional.scaled_dot_product_attention(

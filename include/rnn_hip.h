@@ -252,31 +252,42 @@ int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,
 
 /* ------------------------------- RotorQuant KV cache + attention (next row) */
 
-/* Elements of one page array (codes or scales) for `bh` sequences of `seq`
- * positions at head dim `dim`: bh * ceil(seq/64)*64 * ceil(dim/3). Host only. */
-int rnn_rotorquant_kv_page_elems(int64_t bh, int64_t seq, int64_t dim, int64_t *elems);
+/* Page sizes for `bh` sequences of `seq` positions at head dim `dim` (ng =
+ * ceil(dim/3) groups, positions rounded up to tiles of 64): u16 code elements
+ * bh*ceil(seq/64)*64 * 8*ceil(ng/8), f32 scale elements bh*ceil(seq/64)*64 *
+ * 4*ceil(ng/4); enough for either kind. Host only. */
+int rnn_rotorquant_kv_page_elems(int64_t bh, int64_t seq, int64_t dim,
+                                 int64_t *code_elems, int64_t *scale_elems);
+
+#define RNN_RQ_PAGE_K 0
+#define RNN_RQ_PAGE_V 1
 
 /* Lays the codes and scales of rnn_rotorquant_quantize (rows = bh*seq vectors
  * of one K or V cache, codes int8 [rows, 3*ceil(dim/3)], scales f32 [rows,
- * ceil(dim/3)]) out as a KV-cache page: per sequence, tiles of 64 positions;
- * in a tile, position j of group g at ((tile*16 + j/4)*ng + g)*4 + j%4; codes
- * as u16 words of three 4-bit two's-complement codes (c0 | c1<<4 | c2<<8),
- * scales f32. Positions past seq are zero. bits 2..4. No counterpart in the
- * reference, which keeps only the reconstruction (src/quant.rs:116-121
- * describes RotorQuant as a KV-cache quantizer). */
+ * ceil(dim/3)]) out as a KV-cache page of tiles of 64 positions: a u16 per
+ * position and group holding its three 4-bit two's-complement codes
+ * (c0 | c1<<4 | c2<<8) and an f32 scale. kind RNN_RQ_PAGE_K orders a tile for
+ * readers with a lane per position: scales of groups 4a..4a+3 of position j at
+ * ((tile*ceil(ng/4) + a)*64 + j)*4, codes of groups 8b..8b+7 at
+ * ((tile*ceil(ng/8) + b)*64 + j)*8 (groups past ng are padding).
+ * RNN_RQ_PAGE_V orders it for readers with a lane per group: the scale of
+ * position j, group g at ((tile*16 + j/4)*ng + g)*4 + j%4, its code at
+ * ((tile*8 + j/8)*ng + g)*8 + j%8. Positions past seq are zero. bits 2..4. No
+ * counterpart in the reference, which keeps only the reconstruction
+ * (src/quant.rs:116-121 describes RotorQuant as a KV-cache quantizer). */
 int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, int64_t bh,
-                           int64_t seq, int64_t dim, int bits, uint16_t *page_codes,
-                           float *page_scales, void *stream);
+                           int64_t seq, int64_t dim, int bits, int kind,
+                           uint16_t *page_codes, float *page_scales, void *stream);
 
 /* Tensor::flash_attention (src/tensor.rs:618-672) of queries q [bh, nq, dim]
  * over the K and V caches held as pages (rnn_rotorquant_kv_pack), equal to
  * the reference's attention over the RotorQuant reconstructions
  * (rnn_rotorquant_dequantize) of K and V, without forming them: scores are
  * s_g ((R_g q_g) . c_g) summed over groups and V is accumulated in the
- * rotated domain. out [bh, nq, dim]; dim <= 192; scale multiplies q.k as in
- * the reference. f32 sums in the kernel's own order: within a floating-point
- * bound of the reference, not bit for bit. Pages 16-byte (scales) and 8-byte
- * (codes) aligned. */
+ * rotated domain. k_* is a RNN_RQ_PAGE_K page, v_* a RNN_RQ_PAGE_V page.
+ * out [bh, nq, dim]; dim <= 192; scale multiplies q.k as in the reference.
+ * f32 sums in the kernel's own order: within a floating-point bound of the
+ * reference, not bit for bit. Pages 16-byte aligned. */
 int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t nq,
                                 const uint16_t *k_codes, const float *k_scales,
                                 const uint16_t *v_codes, const float *v_scales,

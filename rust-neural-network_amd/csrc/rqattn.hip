@@ -3,15 +3,23 @@
 // over K and V stored by RotorQuant, src/quant.rs:116-239).
 //
 // Page layout. Per (batch*head) sequence the cache holds T = ceil(S/64) tiles
-// of 64 positions. Inside a tile, position j = 4*q4 + r (q4 in 0..15, r in
-// 0..3) of group g sits at ((tile*16 + q4)*ng + g)*4 + r, in two arrays:
-//   codes  u16: the group's three codes as 4-bit two's complement nibbles
-//          (c0 | c1 << 4 | c2 << 8), bits <= 4 only;
-//   scales f32: the group's scale.
-// A lane that owns group g reads four positions with one 16-byte (scales) and
-// one 8-byte (codes) load, and the lanes of a wave read consecutive bytes.
-// That is 258 bytes per vector at head_dim 128 (43 groups), against 512 in
-// f32. Positions past S hold zero codes and scales and are masked.
+// of 64 positions, in two arrays: codes, a u16 per position and group holding
+// the group's three codes as 4-bit two's complement nibbles (c0 | c1 << 4 |
+// c2 << 8, bits <= 4 only), and scales, an f32 per position and group. The
+// order inside a tile depends on which lanes read it:
+//   K pages (a lane per position): scales of groups 4a..4a+3 of position j
+//     side by side at ((tile*ng4 + a)*64 + j)*4, codes of groups 8b..8b+7 at
+//     ((tile*ng8 + b)*64 + j)*8 (ng4 = ceil(ng/4), ng8 = ceil(ng/8); the
+//     groups past ng are padding).
+//   V pages (a lane per group): the scale of position j = 4*q4 + r, group g
+//     at ((tile*16 + q4)*ng + g)*4 + r; its code at ((tile*8 + j/8)*ng + g)*8
+//     + j%8.
+// Every load instruction reads 16 consecutive bytes per lane, consecutive
+// across the lanes; a wave's tile takes 17 loads for K and 24 for V, within
+// the 63 a wave can have in flight. 6 bytes per position and group (plus
+// the K padding): 272 bytes per K vector and 258 per V vector at head_dim 128
+// (43 groups), against 512 in f32. Positions past S hold zero codes and
+// scales and are masked.
 //
 // Attention without reconstructing K or V. RotorQuant reconstructs a group
 // as K_g = R_g^T (c_g * s_g) (R_g the group's rotation). Then
@@ -19,12 +27,12 @@
 //   sum_j p_j V_j = blockdiag(R_g^T) (sum_j p_j s_{j,g} c_{j,g}),
 // so each query is rotated once, scores come straight from codes and
 // scales, V is accumulated in the rotated domain and rotated back once at the
-// end. Lane g of a wave owns group g: its rotated query and its three
-// accumulators stay in registers. Per tile the 64 scores are summed over
-// groups through LDS (a transpose), the softmax runs online per tile (as
-// src/tensor.rs:640-654 does per key), and the probabilities go back through
-// LDS to the group lanes. The waves of a workgroup take tiles round-robin and
-// merge their (max, sum, accumulators) at the end.
+// end. Scores: a lane per position (all 64 busy), the rotated query read from
+// LDS by broadcast. V: a lane per group, which keeps its three rotated
+// accumulators in registers; the tile's probabilities reach it through LDS.
+// The softmax runs online per tile (as src/tensor.rs:640-654 does per key).
+// The waves of a workgroup take tiles round-robin and merge their (max, sum,
+// accumulators) at the end.
 #include "common.hpp"
 #include "rotor.hpp"
 
@@ -33,31 +41,45 @@ namespace rnn {
 constexpr int kTile = 64;
 constexpr int kAttnWaves = 4;
 
-__host__ __device__ inline int64_t rq_page_index(int64_t bh, int64_t T, int64_t ng, int64_t pos,
-                                                 int64_t g) {
-    const int64_t t = pos / kTile, j = pos % kTile;
-    return (((bh * T + t) * 16 + j / 4) * ng + g) * 4 + (j % 4);
+enum { RQ_PAGE_K = 0, RQ_PAGE_V = 1 };
+
+// Indices of (sequence sq, position pos, group g) in the code (u16) and scale
+// arrays of a page of the given kind; T tiles per sequence.
+__host__ __device__ inline void rq_page_pos(int kind, int64_t sq, int64_t T, int64_t ng,
+                                            int64_t pos, int64_t g, int64_t &ci, int64_t &si) {
+    const int64_t t = sq * T + pos / kTile, j = pos % kTile;
+    if (kind == RQ_PAGE_K) {
+        const int64_t ng4 = (ng + 3) / 4, ng8 = (ng + 7) / 8;
+        si = ((t * ng4 + g / 4) * 64 + j) * 4 + (g % 4);
+        ci = ((t * ng8 + g / 8) * 64 + j) * 8 + (g % 8);
+    } else {
+        si = ((t * 16 + j / 4) * ng + g) * 4 + (j % 4);
+        ci = ((t * 8 + j / 8) * ng + g) * 8 + (j % 8);
+    }
 }
 
-// One thread per (sequence, tile position, group).
-__global__ void rq_kv_pack_kernel(const int8_t *__restrict__ codes, const float *__restrict__ scales,
-                                  int64_t BH, int64_t S, int64_t ng, int64_t T,
-                                  uint16_t *__restrict__ pc, float *__restrict__ ps) {
-    const int64_t total = BH * T * kTile * ng;
+// One thread per (sequence, tile position, group incl. the K padding).
+__global__ void rq_kv_pack_kernel(int kind, const int8_t *__restrict__ codes,
+                                  const float *__restrict__ scales, int64_t BH, int64_t S,
+                                  int64_t ng, int64_t T, uint16_t *__restrict__ pc,
+                                  float *__restrict__ ps) {
+    const int64_t ngw = kind == RQ_PAGE_K ? 8 * ((ng + 7) / 8) : ng;
+    const int64_t total = BH * T * kTile * ngw;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t g = i % ng, pos = (i / ng) % (T * kTile), bh = i / (ng * T * kTile);
-        const int64_t dst = rq_page_index(bh, T, ng, pos, g);
+        const int64_t g = i % ngw, pos = (i / ngw) % (T * kTile), sq = i / (ngw * T * kTile);
+        int64_t ci, si;
+        rq_page_pos(kind, sq, T, ng, pos, g, ci, si);
         uint16_t w = 0;
-        float s = 0.0f;
-        if (pos < S) {
-            const int64_t row = bh * S + pos;
+        float sc = 0.0f;
+        if (pos < S && g < ng) {
+            const int64_t row = sq * S + pos;
             const int8_t *c = codes + row * 3 * ng + 3 * g;
             w = (uint16_t)((c[0] & 15) | ((c[1] & 15) << 4) | ((c[2] & 15) << 8));
-            s = scales[row * ng + g];
+            sc = scales[row * ng + g];
         }
-        pc[dst] = w;
-        ps[dst] = s;
+        pc[ci] = w;
+        if (kind == RQ_PAGE_V ? g < ng : g < 4 * ((ng + 3) / 4)) ps[si] = sc;
     }
 }
 
@@ -81,48 +103,63 @@ __device__ __forceinline__ float wave_sum_f(float v) {
     return v;
 }
 
-// One tile's codes and scales for this lane's group: 16 quads of 4 positions.
-struct RqTile {
+// A V tile for this lane's group: 16 quads of 4 positions.
+struct RqTileV {
     f4v s[16];
-    u2v c[16];
+    v4i c[8];
 };
 
-__device__ __forceinline__ void rq_load_tile(RqTile &t, const uint16_t *__restrict__ pc,
-                                             const float *__restrict__ ps, int64_t base,
-                                             int64_t ng, int g) {
+__device__ __forceinline__ void rq_load_v(RqTileV &t, const uint16_t *__restrict__ pc,
+                                          const float *__restrict__ ps, int64_t tile, int64_t ng,
+                                          int g) {
 #pragma unroll
-    for (int q4 = 0; q4 < 16; ++q4) {
-        const int64_t idx = base + ((int64_t)q4 * ng + g) * 4;
-        t.s[q4] = *reinterpret_cast<const f4v *>(ps + idx);
-        t.c[q4] = *reinterpret_cast<const u2v *>(pc + idx);
-    }
+    for (int q4 = 0; q4 < 16; ++q4)
+        t.s[q4] = *reinterpret_cast<const f4v *>(ps + ((tile * 16 + q4) * ng + g) * 4);
+#pragma unroll
+    for (int q8 = 0; q8 < 8; ++q8)
+        t.c[q8] = *reinterpret_cast<const v4i *>(pc + ((tile * 8 + q8) * ng + g) * 8);
 }
 
-__device__ __forceinline__ uint32_t quad_word(const u2v c, int r) {
-    const uint32_t w = r < 2 ? c.x : c.y;
-    return (r & 1) ? (w >> 16) : (w & 0xFFFFu);
+// A K tile for this lane's position: the scales of NG4 x 4 groups and the
+// codes of NG8 x 8 groups (groups past ng are padding; their terms are
+// dropped). Blocks past the page's own count re-read its last one.
+template <int NG4, int NG8>
+struct RqTileK {
+    f4v s[NG4];
+    v4i c[NG8];
+};
+
+template <int NG4, int NG8>
+__device__ __forceinline__ void rq_load_k(RqTileK<NG4, NG8> &t, const uint16_t *__restrict__ pc,
+                                          const float *__restrict__ ps, int64_t tile, int64_t ng,
+                                          int lane) {
+    const int64_t ng4 = (ng + 3) / 4, ng8 = (ng + 7) / 8;
+#pragma unroll
+    for (int a = 0; a < NG4; ++a)
+        t.s[a] = *reinterpret_cast<const f4v *>(ps + ((tile * ng4 + (a < ng4 ? a : ng4 - 1)) * 64 + lane) * 4);
+#pragma unroll
+    for (int b = 0; b < NG8; ++b)
+        t.c[b] = *reinterpret_cast<const v4i *>(pc + ((tile * ng8 + (b < ng8 ? b : ng8 - 1)) * 64 + lane) * 8);
 }
 
-// grid: BH * nq workgroups of kAttnWaves waves; dim <= 192 (ng <= 64).
+
+// grid: BH * nq workgroups of kAttnWaves waves; ng <= 4 * NG4 <= 8 * NG8 <= 64.
+template <int NG4, int NG8>
 __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const float *__restrict__ ks,
     const uint16_t *__restrict__ vc, const float *__restrict__ vs, const float *__restrict__ krot,
     const float *__restrict__ vrot, int64_t nq, int64_t S, int64_t dim, int64_t ng, int64_t T,
     float scale, float *__restrict__ out) {
-    // red: per wave, 64 score terms per group, the slot of position j in row
-    // g swizzled to j ^ 4*(g & 15) (conflict-free 16-byte writes by group
-    // lanes and 4-byte reads by position lanes); pb: the tile's probabilities.
-    __shared__ __attribute__((aligned(16))) float red[kAttnWaves][64 * 64];
+    __shared__ __attribute__((aligned(16))) float qs[4 * 64];  // rotated query, 4 floats per group
     __shared__ __attribute__((aligned(16))) float pb[kAttnWaves][64];
     __shared__ float mrg[kAttnWaves][2 + 3 * 64];
     const int wid = threadIdx.x / 64, lane = threadIdx.x % 64;
     const int64_t bh = blockIdx.x / nq, qi = blockIdx.x % nq;
-    const int g = lane < ng ? lane : (int)ng - 1;  // lanes past the groups mirror the last one
+    const int g = lane < ng ? lane : (int)ng - 1;  // group lanes past ng mirror the last one
     const bool gact = lane < ng;
 
-    // rotated query of this lane's group: q'_g = R_g q_g (zero past dim)
-    float qr[3];
-    {
+    // rotated query q'_g = R_g q_g (zero past dim), published in LDS
+    if (wid == 0) {
         float R[9];
         rotation_matrix(krot + 4 * g, R);
         const float *qrow = q + (bh * nq + qi) * dim;
@@ -133,43 +170,45 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
             const float v = qrow[d < dim ? d : dim - 1];
             x[c] = d < dim ? v : 0.0f;
         }
+        f4v qv;
 #pragma unroll
-        for (int i = 0; i < 3; ++i) qr[i] = R[3 * i] * x[0] + R[3 * i + 1] * x[1] + R[3 * i + 2] * x[2];
+        for (int i = 0; i < 3; ++i)
+            qv[i] = gact ? R[3 * i] * x[0] + R[3 * i + 1] * x[1] + R[3 * i + 2] * x[2] : 0.0f;
+        qv[3] = 0.0f;
+        *reinterpret_cast<f4v *>(&qs[4 * lane]) = qv;
     }
+    __syncthreads();
     float m = -INFINITY, l = 0.0f, a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
-    float *rw = red[wid];
-    const int sw = 4 * (g & 15);
-
-    RqTile K, V;
-    int t = wid;
     const int64_t seq = bh * T;
-    if (t < T) {
-        rq_load_tile(K, kc, ks, (seq + t) * 16 * ng * 4, ng, g);
-        rq_load_tile(V, vc, vs, (seq + t) * 16 * ng * 4, ng, g);
+    const int64_t nt = wid < T ? (T - wid + kAttnWaves - 1) / kAttnWaves : 0;
+    const int64_t last = wid + (nt - 1) * kAttnWaves;
+    RqTileK<NG4, NG8> K;
+    RqTileV V;
+    if (nt > 0) {
+        rq_load_k<NG4, NG8>(K, kc, ks, seq + wid, ng, lane);
+        rq_load_v(V, vc, vs, seq + wid, ng, g);
     }
-    for (; t < T; t += kAttnWaves) {
+    for (int64_t i = 0; i < nt; ++i) {
+        const int64_t t = wid + i * kAttnWaves;
         // the next tile, or this one again at the end (an L2 hit): the loads
         // stay unconditional so that the compiler's waits stay exact
-        const int tn = t + kAttnWaves < T ? t + kAttnWaves : t;
-        // score terms of the 64 positions for this group
-#pragma unroll
-        for (int q4 = 0; q4 < 16; ++q4) {
-            f4v term;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t w = quad_word(K.c[q4], r);
-                const float d = qr[0] * rq_code(w, 0) + qr[1] * rq_code(w, 1) + qr[2] * rq_code(w, 2);
-                term[r] = K.s[q4][r] * d;
-            }
-            if (gact) *reinterpret_cast<f4v *>(&rw[g * 64 + ((4 * q4) ^ sw)]) = term;
-        }
-        rq_load_tile(K, kc, ks, (seq + tn) * 16 * ng * 4, ng, g);
-        __builtin_amdgcn_wave_barrier();
-        // lane = position: sum over groups, scale, mask, online softmax
+        const int64_t tn = t + kAttnWaves <= last ? t + kAttnWaves : t;
+        // lane = position: score = scale * sum_g s_g (q'_g . c_g)
         float sc = 0.0f;
-        for (int gg = 0; gg < ng; ++gg) sc += rw[gg * 64 + (lane ^ (4 * (gg & 15)))];
+#pragma unroll
+        for (int gg = 0; gg < 4 * NG4; ++gg) {
+            const f4v qv = *reinterpret_cast<const f4v *>(&qs[4 * (gg < ng ? gg : 0)]);
+            const uint32_t word = (uint32_t)K.c[gg / 8][(gg % 8) / 2];
+            const uint32_t w = (gg & 1) ? (word >> 16) : word;
+            float d = qv[0] * rq_code(w, 0);
+            d = __builtin_fmaf(qv[1], rq_code(w, 1), d);
+            d = __builtin_fmaf(qv[2], rq_code(w, 2), d);
+            const float sg = gg < ng ? K.s[gg / 4][gg % 4] : 0.0f;
+            sc = __builtin_fmaf(sg, d, sc);
+        }
+        rq_load_k<NG4, NG8>(K, kc, ks, seq + tn, ng, lane);
         sc *= scale;
-        if ((int64_t)t * kTile + lane >= S) sc = -INFINITY;
+        if (t * kTile + lane >= S) sc = -INFINITY;
         const float mt = wave_max_f(sc);
         const float mn = fmaxf(m, mt);
         const float corr = expf(m - mn);  // 0 on the first tile (m = -inf)
@@ -177,22 +216,23 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
         l = l * corr + p;
         m = mn;
         pb[wid][lane] = p;
-        __builtin_amdgcn_wave_barrier();
-        // V in the rotated domain: acc_g = acc_g * corr + sum_j p_j s_jg c_jg
+        __builtin_amdgcn_wave_barrier();  // one wave's LDS operations complete in order
+        // lane = group: acc_g = acc_g * corr + sum_j p_j s_jg c_jg (rotated domain)
         a0 *= corr, a1 *= corr, a2 *= corr;
 #pragma unroll
         for (int q4 = 0; q4 < 16; ++q4) {
             const f4v p4 = *reinterpret_cast<const f4v *>(&pb[wid][4 * q4]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint32_t w = quad_word(V.c[q4], r);
+                const uint32_t word = (uint32_t)V.c[q4 / 2][2 * (q4 & 1) + r / 2];
+                const uint32_t w = (r & 1) ? (word >> 16) : (word & 0xFFFFu);
                 const float ws = p4[r] * V.s[q4][r];
                 a0 = __builtin_fmaf(ws, rq_code(w, 0), a0);
                 a1 = __builtin_fmaf(ws, rq_code(w, 1), a1);
                 a2 = __builtin_fmaf(ws, rq_code(w, 2), a2);
             }
         }
-        rq_load_tile(V, vc, vs, (seq + tn) * 16 * ng * 4, ng, g);
+        rq_load_v(V, vc, vs, seq + tn, ng, g);
         __builtin_amdgcn_wave_barrier();
     }
     // merge the waves: M = max m_w, L = sum l_w e^(m_w - M), A = sum a_w e^(m_w - M)
@@ -232,25 +272,30 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
 
 using namespace rnn;
 
-extern "C" int rnn_rotorquant_kv_page_elems(int64_t bh, int64_t seq, int64_t dim, int64_t *elems) {
-    RNN_REQUIRE(bh >= 0 && seq >= 0 && dim > 0 && elems, "rnn_rotorquant_kv_page_elems: bad argument");
-    *elems = bh * ceil_div(seq, kTile) * kTile * ceil_div(dim, 3);
+extern "C" int rnn_rotorquant_kv_page_elems(int64_t bh, int64_t seq, int64_t dim,
+                                            int64_t *code_elems, int64_t *scale_elems) {
+    RNN_REQUIRE(bh >= 0 && seq >= 0 && dim > 0 && code_elems && scale_elems,
+                "rnn_rotorquant_kv_page_elems: bad argument");
+    const int64_t ng = ceil_div(dim, 3), pos = bh * ceil_div(seq, kTile) * kTile;
+    *code_elems = pos * 8 * ceil_div(ng, 8);   // K pages pad to 8 groups, V pages use ng
+    *scale_elems = pos * 4 * ceil_div(ng, 4);  // K pages pad to 4 groups
     return RNN_OK;
 }
 
 extern "C" int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, int64_t bh,
-                                      int64_t seq, int64_t dim, int bits, uint16_t *page_codes,
-                                      float *page_scales, void *stream) {
+                                      int64_t seq, int64_t dim, int bits, int kind,
+                                      uint16_t *page_codes, float *page_scales, void *stream) {
     const char *name = "rnn_rotorquant_kv_pack";
     RNN_REQUIRE(bh >= 0 && seq >= 0 && dim > 0, "%s: bad size", name);
     RNN_REQUIRE(bits >= 2 && bits <= 4, "%s: the page stores 4-bit codes (bits 2..4), got %d", name,
                 bits);
+    RNN_REQUIRE(kind == RQ_PAGE_K || kind == RQ_PAGE_V, "%s: kind must be K (0) or V (1)", name);
     if (bh == 0 || seq == 0) return RNN_OK;
     RNN_REQUIRE(codes && scales && page_codes && page_scales, "%s: null pointer", name);
     const int64_t ng = ceil_div(dim, 3), T = ceil_div(seq, kTile);
-    const int64_t total = bh * T * kTile * ng;
+    const int64_t total = bh * T * kTile * (kind == RQ_PAGE_K ? 8 * ceil_div(ng, 8) : ng);
     const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 8 * (int64_t)device_cu_count());
-    rq_kv_pack_kernel<<<blocks, 256, 0, as_stream(stream)>>>(codes, scales, bh, seq, ng, T,
+    rq_kv_pack_kernel<<<blocks, 256, 0, as_stream(stream)>>>(kind, codes, scales, bh, seq, ng, T,
                                                              page_codes, page_scales);
     return check_launch(name);
 }
@@ -268,12 +313,20 @@ extern "C" int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t n
     if (bh == 0 || nq == 0) return RNN_OK;
     RNN_REQUIRE(q && out && k_rotors && v_rotors, "%s: null pointer", name);
     RNN_REQUIRE(seq == 0 || (k_codes && k_scales && v_codes && v_scales), "%s: null page", name);
-    RNN_REQUIRE(((uintptr_t)k_scales % 16) == 0 && ((uintptr_t)v_scales % 16) == 0 &&
-                    ((uintptr_t)k_codes % 8) == 0 && ((uintptr_t)v_codes % 8) == 0,
-                "%s: pages must be 16-byte (scales) and 8-byte (codes) aligned", name);
+    RNN_REQUIRE(((uintptr_t)v_scales % 16) == 0 && ((uintptr_t)v_codes % 16) == 0 &&
+                    ((uintptr_t)k_scales % 16) == 0 && ((uintptr_t)k_codes % 16) == 0,
+                "%s: pages must be 16-byte aligned", name);
     RNN_REQUIRE(bh * nq <= 0x7fffffffLL, "%s: too many queries", name);
     const int64_t ng = ceil_div(dim, 3), T = ceil_div(seq, kTile);
-    rq_kv_attn_kernel<<<(unsigned)(bh * nq), kAttnWaves * 64, 0, as_stream(stream)>>>(
-        q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, scale, out);
+    const unsigned grid = (unsigned)(bh * nq);
+    hipStream_t st = as_stream(stream);
+    if (ng <= 44)
+        rq_kv_attn_kernel<11, 6><<<grid, kAttnWaves * 64, 0, st>>>(
+            q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, scale,
+            out);
+    else
+        rq_kv_attn_kernel<16, 8><<<grid, kAttnWaves * 64, 0, st>>>(
+            q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, scale,
+            out);
     return check_launch(name);
 }

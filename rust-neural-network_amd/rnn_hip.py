@@ -74,8 +74,8 @@ SIGNATURES = {
     "rnn_qt_dequantize": ([_INT, _P, _I64, _P, _I64, _I64, _I64, _P, _P], _INT),
     "rnn_qt_linear_forward": ([_INT, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P,
                                _UINT, _P], _INT),
-    "rnn_rotorquant_kv_page_elems": ([_I64, _I64, _I64, _P], _INT),
-    "rnn_rotorquant_kv_pack": ([_P, _P, _I64, _I64, _I64, _INT, _P, _P, _P], _INT),
+    "rnn_rotorquant_kv_page_elems": ([_I64, _I64, _I64, _P, _P], _INT),
+    "rnn_rotorquant_kv_pack": ([_P, _P, _I64, _I64, _I64, _INT, _INT, _P, _P, _P], _INT),
     "rnn_rotorquant_kv_attention": ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                      ctypes.c_float, _P, _P], _INT),
     "rnn_sgemm": ([_INT, _INT, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P, _I64,
@@ -408,29 +408,38 @@ def qt_linear_forward(fmt, x, data, scales, group, out_f, bias=None, algo=ALGO_A
 
 
 # ------------------------------------------------------------------ RotorQuant KV cache
+RQ_PAGE_K = 0
+RQ_PAGE_V = 1
+
+
 def rotorquant_kv_page_elems(bh, seq, dim):
-    out = (ctypes.c_int64 * 1)()
-    _check(load().rnn_rotorquant_kv_page_elems(bh, seq, dim, ctypes.c_void_p(ctypes.addressof(out))))
-    return int(out[0])
+    """(u16 code elements, f32 scale elements) of one page."""
+    out = (ctypes.c_int64 * 2)()
+    base = ctypes.addressof(out)
+    _check(load().rnn_rotorquant_kv_page_elems(bh, seq, dim, ctypes.c_void_p(base),
+                                               ctypes.c_void_p(base + 8)))
+    return int(out[0]), int(out[1])
 
 
-def rotorquant_kv_pack(codes, scales, bh, seq, dim, bits, stream=None):
+def rotorquant_kv_pack(codes, scales, bh, seq, dim, bits, kind, stream=None):
     """Codes/scales of rotorquant_quantize (rows = bh*seq) -> a KV-cache page
-    (u16 codes as int16, f32 scales), both flat [page elements]."""
+    of the given kind (RQ_PAGE_K or RQ_PAGE_V): (u16 codes as int16, f32
+    scales), both flat."""
     import torch
     _dev(codes, torch.int8, "codes"), _dev(scales, torch.float32, "scales")
-    n = rotorquant_kv_page_elems(bh, seq, dim)
-    pc = _empty((n,), torch.int16, codes)
-    ps = _empty((n,), torch.float32, codes)
-    _check(load().rnn_rotorquant_kv_pack(_ptr(codes), _ptr(scales), bh, seq, dim, bits, _ptr(pc),
-                                         _ptr(ps), _stream(stream)))
+    nc, ns = rotorquant_kv_page_elems(bh, seq, dim)
+    pc = _empty((nc,), torch.int16, codes)
+    ps = _empty((ns,), torch.float32, codes)
+    _check(load().rnn_rotorquant_kv_pack(_ptr(codes), _ptr(scales), bh, seq, dim, bits, kind,
+                                         _ptr(pc), _ptr(ps), _stream(stream)))
     return pc, ps
 
 
 def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, out=None,
                             stream=None):
     """Tensor::flash_attention (src/tensor.rs:618-672) of q [bh, nq, dim] over
-    K and V pages (rotorquant_kv_pack). Returns out [bh, nq, dim]."""
+    a K page (RQ_PAGE_K) and a V page (RQ_PAGE_V) of rotorquant_kv_pack.
+    Returns out [bh, nq, dim]."""
     import torch
     _dev(q, torch.float32, "q")
     for t, nm in ((k_page[0], "k codes"), (v_page[0], "v codes")):

@@ -38,12 +38,13 @@ def bound(q, k, v, scale):
     return (4 * ds[..., None] + (skv + 8) * u) * vmax * 2
 
 
-def make_cache(hip, dev, x, rot, bits, bh, seq):
-    """quantize x [bh*seq, dim] on the GPU, pack it; return (page, reconstruction)."""
+def make_cache(hip, dev, x, rot, bits, bh, seq, kind):
+    """quantize x [bh*seq, dim] on the GPU, pack it as a K or V page; return
+    (page, reconstruction)."""
     dim = x.shape[1]
     _, codes, scales = hip.rotorquant_quantize(to_dev(x, dev), to_dev(rot, dev), bits,
                                                want_y=False, want_codes=True)
-    page = hip.rotorquant_kv_pack(codes, scales, bh, seq, dim, bits)
+    page = hip.rotorquant_kv_pack(codes, scales, bh, seq, dim, bits, kind)
     recon = O.rotorquant_dequantize(codes.cpu().numpy(), scales.cpu().numpy(), dim, rot)
     return page, recon.reshape(bh, seq, dim)
 
@@ -59,8 +60,8 @@ def test_kv_attention_parity(dev, hip, bh, nq, seq, dim, bits):
     kx[:, : max(1, dim // 40)] *= 10.0                      # outlier channels
     vx = W.activations(bh * seq, dim, seed=seq + 2)
     krot, vrot = W.rotors(ng, seed=dim + 3), W.rotors(ng, seed=dim + 4)
-    kp, k = make_cache(hip, dev, kx, krot, bits, bh, seq)
-    vp, v = make_cache(hip, dev, vx, vrot, bits, bh, seq)
+    kp, k = make_cache(hip, dev, kx, krot, bits, bh, seq, hip.RQ_PAGE_K)
+    vp, v = make_cache(hip, dev, vx, vrot, bits, bh, seq, hip.RQ_PAGE_V)
     q = rng.standard_normal((bh, nq, dim)).astype(np.float32)
     scale = float(1.0 / np.sqrt(dim))
     out = hip.rotorquant_kv_attention(to_dev(q, dev), kp, vp, to_dev(krot, dev), to_dev(vrot, dev),
@@ -79,8 +80,8 @@ def test_kv_attention_self_attention_signature(dev, hip):
     ng = (dim + 2) // 3
     x = W.activations(bh * seq, dim, seed=5)
     rot = W.rotors(ng, seed=6)
-    kp, k = make_cache(hip, dev, x, rot, 4, bh, seq)
-    vp, v = make_cache(hip, dev, x * 0.5, rot, 4, bh, seq)
+    kp, k = make_cache(hip, dev, x, rot, 4, bh, seq, hip.RQ_PAGE_K)
+    vp, v = make_cache(hip, dev, x * 0.5, rot, 4, bh, seq, hip.RQ_PAGE_V)
     q = k.copy()
     out = hip.rotorquant_kv_attention(to_dev(q, dev), kp, vp, to_dev(rot, dev), to_dev(rot, dev),
                                       seq, 0.125).cpu().numpy()
@@ -98,5 +99,8 @@ def test_kv_attention_empty_cache_and_errors(dev, hip):
         hip.rotorquant_kv_attention(torch.ones((1, 1, 195), device=dev), (z16, z32), (z16, z32),
                                     rot, rot, 0, 1.0)
     codes = torch.zeros((4, 129), dtype=torch.int8, device=dev)
+    with pytest.raises(hip.RnnError):                       # page kind must be K or V
+        hip.rotorquant_kv_pack(codes, torch.zeros((4, 43), device=dev), 1, 4, 128, 4, 2)
     with pytest.raises(hip.RnnError):                       # 8-bit codes do not fit the page
-        hip.rotorquant_kv_pack(codes, torch.zeros((4, 43), device=dev), 1, 4, 128, 8)
+        hip.rotorquant_kv_pack(codes, torch.zeros((4, 43), device=dev), 1, 4, 128, 8,
+                               hip.RQ_PAGE_K)
