@@ -159,19 +159,20 @@ def bench_gemv(H, W, dev, steps):
 
 # ---------------------------------------------------------------- QuantizedLinear GEMV
 QT_SHAPES = [(1, 4096, 11008), (4, 4096, 11008), (1, 4096, 4096)]
-QT_FORMATS = [("INT4_g128", 3, 128), ("GGUF_Q4_0", 6, 32), ("GGUF_Q8_0", 8, 32), ("BF16", 1, 0)]
+QT_FORMATS = [("INT4_g128", 3, 128), ("GGUF_Q4_0", 6, 32), ("GGUF_Q8_0", 8, 32), ("BF16", 1, 0),
+              ("NF4_g64", 4, 64)]
 
 
 def bench_qt_gemv(H, dev, steps):
     """QuantizedLinear::forward (src/quantize.rs:744-754) at decode shapes:
-    the fused GEMV that decodes INT4/GGUF/BF16 weights in registers. Bytes per
+    the fused GEMV that decodes INT4/GGUF/BF16/NF4 weights in registers. Bytes per
     launch = weight codes + f32 scales + x (4 m k) + y (4 m n); weights
     rotate over copies past the MALL as for the W8A8 GEMV."""
     import torch
     out = {}
     for name, fmt, gs in QT_FORMATS:
         for (m, k, n) in QT_SHAPES:
-            if name == "BF16" and (m, n) != (1, 11008):
+            if name in ("BF16", "NF4_g64") and (m, n) != (1, 11008):
                 continue
             nb, ns, g = H.qt_layout(fmt, n * k, gs)
             wbytes = nb + 4 * ns

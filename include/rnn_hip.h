@@ -237,9 +237,11 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
 
 /* QuantizedLinear::forward (src/quantize.rs:744-754): y [m, out_f] =
  * x [m, in_f] . W^T (+ bias[out_f]) with W = the dequantized [out_f, in_f]
- * weight. AUTO: for m <= 16 with INT4/INT8/GGUF/FP16/BF16 weights, in_f % 32
- * == 0, group % 32 == 0 and 16-byte aligned x and data, a fused GEMV that
- * decodes the codes in registers (weights read once); otherwise dequantize
+ * weight. AUTO: for m <= 16, in_f % 32 == 0, a group that is a multiple of
+ * 32 (4-bit formats) or 16 (INT8, GGUF Q8_0) and divides or is divided by
+ * in_f, and 16-byte aligned x and data, a fused GEMV that decodes the codes
+ * in registers (NF4 and NVFP4 through a 16-entry table; weights read once);
+ * otherwise dequantize
  * into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV forces the
  * former (error if it does not fit), RNN_ALGO_TILED the latter. f32 sums in
  * the kernel's own order: within the rnn_sgemm rounding bound of the

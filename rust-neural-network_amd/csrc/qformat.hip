@@ -12,7 +12,11 @@
 
 namespace rnn {
 
-enum QKind { KIND_I4 = 0, KIND_I8 = 1, KIND_F16 = 2, KIND_BF16 = 3 };
+// Code kinds of the fused GEMV: signed 4-bit, int8, f16, bf16, and 4-bit
+// indices into a 16-entry table (NF4, E2M1).
+enum QKind { KIND_I4 = 0, KIND_I8 = 1, KIND_F16 = 2, KIND_BF16 = 3, KIND_NF4 = 4, KIND_E2M1 = 5 };
+
+__host__ __device__ constexpr bool kind4(int k) { return k == KIND_I4 || k == KIND_NF4 || k == KIND_E2M1; }
 
 __host__ __device__ inline bool qf_is4(int f) {
     return f == RNN_QF_INT4 || f == RNN_QF_NF4 || f == RNN_QF_NVFP4 || f == RNN_QF_GGUF_Q4 ||
@@ -263,7 +267,7 @@ __global__ void qt_dequant_kernel(int f, const uint8_t *__restrict__ data,
 // reduces its R*MT partial sums with a halving butterfly.
 template <int KIND>
 struct Fmt {
-    static constexpr int NV = KIND == KIND_I4 ? 1 : (KIND == KIND_I8 ? 2 : 4);  // pieces per lane
+    static constexpr int NV = kind4(KIND) ? 1 : (KIND == KIND_I8 ? 2 : 4);  // pieces per lane
     static constexpr int EP = 32 / NV;               // elements per 16-byte piece
     static constexpr int PIECE_STRIDE = 1024 * EP / 16;  // elements between a lane's pieces
 };
@@ -273,10 +277,20 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 // Decodes one 16-byte piece into EP floats. INT4 nibbles are moved into the
 // high half of a byte, where the sign-extending byte conversion reads them
-// as exactly 16*q; the caller multiplies the piece's sum by 1/16.
+// as exactly 16*q; the caller multiplies the piece's sum by 1/16. NF4 and
+// E2M1 nibbles index a 16-float table in LDS (the 16 entries sit in 16
+// different banks, so a wave's lookups never conflict).
 template <int KIND>
-__device__ __attribute__((always_inline)) inline void decode_piece(const v4i raw, float *v) {
-    if (KIND == KIND_I4) {
+__device__ __attribute__((always_inline)) inline void decode_piece(const v4i raw, float *v,
+                                                                   const float *lut) {
+    if (KIND == KIND_NF4 || KIND == KIND_E2M1) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t w = (uint32_t)raw[d];
+#pragma unroll
+            for (int b = 0; b < 8; ++b) v[8 * d + b] = lut[(w >> (4 * b)) & 0xFu];
+        }
+    } else if (KIND == KIND_I4) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const uint32_t w = (uint32_t)raw[d];
@@ -384,7 +398,8 @@ __device__ __attribute__((always_inline)) inline void stage_x_load(f4v (&t)[MT],
 
 template <int KIND, int MT, int R, bool SCALED>
 __device__ __attribute__((always_inline)) inline void compute_slice(const SliceRegs<KIND, R> &s, const float *__restrict__ xs,
-                                     int64_t K, int64_t kb, int lane, float (&acc)[R][MT]) {
+                                     int64_t K, int64_t kb, int lane, float (&acc)[R][MT],
+                                     const float *lut) {
     using F = Fmt<KIND>;
 #pragma unroll
     for (int j = 0; j < F::NV; ++j) {
@@ -406,7 +421,7 @@ __device__ __attribute__((always_inline)) inline void compute_slice(const SliceR
             // every row up front and the values of all rows stay live
             __builtin_amdgcn_sched_barrier(0);
             float v[F::EP];
-            decode_piece<KIND>(s.raw[r][j], v);
+            decode_piece<KIND>(s.raw[r][j], v, lut);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 float p = xr[m][0] * v[0];
@@ -432,6 +447,10 @@ __global__ __launch_bounds__(256) void qt_gemv_kernel(
     constexpr int V = R * MT;
     static_assert((V & (V - 1)) == 0 && V <= 64, "R*MT must be a power of two <= 64");
     __shared__ __attribute__((aligned(16))) float xs[2][MT * kSlice];
+    __shared__ float lut[16];  // NF4 / E2M1 values (src/quantize.rs:96-114, :138-144)
+    if ((KIND == KIND_NF4 || KIND == KIND_E2M1) && threadIdx.x < 16)
+        lut[threadIdx.x] = KIND == KIND_NF4 ? kNF4[threadIdx.x] : kE2M1[threadIdx.x];
+    // (published by the barrier after the first x slice is staged)
     const int lane = threadIdx.x % 64;
     const int64_t r0 = (blockIdx.x * 4 + threadIdx.x / 64) * (int64_t)R;  // rows past N: clamped
     float acc[R][MT];
@@ -483,12 +502,12 @@ __global__ __launch_bounds__(256) void qt_gemv_kernel(
         // compiler waits for exactly the loads each row needs. Where loads
         // are conditional or sit behind a loop back-edge it waits for every
         // outstanding load first, so slice 0 would wait for slice 1's data.
-        compute_slice<KIND, MT, R, SCALED>(A, xs[0], K, 0, lane, acc);
-        if (SFIX == 2) compute_slice<KIND, MT, R, SCALED>(B, xs[1], K, kSlice, lane, acc);
+        compute_slice<KIND, MT, R, SCALED>(A, xs[0], K, 0, lane, acc, lut);
+        if (SFIX == 2) compute_slice<KIND, MT, R, SCALED>(B, xs[1], K, kSlice, lane, acc, lut);
     } else
     for (int64_t s = 0; s < S; s += 2) {
         const int64_t kb = s * kSlice;
-        compute_slice<KIND, MT, R, SCALED>(A, xs[0], K, kb, lane, acc);
+        compute_slice<KIND, MT, R, SCALED>(A, xs[0], K, kb, lane, acc, lut);
         const bool n2 = s + 2 < S, n3 = s + 3 < S;
         if (n2) {
             stage_x_load<MT>(tx[0][0], x, mrows, K, kb + 2 * kSlice);
@@ -499,7 +518,7 @@ __global__ __launch_bounds__(256) void qt_gemv_kernel(
             stage_x_load<MT>(tx[1][1], x, mrows, K, kb + 3 * kSlice + 1024);
         }
         if (n2) ld(A, kb + 2 * kSlice);
-        if (s + 1 < S) compute_slice<KIND, MT, R, SCALED>(B, xs[1], K, kb + kSlice, lane, acc);
+        if (s + 1 < S) compute_slice<KIND, MT, R, SCALED>(B, xs[1], K, kb + kSlice, lane, acc, lut);
         if (n3) ld(B, kb + 3 * kSlice);
         if (!n2) break;
         __syncthreads();  // every wave is done reading both buffers
@@ -691,21 +710,24 @@ template <int KIND, bool SCALED>
 static void gemv_chunk(int mt, const float *x, int64_t K, const uint8_t *data, const float *scales,
                        int64_t ns, int64_t g, int64_t N, const float *bias, float *y,
                        hipStream_t st) {
-    constexpr int R = KIND == KIND_I4 ? 4 : 2;  // rows per wave (wider pieces hold more registers)
+    constexpr int R = kind4(KIND) ? 4 : 2;  // rows per wave (wider pieces hold more registers)
     if (mt == 1) launch_gemv<KIND, 1, R, SCALED>(x, 1, K, data, scales, ns, g, N, bias, y, st);
     else if (mt == 2) launch_gemv<KIND, 2, R, SCALED>(x, 2, K, data, scales, ns, g, N, bias, y, st);
     else launch_gemv<KIND, 4, 2, SCALED>(x, mt, K, data, scales, ns, g, N, bias, y, st);
 }
 
-// The fused path takes formats whose codes decode without a table, K a
-// multiple of 32, 16-byte aligned x and data, and (for scaled formats) a
-// group that is a multiple of 32.
+// The fused path takes every format: K a multiple of 32, 16-byte aligned x
+// and data, and (for scaled formats) a group that is a multiple of the
+// piece length (32 for 4-bit codes, 16 for int8) and divides or is divided
+// by K.
 static int gemv_kind(int format) {
     switch (format) {
     case RNN_QF_INT4: case RNN_QF_GGUF_Q4: case RNN_QF_GGUF_Q4K: return KIND_I4;
     case RNN_QF_INT8: case RNN_QF_GGUF_Q8: return KIND_I8;
     case RNN_QF_FP16: return KIND_F16;
     case RNN_QF_BF16: return KIND_BF16;
+    case RNN_QF_NF4: return KIND_NF4;
+    case RNN_QF_NVFP4: return KIND_E2M1;
     default: return -1;
     }
 }
@@ -732,15 +754,15 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
     const int kind = gemv_kind(format);
     const bool scaled = format != RNN_QF_FP16 && format != RNN_QF_BF16;
     const bool fits = kind >= 0 && in_f % 32 == 0 &&
-                      (!scaled || (group % (kind == KIND_I4 ? 32 : 16) == 0 && group <= 0xffffffffLL &&
+                      (!scaled || (group % (kind4(kind) ? 32 : 16) == 0 && group <= 0xffffffffLL &&
                                    (in_f % group == 0 || group % in_f == 0))) &&
                       ((uintptr_t)x % 16) == 0 && ((uintptr_t)data % 16) == 0 &&
                       out_f <= 0x7fffffffLL;
     const bool gemv = algo == RNN_ALGO_GEMV || (algo == RNN_ALGO_AUTO && m <= 16 && fits);
     if (gemv) {
-        RNN_REQUIRE(fits, "%s: the fused GEMV needs an INT4/INT8/GGUF/FP16/BF16 format, in_f %% 32 "
-                    "== 0, group %% 32 == 0 (INT4, Q4) or %% 16 == 0 (INT8, Q8), groups that divide or "
-                    "are divided by in_f, and 16-byte aligned x and data", name);
+        RNN_REQUIRE(fits, "%s: the fused GEMV needs in_f %% 32 == 0, a group that is a multiple of "
+                    "32 (4-bit formats) or 16 (INT8, Q8) and divides or is divided by in_f, and "
+                    "16-byte aligned x and data", name);
         for (int64_t m0 = 0; m0 < m; m0 += 4) {
             const int mt = (int)std::min<int64_t>(4, m - m0);
             const float *xs = x + m0 * in_f;
@@ -749,6 +771,14 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
             case KIND_I4:
                 gemv_chunk<KIND_I4, true>(mt, xs, in_f, data, scales, n_scales, group, out_f, bias,
                                           ys, st);
+                break;
+            case KIND_NF4:
+                gemv_chunk<KIND_NF4, true>(mt, xs, in_f, data, scales, n_scales, group, out_f, bias,
+                                           ys, st);
+                break;
+            case KIND_E2M1:
+                gemv_chunk<KIND_E2M1, true>(mt, xs, in_f, data, scales, n_scales, group, out_f,
+                                            bias, ys, st);
                 break;
             case KIND_I8:
                 gemv_chunk<KIND_I8, true>(mt, xs, in_f, data, scales, n_scales, group, out_f, bias,

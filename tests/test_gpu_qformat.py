@@ -22,7 +22,8 @@ pytestmark = pytest.mark.gpu
 
 ALL = [O.QF_FP16, O.QF_BF16, O.QF_INT8, O.QF_INT4, O.QF_NF4, O.QF_NVFP4, O.QF_GGUF_Q4,
        O.QF_GGUF_Q4K, O.QF_GGUF_Q8]
-GEMV_FMTS = [O.QF_INT4, O.QF_INT8, O.QF_GGUF_Q4, O.QF_GGUF_Q8, O.QF_FP16, O.QF_BF16]
+GEMV_FMTS = [O.QF_INT4, O.QF_INT8, O.QF_GGUF_Q4, O.QF_GGUF_Q8, O.QF_FP16, O.QF_BF16, O.QF_NF4,
+             O.QF_NVFP4]
 
 
 def to_dev(a, dev):
@@ -120,7 +121,7 @@ def test_argument_errors(dev, hip):
     d, s, g = hip.qt_quantize(O.QF_INT4, torch.zeros(48 * 8, device=dev), 48)
     with pytest.raises(hip.RnnError):          # forced GEMV: in_f % 32 != 0
         hip.qt_linear_forward(O.QF_INT4, xr, d, s, g, 8, algo=hip.ALGO_GEMV)
-    with pytest.raises(hip.RnnError):          # NF4 has no fused GEMV
+    with pytest.raises(hip.RnnError):          # forced GEMV: group 48 is not a multiple of 32
         hip.qt_linear_forward(O.QF_NF4, torch.zeros((1, 64), device=dev), d, s, g, 3,
                               algo=hip.ALGO_GEMV)
 
@@ -170,8 +171,8 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
 @pytest.mark.parametrize("fmt", [O.QF_NF4, O.QF_NVFP4, O.QF_INT4],
                          ids=["NF4", "NVFP4", "INT4-odd-group"])
 def test_linear_forward_dequant_path(dev, hip, fmt):
-    """Formats and groups outside the fused GEMV (table formats, a group that
-    is not a multiple of 32) take dequantize + f32 GEMM, for m = 1 and 40."""
+    """Shapes outside the fused GEMV (in_f = 200 is not a multiple of 32, a
+    group of 33) take dequantize + f32 GEMM, for m = 1 and 40."""
     rng = np.random.default_rng(fmt)
     n, k = 70, 200
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
