@@ -153,6 +153,64 @@ def cases() -> dict[str, np.ndarray]:
             g[f"rq_d{dim}.b{bits}.y"], g[f"rq_d{dim}.b{bits}.codes"] = y, c
             g[f"rq_d{dim}.b{bits}.scales"] = s
             g[f"rq_d{dim}.b{bits}.deq"] = O.rotorquant_dequantize(c, s, dim, rr)
+
+    # --- QuantizedTensor (src/quantize.rs): every format on the reference tests'
+    # inputs -- int8_roundtrip (:825-834, group 0), nvfp4_roundtrip (:862-872,
+    # group 8), fp16_roundtrip (:874-887), all_formats_produce_valid_output
+    # (:939-961, a 16x16 tensor, group 32) -- and the odd-group INT4 layout
+    # (group 3 over 6 elements).
+    ref_inputs = {
+        "int8": (np.array([0.1, 0.5, -0.3, 0.8, -0.9, 0.0], np.float32), 0),
+        "nvfp4": (np.array([0.0, 0.5, 1.0, -1.5, 3.0, -6.0, 2.0, -0.5], np.float32), 8),
+        "fp16": (np.array([1.0, 0.5, -0.25, 100.0, -1000.0, 0.001], np.float32), 0),
+        "rand": (W.activations(16, 16, seed=27).ravel(), 32),
+        "odd": (np.array([7.0, -7.0, 1.0, 3.5, 7.0, -3.5], np.float32), 3),
+    }
+    for tag, (x, gs) in ref_inputs.items():
+        g[f"qt_{tag}.x"] = x
+        g[f"qt_{tag}.gs"] = np.array([gs], np.int64)
+        for f in range(9):
+            d, sc, grp = O.qt_quantize(f, x, gs)
+            key = f"qt_{tag}.{O.QF_NAMES[f]}"
+            g[f"{key}.data"], g[f"{key}.scales"] = d, sc
+            g[f"{key}.group"] = np.array([grp], np.int64)
+            g[f"{key}.deq"] = O.qt_dequantize(f, d, sc, grp, x.size)
+
+    # --- QuantizedLinear::forward (src/quantize.rs:744-754), INT4 group 32, with
+    # bias; y from the oracle's sgemm order and sum|x||W| + |b| for the f32 bound
+    wq = (W.rng(28).standard_normal((40, 96)) * 0.02).astype(np.float32)
+    xq = W.activations(3, 96, seed=29)
+    bq = W.rng(30).standard_normal(40).astype(np.float32)
+    d, sc, grp = O.qt_quantize(O.QF_INT4, wq, 32)
+    g["qt_linear.x"], g["qt_linear.bias"], g["qt_linear.data"], g["qt_linear.scales"] = xq, bq, d, sc
+    g["qt_linear.group"] = np.array([grp], np.int64)
+    g["qt_linear.y"] = O.qt_linear_forward(O.QF_INT4, xq, d, sc, grp, 40, bq)
+    wdq = O.qt_dequantize(O.QF_INT4, d, sc, grp, wq.size).reshape(40, 96).astype(np.float64)
+    g["qt_linear.absdot"] = np.abs(xq.astype(np.float64)) @ np.abs(wdq).T + np.abs(bq)
+
+    # --- attention over the RotorQuant KV cache: Tensor::flash_attention
+    # (src/tensor.rs:618-672) over the 4-bit reconstructions of K and V,
+    # 2 sequences x 70 positions, head dim 12 (4 groups), one query each
+    kx = W.activations(140, 12, seed=31)
+    vx = W.activations(140, 12, seed=32)
+    kr, vr = W.rotors(4, seed=33), W.rotors(4, seed=34)
+    _, kcodes, ksc = O.rotorquant_quantize(kx, kr, 4)
+    _, vcodes, vsc = O.rotorquant_quantize(vx, vr, 4)
+    kd = O.rotorquant_dequantize(kcodes, ksc, 12, kr).reshape(2, 70, 12)
+    vd = O.rotorquant_dequantize(vcodes, vsc, 12, vr).reshape(2, 70, 12)
+    qa = W.activations(2, 12, seed=35).reshape(2, 1, 12)
+    g["kv_attn.k_codes"], g["kv_attn.k_scales"], g["kv_attn.k_rotors"] = kcodes, ksc, kr
+    g["kv_attn.v_codes"], g["kv_attn.v_scales"], g["kv_attn.v_rotors"] = vcodes, vsc, vr
+    g["kv_attn.q"] = qa
+    g["kv_attn.out"] = O.flash_attention(qa, kd, vd, np.float32(0.25))
+    # tolerance between any two evaluations within the f32 bound of the exact
+    # attention: 2 x (4 ds + (skv + 8) u) 2 max|V|, ds = (dim + 16) u scale
+    # max_j sum_t |q_t||K_jt| (the bound the GPU tests apply)
+    u = 2.0 ** -24
+    sabs = np.einsum("bid,bjd->bij", np.abs(qa).astype(np.float64), np.abs(kd).astype(np.float64))
+    ds = (12 + 16) * u * 0.25 * sabs.max(axis=2)
+    vmax = np.abs(vd).max(axis=(1, 2))[:, None, None]
+    g["kv_attn.tol"] = 2 * (4 * ds[..., None] + (70 + 8) * u) * vmax * 2
     return g
 
 

@@ -51,3 +51,9 @@ def test_literal_known_answers(stored):
     p = stored["ternary_rows.packed"]
     first = [(int(p[0]) >> (2 * i)) & 3 for i in range(4)]
     assert first == [1, 2, 0, 0]
+
+    # src/quantize.rs:862-872: E2M1 points at scale 1 round-trip exactly
+    assert stored["qt_nvfp4.NVFP4.deq"].tolist() == stored["qt_nvfp4.x"].tolist()
+    # odd groups: each packed on its own, read through data[i/2] (src/quantize.rs:377-396)
+    assert stored["qt_odd.INT4.data"].tolist() == [0x97, 0x01, 0x74, 0x0C]
+    assert stored["qt_odd.INT4.deq"].tolist() == [7.0, -7.0, 1.0, 0.0, 4.0, 7.0]

@@ -115,3 +115,50 @@ def test_golden_rotorquant(dev, hip, G, case):
     if base != "rq_ref":
         yd = hip.rotorquant_dequantize(codes, scales, x.shape[-1], r)
         assert_f32_equal(host(yd), G[f"{pre}.deq"])
+
+
+QT_TAGS = ["int8", "nvfp4", "fp16", "rand", "odd"]
+QT_NAMES = ["FP16", "BF16", "INT8", "INT4", "NF4", "NVFP4", "GGUF_Q4", "GGUF_Q4K", "GGUF_Q8"]
+
+
+@pytest.mark.parametrize("tag", QT_TAGS)
+def test_golden_quantized_tensor(dev, hip, G, tag):
+    """QuantizedTensor::quantize / dequantize (src/quantize.rs:231-269), every
+    format: bytes, scales, stored group and values bit-exact."""
+    x, gs = G[f"qt_{tag}.x"], int(G[f"qt_{tag}.gs"][0])
+    for f, name in enumerate(QT_NAMES):
+        key = f"qt_{tag}.{name}"
+        d, s, grp = hip.qt_quantize(f, to_dev(x, dev), gs)
+        assert grp == int(G[f"{key}.group"][0]), name
+        assert np.array_equal(host(d), G[f"{key}.data"]), name
+        assert np.array_equal(host(s).view(np.uint32), G[f"{key}.scales"].view(np.uint32)), name
+        sd = s if s.numel() else to_dev(np.zeros(1, np.float32), dev)
+        out = host(hip.qt_dequantize(f, d, sd, grp, x.size))
+        assert np.array_equal(out.view(np.uint32), G[f"{key}.deq"].view(np.uint32)), name
+
+
+def test_golden_quantized_linear(dev, hip, G):
+    """QuantizedLinear::forward (src/quantize.rs:744-754): both GPU paths
+    within twice the f32 GEMM bound of the stored oracle output."""
+    x, k = G["qt_linear.x"], G["qt_linear.x"].shape[1]
+    u = 2.0 ** -24
+    tol = 2 * (k + 2) * u / (1 - (k + 2) * u) * G["qt_linear.absdot"] + 1e-30
+    for algo in (hip.ALGO_GEMV, hip.ALGO_TILED):
+        y = hip.qt_linear_forward(3, to_dev(x, dev), to_dev(G["qt_linear.data"], dev),
+                                  to_dev(G["qt_linear.scales"], dev), int(G["qt_linear.group"][0]),
+                                  40, to_dev(G["qt_linear.bias"], dev), algo=algo)
+        assert np.all(np.abs(host(y).astype(np.float64) - G["qt_linear.y"]) <= tol)
+
+
+def test_golden_kv_attention(dev, hip, G):
+    """Attention over the RotorQuant KV cache (src/tensor.rs:618-672 over the
+    4-bit reconstructions) within the stored tolerance of the oracle's output."""
+    pages = []
+    for kv, kind in (("k", hip.RQ_PAGE_K), ("v", hip.RQ_PAGE_V)):
+        pages.append(hip.rotorquant_kv_pack(to_dev(G[f"kv_attn.{kv}_codes"], dev),
+                                            to_dev(G[f"kv_attn.{kv}_scales"], dev), 2, 70, 12, 4,
+                                            kind))
+    out = hip.rotorquant_kv_attention(to_dev(G["kv_attn.q"], dev), pages[0], pages[1],
+                                      to_dev(G["kv_attn.k_rotors"], dev),
+                                      to_dev(G["kv_attn.v_rotors"], dev), 70, 0.25)
+    assert np.all(np.abs(host(out).astype(np.float64) - G["kv_attn.out"]) <= G["kv_attn.tol"])
