@@ -158,21 +158,24 @@ def bench_gemv(H, W, dev, steps):
 
 
 # ---------------------------------------------------------------- QuantizedLinear GEMV
-QT_SHAPES = [(1, 4096, 11008), (4, 4096, 11008), (1, 4096, 4096)]
+QT_SHAPES = [(1, 4096, 11008), (4, 4096, 11008), (8, 4096, 11008), (16, 4096, 11008),
+             (1, 4096, 4096)]
 QT_FORMATS = [("INT4_g128", 3, 128), ("GGUF_Q4_0", 6, 32), ("GGUF_Q8_0", 8, 32), ("BF16", 1, 0),
               ("NF4_g64", 4, 64)]
 
 
 def bench_qt_gemv(H, dev, steps):
     """QuantizedLinear::forward (src/quantize.rs:744-754) at decode shapes:
-    the fused GEMV that decodes INT4/GGUF/BF16/NF4 weights in registers. Bytes per
+    the fused GEMV that decodes INT4/GGUF/BF16/NF4 weights in registers (the
+    VALU GEMV for m <= 4, the f32-MFMA GEMV for m >= 5, as AUTO picks). Bytes per
     launch = weight codes + f32 scales + x (4 m k) + y (4 m n); weights
     rotate over copies past the MALL as for the W8A8 GEMV."""
     import torch
     out = {}
     for name, fmt, gs in QT_FORMATS:
         for (m, k, n) in QT_SHAPES:
-            if name in ("BF16", "NF4_g64") and (m, n) != (1, 11008):
+            if (name in ("BF16", "NF4_g64") and (m, n) != (1, 11008)) or \
+                    (name == "GGUF_Q4_0" and m in (8, 16)):
                 continue
             nb, ns, g = H.qt_layout(fmt, n * k, gs)
             wbytes = nb + 4 * ns
@@ -186,7 +189,7 @@ def bench_qt_gemv(H, dev, steps):
             y = torch.empty((m, n), dtype=torch.float32, device=dev)
             n_launch = copies * max(1, -(-max(steps, 100) // copies))
             ms = graph_timed(lambda i: H.qt_linear_forward(fmt, x, ds[i % copies], ss[i % copies],
-                                                           g, n, y=y, algo=H.ALGO_GEMV), n_launch)
+                                                           g, n, y=y), n_launch)
             nbytes = wbytes + 4 * m * k + 4 * m * n
             gbs = nbytes / (ms * 1e-3) / 1e9
             out[f"{name}_m{m}_k{k}_n{n}"] = {

@@ -45,6 +45,7 @@ enum rnn_status {
 #define RNN_ALGO_TILED 0x10u        /* force the register-staged 128x128 MFMA GEMM */
 #define RNN_ALGO_GEMV 0x20u         /* force the skinny GEMV (m <= 16)        */
 #define RNN_ALGO_TILED_DMA 0x30u    /* force the LDS-DMA pipelined big-tile GEMM (k % 128 == 0, n % 4 == 0) */
+#define RNN_ALGO_GEMV_MFMA 0x40u    /* rnn_qt_linear_forward: force the f32-MFMA GEMV (m <= 16) */
 #define RNN_ALGO_MASK 0xF0u
 
 int rnn_abi_version(void);
@@ -240,7 +241,10 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
  * weight. AUTO: for m <= 16, in_f % 32 == 0, a group that is a multiple of
  * 32 (4-bit formats) or 16 (INT8, GGUF Q8_0) and divides or is divided by
  * in_f, and 16-byte aligned x and data, a fused GEMV that decodes the codes
- * in registers (NF4 and NVFP4 through a 16-entry table; weights read once);
+ * in registers (NF4 and NVFP4 through a 16-entry table; weights read once):
+ * for m >= 5 with in_f a multiple of 1024 (4-bit), 512 (8-bit) or 256
+ * (16-bit) the GEMV on f32 MFMA that takes all m rows at once
+ * (RNN_ALGO_GEMV_MFMA forces it), else the VALU GEMV (m <= 4, or per 4 rows);
  * otherwise dequantize
  * into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV forces the
  * former (error if it does not fit), RNN_ALGO_TILED the latter. f32 sums in

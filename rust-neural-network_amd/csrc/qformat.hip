@@ -565,6 +565,118 @@ __global__ __launch_bounds__(256) void qt_gemv_kernel(
     }
 }
 
+// ------------------------------------------------------------ MFMA GEMV (m up to 16)
+
+// QuantizedLinear::forward for 5..16 rows of x on v_mfma_f32_16x16x4f32, all
+// rows at once (the VALU GEMV above re-reads the weights for every 4 rows).
+// A workgroup of 8 waves owns 16*NT output columns (weight rows); wave w takes
+// the w-th eighth of K. Lane l = 16*k4 + i provides, per MFMA, the A value
+// x[i][k] and the B value W[n0 + i][k] for the same k: both walk the lane's
+// 16-byte weight piece (EP codes of row i at k = kc + k4*EP + t, MFMA t). The
+// codes are decoded and scaled in registers -- the value is exactly the
+// reference's dequantized q*s (for INT4, 16q * (s/16)) -- so the MFMA sums
+// x * W as QuantizedLinear::forward does, in its own order. Rows of x past m
+// read row m-1 and their outputs are dropped. Partial 16x16 tiles of the 8
+// waves are summed through LDS.
+constexpr int kMfmaWaves = 8;
+
+template <int KIND, int NT, bool SCALED, bool BIAS>
+__global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
+    const float *__restrict__ x, int mrows, int64_t K, const uint8_t *__restrict__ data,
+    const float *__restrict__ scales, int64_t ns, uint32_t g, uint32_t kg, uint32_t rpg, int64_t N,
+    const float *__restrict__ bias, float *__restrict__ y) {
+    using F = Fmt<KIND>;
+    constexpr int EP = F::EP;  // elements per 16-byte piece
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __shared__ float part[kMfmaWaves][NT][16][17];
+    __shared__ float lut[16];
+    if ((KIND == KIND_NF4 || KIND == KIND_E2M1) && threadIdx.x < 16)
+        lut[threadIdx.x] = KIND == KIND_NF4 ? kNF4[threadIdx.x] : kE2M1[threadIdx.x];
+    __syncthreads();
+    const int wid = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int i = lane % 16, k4 = lane / 16;
+    const int64_t n0 = (int64_t)blockIdx.x * 16 * NT;
+    const int64_t kw = K / kMfmaWaves, k0 = wid * kw;  // kw % (4 * EP) == 0 (host check)
+    const float *xrow = x + (int64_t)(i < mrows ? i : mrows - 1) * K;
+    const uint8_t *wrow[NT];
+    int64_t gbase[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int64_t n = n0 + 16 * nt + i < N ? n0 + 16 * nt + i : N - 1;
+        wrow[nt] = data + (n * K) * 16 / EP;  // row start (EP codes per 16 bytes)
+        gbase[nt] = !SCALED ? 0 : (kg ? n * (int64_t)kg : (int64_t)((uint32_t)n / rpg));
+    }
+    f4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
+    // One K chunk (4*EP) of this lane: EP values of x and one piece per tile.
+    struct Chunk {
+        float xr[EP];
+        v4i raw[NT];
+        float sc[NT];
+    };
+    auto load = [&](Chunk &c, int64_t kc) {
+        const int64_t e = kc + k4 * EP;
+#pragma unroll
+        for (int q = 0; q < EP / 4; ++q) {
+            const f4 t = *reinterpret_cast<const f4 *>(xrow + e + 4 * q);
+            c.xr[4 * q] = t.x, c.xr[4 * q + 1] = t.y, c.xr[4 * q + 2] = t.z, c.xr[4 * q + 3] = t.w;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            c.raw[nt] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wrow[nt] + e * 16 / EP));
+            if (SCALED) {
+                const int64_t gi = gbase[nt] + (kg ? (int64_t)((uint32_t)e / g) : 0);
+                c.sc[nt] = scales[gi < ns - 1 ? gi : ns - 1];
+            }
+        }
+    };
+    auto compute = [&](const Chunk &c) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            float v[EP];
+            decode_piece<KIND>(c.raw[nt], v, lut);
+            const float s = SCALED ? (KIND == KIND_I4 ? c.sc[nt] * 0.0625f : c.sc[nt]) : 1.0f;
+#pragma unroll
+            for (int t = 0; t < EP; ++t) {
+                const float w = SCALED ? v[t] * s : v[t];
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(c.xr[t], w, acc[nt], 0, 0, 0);
+            }
+        }
+    };
+    // Two chunks in flight (register sets A and B alternate, two chunks per
+    // iteration); loads past the wave's range re-read its last chunk so that
+    // every load is unconditional and the compiler's waits stay exact.
+    const int64_t nch = kw / (4 * EP), lastk = k0 + (nch - 1) * 4 * EP;
+    auto kof = [&](int64_t c) { const int64_t k = k0 + c * 4 * EP; return k < lastk ? k : lastk; };
+    Chunk A, B;
+    load(A, kof(0));
+    load(B, kof(1));
+    for (int64_t c = 0; c < nch; c += 2) {
+        compute(A);
+        load(A, kof(c + 2));
+        if (c + 1 < nch) compute(B);
+        load(B, kof(c + 3));
+    }
+    // lane holds D[m = 4*k4 + r][n = i] of each tile
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[wid][nt][4 * k4 + r][i] = acc[nt][r];
+    __syncthreads();
+    for (int t = threadIdx.x; t < NT * 256; t += kMfmaWaves * 64) {
+        const int nt = t / 256, m = (t / 16) % 16, n = t % 16;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kMfmaWaves; ++w) s += part[w][nt][m][n];
+        const int64_t col = n0 + 16 * nt + n;
+        if (m < mrows && col < N) {
+            if (BIAS) s = s + bias[col];
+            y[(int64_t)m * N + col] = s;
+        }
+    }
+}
+
 __global__ void qt_bias_kernel(float *__restrict__ y, int64_t m, int64_t n,
                                const float *__restrict__ bias) {
     const int64_t total = m * n;
@@ -716,6 +828,37 @@ static void gemv_chunk(int mt, const float *x, int64_t K, const uint8_t *data, c
     else launch_gemv<KIND, 4, 2, SCALED>(x, mt, K, data, scales, ns, g, N, bias, y, st);
 }
 
+template <int KIND, bool SCALED>
+static void launch_mfma(const float *x, int mrows, int64_t K, const uint8_t *data,
+                        const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
+                        float *y, hipStream_t st) {
+    constexpr int NT = 2;
+    const unsigned blocks = (unsigned)ceil_div(N, 16 * NT);
+    const uint32_t kg = K % g == 0 ? (uint32_t)(K / g) : 0u;
+    const uint32_t rpg = kg ? 1u : (uint32_t)(g / K);
+    if (bias)
+        qt_gemv_mfma_kernel<KIND, NT, SCALED, true><<<blocks, kMfmaWaves * 64, 0, st>>>(
+            x, mrows, K, data, scales, ns, (uint32_t)g, kg, rpg, N, bias, y);
+    else
+        qt_gemv_mfma_kernel<KIND, NT, SCALED, false><<<blocks, kMfmaWaves * 64, 0, st>>>(
+            x, mrows, K, data, scales, ns, (uint32_t)g, kg, rpg, N, bias, y);
+}
+
+static void launch_mfma_kind(int kind, const float *x, int mrows, int64_t K, const uint8_t *data,
+                             const float *scales, int64_t ns, int64_t g, int64_t N,
+                             const float *bias, float *y, hipStream_t st) {
+    switch (kind) {
+    case KIND_I4: launch_mfma<KIND_I4, true>(x, mrows, K, data, scales, ns, g, N, bias, y, st); break;
+    case KIND_NF4: launch_mfma<KIND_NF4, true>(x, mrows, K, data, scales, ns, g, N, bias, y, st); break;
+    case KIND_E2M1: launch_mfma<KIND_E2M1, true>(x, mrows, K, data, scales, ns, g, N, bias, y, st); break;
+    case KIND_I8: launch_mfma<KIND_I8, true>(x, mrows, K, data, scales, ns, g, N, bias, y, st); break;
+    case KIND_F16: launch_mfma<KIND_F16, false>(x, mrows, K, data, scales, ns, 1, N, bias, y, st); break;
+    default: launch_mfma<KIND_BF16, false>(x, mrows, K, data, scales, ns, 1, N, bias, y, st); break;
+    }
+}
+
+static int piece_elems(int kind) { return kind4(kind) ? 32 : (kind == KIND_I8 ? 16 : 8); }
+
 // The fused path takes every format: K a multiple of 32, 16-byte aligned x
 // and data, and (for scaled formats) a group that is a multiple of the
 // piece length (32 for 4-bit codes, 16 for int8) and divides or is divided
@@ -740,7 +883,8 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
     RNN_REQUIRE(m >= 0 && in_f >= 0 && out_f >= 0, "%s: negative size", name);
     RNN_TRY(check_tensor(name, format, data, data_bytes, scales, n_scales, group, out_f * in_f));
     const unsigned algo = flags & RNN_ALGO_MASK;
-    RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_GEMV || algo == RNN_ALGO_TILED,
+    RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_GEMV || algo == RNN_ALGO_TILED ||
+                    algo == RNN_ALGO_GEMV_MFMA,
                 "%s: bad algo 0x%x", name, algo);
     if (m == 0 || out_f == 0) return RNN_OK;
     RNN_REQUIRE(y != nullptr && (in_f == 0 || x != nullptr), "%s: null pointer", name);
@@ -758,6 +902,15 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
                                    (in_f % group == 0 || group % in_f == 0))) &&
                       ((uintptr_t)x % 16) == 0 && ((uintptr_t)data % 16) == 0 &&
                       out_f <= 0x7fffffffLL;
+    // the MFMA GEMV takes all m <= 16 rows at once; its 8 waves split K in
+    // whole chunks of 4 pieces
+    const bool fits_mfma = fits && m <= 16 && in_f % (kMfmaWaves * 4 * piece_elems(kind)) == 0;
+    if (algo == RNN_ALGO_GEMV_MFMA || (algo == RNN_ALGO_AUTO && m >= 5 && fits_mfma)) {
+        RNN_REQUIRE(fits_mfma, "%s: the MFMA GEMV needs m <= 16, the fused GEMV's conditions and "
+                    "in_f a multiple of %d", name, kMfmaWaves * 4 * (kind >= 0 ? piece_elems(kind) : 32));
+        launch_mfma_kind(kind, x, (int)m, in_f, data, scales, n_scales, group, out_f, bias, y, st);
+        return check_launch(name);
+    }
     const bool gemv = algo == RNN_ALGO_GEMV || (algo == RNN_ALGO_AUTO && m <= 16 && fits);
     if (gemv) {
         RNN_REQUIRE(fits, "%s: the fused GEMV needs in_f %% 32 == 0, a group that is a multiple of "

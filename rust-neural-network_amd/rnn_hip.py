@@ -26,6 +26,7 @@ ALGO_AUTO = 0x00
 ALGO_TILED = 0x10
 ALGO_GEMV = 0x20
 ALGO_TILED_DMA = 0x30
+ALGO_GEMV_MFMA = 0x40
 
 TERNARY_ROWS = 0
 TERNARY_ABSMEAN = 1

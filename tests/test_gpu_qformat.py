@@ -10,8 +10,8 @@ ABI against the oracle.
 - QuantizedLinear::forward: f32 sums in the kernel's own order, so the bar is
   the GEMM rounding bound |got - exact| <= gamma_(k+2) * sum |x||W| (+ |b| u)
   around the float64 product of the oracle's dequantized weight (gamma_j =
-  j u / (1 - j u), u = 2^-24); both the fused GEMV and the dequantize +
-  f32 GEMM path are forced on the same inputs.
+  j u / (1 - j u), u = 2^-24); the VALU GEMV, the f32-MFMA GEMV and the
+  dequantize + f32 GEMM path are each forced on the same inputs.
 """
 import numpy as np
 import pytest
@@ -144,7 +144,7 @@ def gemm_check(got, x, wdeq, bias):
 @pytest.mark.parametrize("fmt", GEMV_FMTS, ids=[O.QF_NAMES[f] for f in GEMV_FMTS])
 @pytest.mark.parametrize("m,k,n,gs", [(1, 4096, 1000, 128), (3, 2048, 257, 32), (4, 64, 9, 64),
                                       (8, 4096, 512, 32), (16, 2080, 130, 32), (2, 6144, 40, 0),
-                                      (5, 96, 1, 32)])
+                                      (5, 96, 1, 32), (16, 1024, 33, 32), (11, 3072, 70, 1024)])
 def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
     rng = np.random.default_rng(m * 1000 + k + n)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -159,9 +159,9 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
     dd, sd, xd = to_dev(d, dev), to_dev(s if s.size else np.zeros(1, np.float32), dev), to_dev(x, dev)
     for bias in (None, b):
         bd = None if bias is None else to_dev(bias, dev)
-        for algo in (hip.ALGO_GEMV, hip.ALGO_TILED):
-            if algo == hip.ALGO_GEMV and m > 16:
-                continue
+        ep = 32 if O.QF_BITS[fmt] == 4 else (16 if O.QF_BITS[fmt] == 8 else 8)
+        algos = [hip.ALGO_GEMV, hip.ALGO_TILED] + ([hip.ALGO_GEMV_MFMA] if k % (32 * ep) == 0 else [])
+        for algo in algos:
             y = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd, algo=algo))
             gemm_check(y, x, wdeq, bias)
         auto = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd))
@@ -199,7 +199,7 @@ def test_linear_forward_decode_config_sampled(dev, hip):
         dq, sq, _ = hip.qt_quantize(fmt, to_dev(w, dev), gs)
         assert np.array_equal(host(dq), d) and np.array_equal(host(sq), s)
         wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
-        for m in (1, 4):
+        for m in (1, 4, 16):
             x = rng.standard_normal((m, k)).astype(np.float32)
             y = host(hip.qt_linear_forward(fmt, to_dev(x, dev), dq, sq, g, n))
             gemm_check(y, x, wdeq, None)
