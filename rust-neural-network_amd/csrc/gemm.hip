@@ -1607,12 +1607,22 @@ static int launch_dma_auto(const int8_t *A, const int8_t *B, int64_t M, int64_t 
 // balancing.
 static int launch_gemv(const int8_t *A, const int8_t *W, int64_t M, int64_t N, int64_t K,
                        const Epilogue &epi, hipStream_t st, const char *name) {
-    // whole-line weight loads when K % 4096 == 0; activations staged in LDS
-    // for M <= 4
+    // Whole-line weight loads when K % 4096 == 0. Activation rows are staged
+    // in LDS (one contiguous 1 KiB load per row and wave) for M <= 8, and for
+    // M <= 16 while the grid takes at most one workgroup per CU: at 16 rows
+    // the 96 KiB of LDS per workgroup would otherwise cap residency. Measured
+    // against fragment-layout activation loads, K = 4096: M = 8 5.19 vs
+    // 6.04 us (N 4096), 10.17 vs 11.31 (N 11008); M = 16 6.21 vs 6.75
+    // (N 4096), 14.96 vs 13.57 (N 11008, 688 workgroups: not taken).
+    const unsigned wgs = (unsigned)ceil_div(N, 16);
     if (K % 4096 == 0 && M <= 4)
-        gemv_wl_kernel<4, 4><<<(unsigned)ceil_div(N, 16), 256, 0, st>>>(A, W, M, N, K, epi);
+        gemv_wl_kernel<4, 4><<<wgs, 256, 0, st>>>(A, W, M, N, K, epi);
+    else if (K % 4096 == 0 && M <= 8)
+        gemv_wl_kernel<4, 8><<<wgs, 256, 0, st>>>(A, W, M, N, K, epi);
+    else if (K % 4096 == 0 && M <= 16 && (int64_t)wgs <= device_cu_count())
+        gemv_wl_kernel<4, 16><<<wgs, 256, 0, st>>>(A, W, M, N, K, epi);
     else if (K % 4096 == 0)
-        gemv_wl_kernel<4, 0><<<(unsigned)ceil_div(N, 16), 256, 0, st>>>(A, W, M, N, K, epi);
+        gemv_wl_kernel<4, 0><<<wgs, 256, 0, st>>>(A, W, M, N, K, epi);
     else
         gemv_kernel<4, 16><<<(unsigned)ceil_div(N, 16), 256, 0, st>>>(A, W, M, N, K, epi);
     return check_launch(name);
