@@ -589,6 +589,10 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
     constexpr int EP = F::EP;  // elements per 16-byte piece
     typedef float f4 __attribute__((ext_vector_type(4)));
     __shared__ float part[kMfmaWaves][NT][16][17];
+    // per wave, the x chunk (16 rows x 4*EP floats, row pitch 4*EP + 4: the
+    // lanes' 16-byte reads of one pass fall in different banks)
+    constexpr int XP = 4 * EP + 4;
+    __shared__ __attribute__((aligned(16))) float xsh[kMfmaWaves][16 * XP];
     __shared__ float lut[16];
     if ((KIND == KIND_NF4 || KIND == KIND_E2M1) && threadIdx.x < 16)
         lut[threadIdx.x] = KIND == KIND_NF4 ? kNF4[threadIdx.x] : kE2M1[threadIdx.x];
@@ -597,7 +601,10 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
     const int i = lane % 16, k4 = lane / 16;
     const int64_t n0 = (int64_t)blockIdx.x * 16 * NT;
     const int64_t kw = K / kMfmaWaves, k0 = wid * kw;  // kw % (4 * EP) == 0 (host check)
-    const float *xrow = x + (int64_t)(i < mrows ? i : mrows - 1) * K;
+    // x staging: load instruction q covers rows 2q' .. (EP/4 instructions of
+    // 64 lanes x 16 bytes = the 16 x 4*EP chunk, each row contiguous)
+    constexpr int LPR = EP;  // lanes per x row of the chunk (4*EP floats / 4)
+    const int sr0 = lane / LPR, sc4 = lane % LPR;
     const uint8_t *wrow[NT];
     int64_t gbase[NT];
 #pragma unroll
@@ -611,7 +618,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
     for (int nt = 0; nt < NT; ++nt) acc[nt] = f4{0.f, 0.f, 0.f, 0.f};
     // One K chunk (4*EP) of this lane: EP values of x and one piece per tile.
     struct Chunk {
-        float xr[EP];
+        f4 xt[EP / 4];  // this lane's share of the x chunk, before it goes to LDS
         v4i raw[NT];
         float sc[NT];
     };
@@ -619,8 +626,9 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
         const int64_t e = kc + k4 * EP;
 #pragma unroll
         for (int q = 0; q < EP / 4; ++q) {
-            const f4 t = *reinterpret_cast<const f4 *>(xrow + e + 4 * q);
-            c.xr[4 * q] = t.x, c.xr[4 * q + 1] = t.y, c.xr[4 * q + 2] = t.z, c.xr[4 * q + 3] = t.w;
+            const int r = sr0 + q * (64 / LPR);
+            const float *xr = x + (int64_t)(r < mrows ? r : mrows - 1) * K;
+            c.xt[q] = *reinterpret_cast<const f4 *>(xr + kc + 4 * sc4);
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -632,6 +640,18 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
         }
     };
     auto compute = [&](const Chunk &c) {
+        float *xs = xsh[wid];
+#pragma unroll
+        for (int q = 0; q < EP / 4; ++q)
+            *reinterpret_cast<f4 *>(&xs[(sr0 + q * (64 / LPR)) * XP + 4 * sc4]) = c.xt[q];
+        __builtin_amdgcn_wave_barrier();  // one wave's LDS operations complete in order
+        float xv[EP];
+#pragma unroll
+        for (int q = 0; q < EP / 4; ++q) {
+            const f4 t = *reinterpret_cast<const f4 *>(&xs[i * XP + k4 * EP + 4 * q]);
+            xv[4 * q] = t.x, xv[4 * q + 1] = t.y, xv[4 * q + 2] = t.z, xv[4 * q + 3] = t.w;
+        }
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             float v[EP];
@@ -640,7 +660,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
 #pragma unroll
             for (int t = 0; t < EP; ++t) {
                 const float w = SCALED ? v[t] * s : v[t];
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(c.xr[t], w, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t], w, acc[nt], 0, 0, 0);
             }
         }
     };
