@@ -242,7 +242,7 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
  * 32 (4-bit formats) or 16 (INT8, GGUF Q8_0) and divides or is divided by
  * in_f, and 16-byte aligned x and data, a fused GEMV that decodes the codes
  * in registers (NF4 and NVFP4 through a 16-entry table; weights read once):
- * for m >= 5 with in_f a multiple of 1024 (4-bit), 512 (8-bit) or 256
+ * for m >= 5 with in_f a multiple of 512 (4-bit), 256 (8-bit) or 128
  * (16-bit) the GEMV on f32 MFMA that takes all m rows at once
  * (RNN_ALGO_GEMV_MFMA forces it), else the VALU GEMV (m <= 4, or per 4 rows);
  * otherwise dequantize

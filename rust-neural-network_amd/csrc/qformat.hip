@@ -569,8 +569,10 @@ __global__ __launch_bounds__(256) void qt_gemv_kernel(
 
 // QuantizedLinear::forward for 5..16 rows of x on v_mfma_f32_16x16x4f32, all
 // rows at once (the VALU GEMV above re-reads the weights for every 4 rows).
-// A workgroup of 8 waves owns 16*NT output columns (weight rows); wave w takes
-// the w-th eighth of K. Lane l = 16*k4 + i provides, per MFMA, the A value
+// A workgroup of 4 waves owns 16*NT output columns (weight rows); wave w takes
+// the w-th quarter of K. (4 waves and one 16-column tile per workgroup: 23 /
+// 25 us at m = 8 / 16 over 4096 x 11008 INT4, against 29-33 for 8 waves or
+// two tiles, which hold fewer workgroups per CU.) Lane l = 16*k4 + i provides, per MFMA, the A value
 // x[i][k] and the B value W[n0 + i][k] for the same k: both walk the lane's
 // 16-byte weight piece (EP codes of row i at k = kc + k4*EP + t, MFMA t). The
 // codes are decoded and scaled in registers -- the value is exactly the
@@ -578,7 +580,7 @@ __global__ __launch_bounds__(256) void qt_gemv_kernel(
 // x * W as QuantizedLinear::forward does, in its own order. Rows of x past m
 // read row m-1 and their outputs are dropped. Partial 16x16 tiles of the 8
 // waves are summed through LDS.
-constexpr int kMfmaWaves = 8;
+constexpr int kMfmaWaves = 4;
 
 template <int KIND, int NT, bool SCALED, bool BIAS>
 __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
@@ -852,7 +854,7 @@ template <int KIND, bool SCALED>
 static void launch_mfma(const float *x, int mrows, int64_t K, const uint8_t *data,
                         const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
                         float *y, hipStream_t st) {
-    constexpr int NT = 2;
+    constexpr int NT = 1;  // 16 columns per workgroup: more workgroups in flight
     const unsigned blocks = (unsigned)ceil_div(N, 16 * NT);
     const uint32_t kg = K % g == 0 ? (uint32_t)(K / g) : 0u;
     const uint32_t rpg = kg ? 1u : (uint32_t)(g / K);
@@ -922,7 +924,7 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
                                    (in_f % group == 0 || group % in_f == 0))) &&
                       ((uintptr_t)x % 16) == 0 && ((uintptr_t)data % 16) == 0 &&
                       out_f <= 0x7fffffffLL;
-    // the MFMA GEMV takes all m <= 16 rows at once; its 8 waves split K in
+    // the MFMA GEMV takes all m <= 16 rows at once; its 4 waves split K in
     // whole chunks of 4 pieces
     const bool fits_mfma = fits && m <= 16 && in_f % (kMfmaWaves * 4 * piece_elems(kind)) == 0;
     if (algo == RNN_ALGO_GEMV_MFMA || (algo == RNN_ALGO_AUTO && m >= 5 && fits_mfma)) {

@@ -160,7 +160,7 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
     for bias in (None, b):
         bd = None if bias is None else to_dev(bias, dev)
         ep = 32 if O.QF_BITS[fmt] == 4 else (16 if O.QF_BITS[fmt] == 8 else 8)
-        algos = [hip.ALGO_GEMV, hip.ALGO_TILED] + ([hip.ALGO_GEMV_MFMA] if k % (32 * ep) == 0 else [])
+        algos = [hip.ALGO_GEMV, hip.ALGO_TILED] + ([hip.ALGO_GEMV_MFMA] if k % (16 * ep) == 0 else [])
         for algo in algos:
             y = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd, algo=algo))
             gemm_check(y, x, wdeq, bias)
