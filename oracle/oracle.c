@@ -461,130 +461,6 @@ void orc_rotorquant_dequantize(const int8_t *codes, const float *scales,
 }
 
 /* ------------------------------------------------------------------ */
-/* Rotor::random via rand 0.8.5 StdRng (ChaCha12) -- parity unpinned   */
-/* ------------------------------------------------------------------ */
-static inline uint32_t rotl32(uint32_t v, int c) { return (v << c) | (v >> (32 - c)); }
-
-#define QR(a, b, c, d)            \
-    a += b; d ^= a; d = rotl32(d, 16); \
-    c += d; b ^= c; b = rotl32(b, 12); \
-    a += b; d ^= a; d = rotl32(d, 8);  \
-    c += d; b ^= c; b = rotl32(b, 7);
-
-static void chacha_core(const uint32_t in[16], int rounds, uint32_t out[16]) {
-    uint32_t x[16];
-    memcpy(x, in, sizeof x);
-    for (int i = 0; i < rounds; i += 2) {
-        QR(x[0], x[4], x[8], x[12]);
-        QR(x[1], x[5], x[9], x[13]);
-        QR(x[2], x[6], x[10], x[14]);
-        QR(x[3], x[7], x[11], x[15]);
-        QR(x[0], x[5], x[10], x[15]);
-        QR(x[1], x[6], x[11], x[12]);
-        QR(x[2], x[7], x[8], x[13]);
-        QR(x[3], x[4], x[9], x[14]);
-    }
-    for (int i = 0; i < 16; ++i) out[i] = x[i] + in[i];
-}
-
-static const uint32_t CHACHA_SIGMA[4] = {0x61707865u, 0x3320646eu, 0x79622d32u,
-                                         0x6b206574u};
-
-void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream,
-                      int rounds, uint32_t out[16]) {
-    uint32_t st[16];
-    memcpy(st, CHACHA_SIGMA, 16);
-    memcpy(st + 4, key, 32);
-    st[12] = (uint32_t)counter;
-    st[13] = (uint32_t)(counter >> 32);
-    st[14] = (uint32_t)stream;
-    st[15] = (uint32_t)(stream >> 32);
-    chacha_core(st, rounds, out);
-}
-
-void orc_chacha20_block_ietf(const uint32_t key[8], uint32_t counter,
-                             const uint32_t nonce[3], uint32_t out[16]) {
-    uint32_t st[16];
-    memcpy(st, CHACHA_SIGMA, 16);
-    memcpy(st + 4, key, 32);
-    st[12] = counter;
-    st[13] = nonce[0];
-    st[14] = nonce[1];
-    st[15] = nonce[2];
-    chacha_core(st, 20, out);
-}
-
-/* rand_chacha ChaCha12Rng as a block RNG: 4 consecutive blocks (64 words)
- * per refill, 64-bit block counter starting at 0, stream 0. */
-struct std_rng {
-    uint32_t key[8];
-    uint64_t counter;
-    uint32_t buf[64];
-    int idx;
-};
-
-/* rand_core 0.6.4 SeedableRng::seed_from_u64: PCG32 output words fill the
- * 32-byte seed little-endian. */
-static void std_rng_seed(struct std_rng *g, uint64_t state) {
-    const uint64_t MUL = 6364136223846793005ull, INC = 11634580027462260723ull;
-    for (int i = 0; i < 8; ++i) {
-        state = state * MUL + INC;
-        uint32_t xs = (uint32_t)(((state >> 18) ^ state) >> 27);
-        uint32_t rot = (uint32_t)(state >> 59);
-        g->key[i] = (xs >> rot) | (xs << ((32 - rot) & 31));
-    }
-    g->counter = 0;
-    g->idx = 64;
-}
-
-static uint32_t std_rng_next_u32(struct std_rng *g) {
-    if (g->idx >= 64) {
-        for (int b = 0; b < 4; ++b)
-            orc_chacha_block(g->key, g->counter + (uint64_t)b, 0, 12, g->buf + 16 * b);
-        g->counter += 4;
-        g->idx = 0;
-    }
-    return g->buf[g->idx++];
-}
-
-/* rand 0.8.5 UniformFloat<f32>::sample_single(low, high). */
-static float std_rng_range_f32(struct std_rng *g, float low, float high) {
-    float scale = high - low;
-    for (;;) {
-        uint32_t bits = (std_rng_next_u32(g) >> 9) | (127u << 23);
-        float v12;
-        memcpy(&v12, &bits, 4);
-        float v01 = v12 - 1.0f;
-        float res = v01 * scale + low;
-        if (res < high) return res;
-    }
-}
-
-void orc_rotorquant_rotors_from_seed(uint64_t seed, size_t n_groups, float *rotors) {
-    struct std_rng g;
-    std_rng_seed(&g, seed);
-    const float PI_F32 = 3.14159265358979323846f;
-    for (size_t i = 0; i < n_groups; ++i) {
-        float a = std_rng_range_f32(&g, -1.0f, 1.0f);
-        float b = std_rng_range_f32(&g, -1.0f, 1.0f);
-        float c = std_rng_range_f32(&g, -1.0f, 1.0f);
-        float norm = sqrtf(a * a + b * b + c * c);
-        float theta = std_rng_range_f32(&g, 0.0f, PI_F32);
-        float *r = rotors + 4 * i;
-        if (norm < 1e-8f) {
-            r[0] = 1.0f; r[1] = 0.0f; r[2] = 0.0f; r[3] = 0.0f;
-            continue;
-        }
-        float ua = a / norm, ub = b / norm, uc = c / norm;
-        float s = cosf(theta / 2.0f), mag = sinf(theta / 2.0f);
-        r[0] = s;
-        r[1] = mag * ua;
-        r[2] = mag * ub;
-        r[3] = mag * uc;
-    }
-}
-
-/* ------------------------------------------------------------------ */
 /* src/blas.rs:104-264 (sgemm contract, gemm_small order)              */
 /* ------------------------------------------------------------------ */
 void orc_sgemm(int transa, int transb, size_t m, size_t n, size_t k, float alpha,

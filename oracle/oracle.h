@@ -10,9 +10,46 @@
  * (file:line into gugu8intel-i9/Rust-Neural-Network). The reference is Rust and
  * cannot be compiled in this image (no cargo/rustc), so there is no oracle/_ref
  * build; every function here is pinned instead by the reference's own
- * known-answer tests, by brute force, closed forms and invariants
- * (tests/test_oracle.py). Functions whose exact values cannot be pinned are
- * marked "parity unpinned" below.
+ * known-answer tests, by brute force, closed forms and invariants. The pin of
+ * each function, chosen so that a dropped term, a wrong sign or index or a
+ * transposed operand fails it (CPU tests under tests/):
+ *   orc_lcg_bytes             reference recurrence, first outputs
+ *                             (test_lcg_generator_matches_reference_recurrence)
+ *   orc_igemm_scalar/_igemm   KAT [-4,7] (src/int8.rs:416-422), the 7 LCG
+ *                             shapes by int64 brute force, bench inputs at
+ *                             512^3, int32 wrap (test_igemm_*)
+ *   orc_quant_rows_i8         closed form: max-abs/127, half-away ties, NaN,
+ *                             saturation, src/int8.rs:322-327 error bound
+ *   orc_int8_dequantize       round trip bound (test_int8_roundtrip_low_error)
+ *   orc_int8_matmul_f32       reciprocal vs division distinguished
+ *                             (test_int8_matmul_f32_uses_reciprocal)
+ *   orc_int8_linear_forward   exact on integer ratios; the reference test's
+ *                             max_diff < 5 against f32 (src/int8.rs:346-369)
+ *   orc_w8a8_linear, orc_relu numpy int64/f32 brute force in the same order
+ *   orc_pack/unpack_ternary   reference KATs (src/ternary.rs:427-446), code 11
+ *   orc_ternary_quantize_*    value counts (src/ternary.rs:402-424), sequential
+ *                             sum, absmean closed form
+ *   orc_ternary_dequantize,
+ *   orc_ternary_gemm_i8       brute force over unpacked codes
+ *   orc_ternary_linear_f32    exact on integer inputs (any order agrees)
+ *   orc_rotor_*               a generic Cl(3,0) geometric product (sandwich =
+ *                             two left products), norm preservation and
+ *                             |R|^4 scaling of non-unit rotors
+ *   orc_rotorquant_*          the reference test's data and bound
+ *                             (src/quant.rs:291-310), |err| <= scale/2 per
+ *                             rotated component, identity rotors = plain group
+ *                             quantization, the zero-group skip (:189-191)
+ *   orc_sgemm                 the reference's 6 sgemm tests and KATs, float64
+ *                             rounding bound with numpy transposes
+ *   orc_f16/bf16 conversions  exhaustive half widening, truncation
+ *                             characterisation, torch RNE for bf16
+ *   orc_qt_*                  the reference's quantize tests, an independent
+ *                             numpy vectorisation, odd-group and Q4_0 KATs
+ *   orc_flash_attention       float64 softmax attention bound, one-hot and
+ *                             uniform cases, empty cache
+ * Rotors are an input everywhere (RotorQuant::rotors is a pub field): the
+ * reference's seeded Rotor::random draws from the rand crate's StdRng, which
+ * is not in this image, so no function here restates that generator.
  *
  * Floating point: compiled with -ffp-contract=off and no fast-math, so every
  * `a*b + c` rounds twice exactly like Rust (which never contracts), divisions
@@ -139,21 +176,6 @@ void orc_rotorquant_quantize(const float *x, size_t rows, size_t dim, int bits,
 void orc_rotorquant_dequantize(const int8_t *codes, const float *scales,
                                size_t rows, size_t dim, const float *rotors,
                                float *y);
-
-/* Rotor::random (src/quant.rs:39-65) driven by rand 0.8.5 StdRng
- * (ChaCha12, rand_chacha 0.3.1) seeded through rand_core 0.6.4
- * seed_from_u64, restated from those crates' published algorithms.
- * PARITY UNPINNED: none of those crates is in this image and the reference's
- * tests only check invariants, so the exact values are not verified; the
- * ChaCha block function itself is pinned by the RFC 7539 test vector via
- * orc_chacha_block. */
-void orc_rotorquant_rotors_from_seed(uint64_t seed, size_t n_groups, float *rotors);
-/* ChaCha block function with `rounds` rounds (20 = RFC 7539). */
-void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream,
-                      int rounds, uint32_t out[16]);
-/* RFC 7539 layout (32-bit counter, 96-bit nonce) for the published vector. */
-void orc_chacha20_block_ietf(const uint32_t key[8], uint32_t counter,
-                             const uint32_t nonce[3], uint32_t out[16]);
 
 /* ---- f32 GEMM (BlasBackend contract) ---- */
 

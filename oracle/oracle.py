@@ -55,9 +55,6 @@ def lib():
             "orc_rotor_rotation_matrix": [_P, _P],
             "orc_rotorquant_quantize": [_P, _SZ, _SZ, ctypes.c_int, _P, _P, _P, _P],
             "orc_rotorquant_dequantize": [_P, _P, _SZ, _SZ, _P, _P],
-            "orc_rotorquant_rotors_from_seed": [ctypes.c_uint64, _SZ, _P],
-            "orc_chacha_block": [_P, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _P],
-            "orc_chacha20_block_ietf": [_P, ctypes.c_uint32, _P, _P],
             "orc_f32_to_f16": [ctypes.c_float],
             "orc_f16_to_f32": [ctypes.c_uint16],
             "orc_f32_to_bf16": [ctypes.c_float],
@@ -273,27 +270,6 @@ def rotorquant_dequantize(codes, scales, dim, rotors):
     y = np.empty((rows, dim), np.float32)
     lib().orc_rotorquant_dequantize(_ptr(c), _ptr(s), rows, dim, _ptr(r), _ptr(y))
     return y
-
-
-def rotors_from_seed(seed, n_groups):
-    """Rotor::random via StdRng (src/quant.rs:39-65, :150-162). Parity unpinned."""
-    out = np.empty((n_groups, 4), np.float32)
-    lib().orc_rotorquant_rotors_from_seed(seed, n_groups, _ptr(out))
-    return out
-
-
-def chacha_block(key_words, counter, stream, rounds):
-    k = _c(key_words, np.uint32)
-    out = np.empty(16, np.uint32)
-    lib().orc_chacha_block(_ptr(k), counter, stream, rounds, _ptr(out))
-    return out
-
-
-def chacha20_block_ietf(key_words, counter, nonce_words):
-    k, nn = _c(key_words, np.uint32), _c(nonce_words, np.uint32)
-    out = np.empty(16, np.uint32)
-    lib().orc_chacha20_block_ietf(_ptr(k), counter, _ptr(nn), _ptr(out))
-    return out
 
 
 # ---------------------------------------------------------------- f32 GEMM

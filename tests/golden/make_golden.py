@@ -132,9 +132,12 @@ def cases() -> dict[str, np.ndarray]:
     g["rotor_mats.rotors"] = r
     g["rotor_mats.m"] = np.stack([O.rotor_rotation_matrix(v) for v in r])
 
-    # --- RotorQuant: the reference test's data and seed (src/quant.rs:291-310):
-    # dim 12, 4 bits, RotorQuant::with_seed(12, 4, 123), data i*0.37-1.5.
-    rq_r = O.rotors_from_seed(123, 4)
+    # --- RotorQuant: the reference test's data and bound (src/quant.rs:291-310):
+    # dim 12, 4 bits, data i*0.37-1.5, error < 0.15 x range. The reference's
+    # with_seed(12, 4, 123) draws its rotors from rand's StdRng, which is not in this
+    # image; the rotors here come from the build's own seeded generator (the formula
+    # of Rotor::random, src/quant.rs:39-65) and are stored with the case.
+    rq_r = W.rotors(4, seed=123)
     data = (np.arange(12, dtype=np.float32) * np.float32(0.37) - np.float32(1.5)).reshape(1, 12)
     y, c, s = O.rotorquant_quantize(data, rq_r, 4)
     g["rq_ref.x"], g["rq_ref.rotors"], g["rq_ref.y"], g["rq_ref.codes"], g["rq_ref.scales"] = \
