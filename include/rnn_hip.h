@@ -9,7 +9,8 @@
  *  - `stream` is a hipStream_t passed as void* (NULL = the null stream). Calls
  *    are asynchronous on that stream; results are visible after it syncs.
  *  - Return value: RNN_OK (0) or an RNN_ERR_* code; rnn_last_error() gives the
- *    calling thread's message. The reference panics on the same conditions
+ *    calling thread's message for its most recent call (empty after a call
+ *    that succeeded). The reference panics on the same conditions
  *    (e.g. src/int8.rs:72, src/quant.rs:136,215-220); a Rust binding maps a
  *    non-zero status to panic!.
  *  - Thread safety: no global mutable state apart from the per-thread error
@@ -151,13 +152,17 @@ int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_t *packed,
 /* ------------------------------------------------------- RotorQuant (a10-a12) */
 
 /* Rotor::rotation_matrix (src/quant.rs:101-113) for n rotors {s,p12,p13,p23};
- * rot9 receives n row-major 3x3 matrices. */
+ * rot9 receives n row-major 3x3 matrices. As in the reference, the sandwich
+ * applies R and then its reverse both on the left (:84-89 over apply,
+ * :70-81), so the matrix is |R|^2 * I (rounded as the reference rounds it):
+ * the identity, up to f32 rounding, for unit rotors. */
 int rnn_rotor_rotation_matrices(const float *rotors, int64_t n, float *rot9,
                                 void *stream);
 
 /* RotorQuant::quantize / Module::forward (src/quant.rs:212-252, quantize_vec
  * :170-208) over x [rows, dim]: zero-pad to padded_dim = ceil(dim/3)*3, per
- * 3-group rotate, scale = max|rv|/qmax, q = (rv/scale).round().clamp(+-qmax),
+ * 3-group rotate (by the rotation matrix above, so |R|^2 * I: for unit rotors
+ * this is per-group absmax quantization, as the reference computes it), scale = max|rv|/qmax, q = (rv/scale).round().clamp(+-qmax),
  * rv = q*scale, inverse-rotate, trim. rotors: ceil(dim/3) x {s,p12,p13,p23}
  * (RotorQuant::rotors, src/quant.rs:127). bits in [2,8] (qmax = 2^(bits-1)-1).
  * y [rows,dim] receives the reconstruction (may be NULL when codes is set);
@@ -194,6 +199,26 @@ int rnn_rotorquant_dequantize(const int8_t *codes, const float *scales,
 int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k,
               float alpha, const float *a, int64_t lda, const float *b,
               int64_t ldb, float beta, float *c, int64_t ldc, void *stream);
+
+/* Tensor::relu (src/tensor.rs:2025-2032): y[i] = x[i].max(0.0), NaN -> 0 as
+ * f32::max returns the non-NaN operand; y may equal x. */
+int rnn_relu(const float *x, int64_t n, float *y, void *stream);
+
+/* The fused bias add + activation of Tensor::linear_layer
+ * (src/tensor.rs:771-786), in place on y [rows, cols]: y = y + bias[col]
+ * (skipped when bias is NULL), then with relu = 1 y = (y > 0 ? y : 0). */
+int rnn_bias_act(float *y, const float *bias, int64_t rows, int64_t cols,
+                 int relu, void *stream);
+
+/* Tensor::linear_layer (src/tensor.rs:747-800) -- the call Linear::forward
+ * makes (src/nn.rs:36-82): y [batch, out_f] = act(x [batch, in_f] . W^T + b)
+ * with W stored [out_f, in_f] (nn::Linear::weight), as rnn_sgemm (transb = 1,
+ * beta = 0) followed by rnn_bias_act. bias may be NULL (Linear without bias);
+ * relu 0 = FusedAct::Identity, 1 = FusedAct::Relu. Within the rnn_sgemm
+ * rounding bound of the reference. */
+int rnn_linear_layer(const float *x, int64_t batch, int64_t in_f,
+                     const float *w, int64_t out_f, const float *bias, int relu,
+                     float *y, void *stream);
 
 /* ------------------------------------- QuantizedTensor formats (next row) */
 

@@ -51,6 +51,11 @@ int device_cu_count();
         if (!(cond)) return ::rnn::set_error(RNN_ERR_INVALID_ARG, __VA_ARGS__); \
     } while (0)
 
+// First statement of every status-returning entry point: a call that succeeds
+// leaves rnn_last_error() empty, so the message always belongs to the calling
+// thread's most recent call.
+#define RNN_ENTRY() ::rnn::clear_error()
+
 #define RNN_TRY(expr)                   \
     do {                                \
         int _rc = (expr);               \

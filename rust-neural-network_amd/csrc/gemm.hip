@@ -1638,6 +1638,7 @@ extern "C" int rnn_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *
                                const float *sw, const float *bias, int64_t m, int64_t k,
                                int64_t n, unsigned flags, float *y, int32_t *acc_out,
                                void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_w8a8_linear";
     RNN_REQUIRE(m >= 0 && k >= 0 && n >= 0, "%s: negative size", name);
     RNN_REQUIRE((flags & ~(RNN_FLAG_RELU | RNN_ALGO_MASK)) == 0, "%s: unknown flags 0x%x", name, flags);
@@ -1674,6 +1675,7 @@ extern "C" int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_
                                 const float *sw, const float *bias, int64_t m, int64_t k,
                                 int64_t n, unsigned flags, float *y, int32_t *acc_out,
                                 void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_ternary_gemm";
     RNN_REQUIRE(m >= 0 && k >= 0 && n >= 0, "%s: negative size", name);
     RNN_REQUIRE((flags & ~(RNN_FLAG_RELU | RNN_ALGO_MASK)) == 0, "%s: unknown flags 0x%x", name,
@@ -1723,6 +1725,7 @@ extern "C" size_t rnn_igemm_workspace_size(int64_t m, int64_t k, int64_t n) {
 
 extern "C" int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k,
                          int64_t n, void *workspace, size_t workspace_bytes, void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_igemm";
     RNN_REQUIRE(m >= 0 && k >= 0 && n >= 0, "%s: negative size", name);
     if (m == 0 || n == 0) return RNN_OK;

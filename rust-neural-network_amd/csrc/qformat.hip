@@ -718,6 +718,7 @@ using namespace rnn;
 
 extern "C" int rnn_qt_layout(int format, int64_t n, int64_t group_size, int64_t *data_bytes,
                              int64_t *n_scales, int64_t *stored_group) {
+    RNN_ENTRY();
     RNN_REQUIRE(format >= RNN_QF_FP16 && format <= RNN_QF_GGUF_Q8, "rnn_qt_layout: bad format %d",
                 format);
     RNN_REQUIRE(n >= 0 && group_size >= 0, "rnn_qt_layout: negative size");
@@ -740,6 +741,7 @@ extern "C" int rnn_qt_layout(int format, int64_t n, int64_t group_size, int64_t 
 
 extern "C" int rnn_qt_quantize(int format, const float *x, int64_t n, int64_t group_size,
                                uint8_t *data, float *scales, void *stream) {
+    RNN_ENTRY();
     int64_t nb, ng, g;
     RNN_TRY(rnn_qt_layout(format, n, group_size, &nb, &ng, &g));
     if (n == 0) return RNN_OK;
@@ -801,6 +803,7 @@ static int check_tensor(const char *name, int format, const uint8_t *data, int64
 extern "C" int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
                                  const float *scales, int64_t n_scales, int64_t group, int64_t n,
                                  float *out, void *stream) {
+    RNN_ENTRY();
     RNN_TRY(check_tensor("rnn_qt_dequantize", format, data, data_bytes, scales, n_scales, group, n));
     if (n == 0) return RNN_OK;
     RNN_REQUIRE(out != nullptr, "rnn_qt_dequantize: null out");
@@ -901,6 +904,7 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
                                      const uint8_t *data, int64_t data_bytes, const float *scales,
                                      int64_t n_scales, int64_t group, int64_t out_f,
                                      const float *bias, float *y, unsigned flags, void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_qt_linear_forward";
     RNN_REQUIRE(m >= 0 && in_f >= 0 && out_f >= 0, "%s: negative size", name);
     RNN_TRY(check_tensor(name, format, data, data_bytes, scales, n_scales, group, out_f * in_f));

@@ -89,6 +89,7 @@ using namespace rnn;
 
 extern "C" int rnn_quant_rows_i8(const float *x, int64_t rows, int64_t cols, int8_t *q,
                                  float *scale, void *stream) {
+    RNN_ENTRY();
     RNN_REQUIRE(rows >= 0 && cols >= 0, "rnn_quant_rows_i8: negative size");
     RNN_REQUIRE(rows <= 0x7fffffff, "rnn_quant_rows_i8: rows too large");
     if (rows == 0) return RNN_OK;
@@ -104,6 +105,7 @@ extern "C" int rnn_quant_rows_i8(const float *x, int64_t rows, int64_t cols, int
 
 extern "C" int rnn_int8_dequantize(const int8_t *q, const float *scale, int64_t rows,
                                    int64_t cols, float *w, void *stream) {
+    RNN_ENTRY();
     RNN_REQUIRE(rows >= 0 && cols >= 0, "rnn_int8_dequantize: negative size");
     if (rows == 0 || cols == 0) return RNN_OK;
     RNN_REQUIRE(q && scale && w, "rnn_int8_dequantize: null pointer");
@@ -133,6 +135,7 @@ static int launch_int8_ref(bool inv, const float *x, int64_t batch, int64_t in_f
 
 extern "C" int rnn_int8_matmul_f32(const int8_t *wq, const float *ws, int64_t out_f, int64_t in_f,
                                    const float *x, int64_t m, float *y, void *stream) {
+    RNN_ENTRY();
     return launch_int8_ref(true, x, m, in_f, wq, ws, out_f, nullptr, y, stream,
                            "rnn_int8_matmul_f32");
 }
@@ -140,6 +143,7 @@ extern "C" int rnn_int8_matmul_f32(const int8_t *wq, const float *ws, int64_t ou
 extern "C" int rnn_int8_linear_forward(const float *x, int64_t batch, int64_t in_f,
                                        const int8_t *wq, const float *ws, int64_t out_f,
                                        const float *bias, float *y, void *stream) {
+    RNN_ENTRY();
     return launch_int8_ref(false, x, batch, in_f, wq, ws, out_f, bias, y, stream,
                            "rnn_int8_linear_forward");
 }

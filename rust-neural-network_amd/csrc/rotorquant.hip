@@ -286,6 +286,7 @@ using namespace rnn;
 
 extern "C" int rnn_rotor_rotation_matrices(const float *rotors, int64_t n, float *rot9,
                                            void *stream) {
+    RNN_ENTRY();
     RNN_REQUIRE(n >= 0, "rnn_rotor_rotation_matrices: negative n");
     if (n == 0) return RNN_OK;
     RNN_REQUIRE(rotors && rot9, "rnn_rotor_rotation_matrices: null pointer");
@@ -297,6 +298,7 @@ extern "C" int rnn_rotor_rotation_matrices(const float *rotors, int64_t n, float
 extern "C" int rnn_rotorquant_quantize(const float *x, int64_t rows, int64_t dim, int bits,
                                        const float *rotors, float *y, int8_t *codes,
                                        float *scales, void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_rotorquant_quantize";
     RNN_REQUIRE(rows >= 0, "%s: negative rows", name);
     RNN_REQUIRE(dim > 0, "%s: dim must be positive (RotorQuant dim %lld)", name, (long long)dim);
@@ -349,6 +351,7 @@ extern "C" int rnn_rotorquant_quantize(const float *x, int64_t rows, int64_t dim
 extern "C" int rnn_rotorquant_dequantize(const int8_t *codes, const float *scales, int64_t rows,
                                          int64_t dim, const float *rotors, float *y,
                                          void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_rotorquant_dequantize";
     RNN_REQUIRE(rows >= 0 && dim > 0, "%s: bad size", name);
     const int64_t ng = (dim + 2) / 3;

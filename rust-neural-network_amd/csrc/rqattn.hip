@@ -274,6 +274,7 @@ using namespace rnn;
 
 extern "C" int rnn_rotorquant_kv_page_elems(int64_t bh, int64_t seq, int64_t dim,
                                             int64_t *code_elems, int64_t *scale_elems) {
+    RNN_ENTRY();
     RNN_REQUIRE(bh >= 0 && seq >= 0 && dim > 0 && code_elems && scale_elems,
                 "rnn_rotorquant_kv_page_elems: bad argument");
     const int64_t ng = ceil_div(dim, 3), pos = bh * ceil_div(seq, kTile) * kTile;
@@ -285,6 +286,7 @@ extern "C" int rnn_rotorquant_kv_page_elems(int64_t bh, int64_t seq, int64_t dim
 extern "C" int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, int64_t bh,
                                       int64_t seq, int64_t dim, int bits, int kind,
                                       uint16_t *page_codes, float *page_scales, void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_rotorquant_kv_pack";
     RNN_REQUIRE(bh >= 0 && seq >= 0 && dim > 0, "%s: bad size", name);
     RNN_REQUIRE(bits >= 2 && bits <= 4, "%s: the page stores 4-bit codes (bits 2..4), got %d", name,
@@ -306,6 +308,7 @@ extern "C" int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t n
                                            const float *k_rotors, const float *v_rotors,
                                            int64_t seq, int64_t dim, float scale, float *out,
                                            void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_rotorquant_kv_attention";
     RNN_REQUIRE(bh >= 0 && nq >= 0 && seq >= 0 && dim > 0, "%s: bad size", name);
     RNN_REQUIRE(dim <= 192, "%s: head dim %lld > 192 (at most 64 groups per wave)", name,

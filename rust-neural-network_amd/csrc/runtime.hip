@@ -1,4 +1,6 @@
 // runtime.hip -- error reporting and device queries shared by every entry point.
+#include <atomic>
+
 #include "common.hpp"
 
 namespace rnn {
@@ -15,18 +17,22 @@ int set_error(int status, const char *fmt, ...) {
 
 void clear_error() { g_err[0] = '\0'; }
 
+// Per-device CU counts, filled on first use. Relaxed atomics: racing threads
+// compute and store the same value, so no ordering is needed beyond the store
+// itself being whole.
+static std::atomic<int> g_cu_count[64];
+
 int device_cu_count() {
-    static int cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             n <= 0)
             n = 256;
-        cached[dev] = n;
+        g_cu_count[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 
 }  // namespace rnn

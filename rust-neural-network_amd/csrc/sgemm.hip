@@ -218,6 +218,7 @@ using namespace rnn;
 extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k, float alpha,
                          const float *a, int64_t lda, const float *b, int64_t ldb, float beta,
                          float *c, int64_t ldc, void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_sgemm";
     RNN_REQUIRE(m >= 0 && n >= 0 && k >= 0, "%s: negative size", name);
     RNN_REQUIRE((transa == 0 || transa == 1) && (transb == 0 || transb == 1),

@@ -148,6 +148,7 @@ __global__ __launch_bounds__(256) void ternary_linear_ref_kernel(
 using namespace rnn;
 
 extern "C" int rnn_ternary_pack(const int8_t *t, int64_t count, uint32_t *packed, void *stream) {
+    RNN_ENTRY();
     RNN_REQUIRE(count >= 0, "rnn_ternary_pack: negative count");
     if (count == 0) return RNN_OK;
     RNN_REQUIRE(t && packed, "rnn_ternary_pack: null pointer");
@@ -157,6 +158,7 @@ extern "C" int rnn_ternary_pack(const int8_t *t, int64_t count, uint32_t *packed
 }
 
 extern "C" int rnn_ternary_unpack(const uint32_t *packed, int64_t count, int8_t *t, void *stream) {
+    RNN_ENTRY();
     RNN_REQUIRE(count >= 0, "rnn_ternary_unpack: negative count");
     if (count == 0) return RNN_OK;
     RNN_REQUIRE(t && packed, "rnn_ternary_unpack: null pointer");
@@ -166,6 +168,7 @@ extern "C" int rnn_ternary_unpack(const uint32_t *packed, int64_t count, int8_t 
 
 extern "C" int rnn_ternary_quantize(const float *w, int64_t rows, int64_t cols, int mode,
                                     uint32_t *packed, float *scales, void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_ternary_quantize";
     RNN_REQUIRE(rows >= 0 && cols >= 0, "%s: negative size", name);
     RNN_REQUIRE(mode == RNN_TERNARY_ROWS || mode == RNN_TERNARY_ABSMEAN, "%s: bad mode %d", name,
@@ -200,6 +203,7 @@ extern "C" int rnn_ternary_quantize(const float *w, int64_t rows, int64_t cols, 
 
 extern "C" int rnn_ternary_dequantize(const uint32_t *packed, int64_t numel, const float *scales,
                                       int64_t n_scales, int64_t cols, float *w, void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_ternary_dequantize";
     RNN_REQUIRE(numel >= 0 && cols > 0 && n_scales > 0, "%s: bad size", name);
     if (numel == 0) return RNN_OK;
@@ -213,6 +217,7 @@ extern "C" int rnn_ternary_linear_forward(const float *x, int64_t batch, int64_t
                                           const uint32_t *packed, const float *scales,
                                           int64_t out_f, const float *bias, float *y,
                                           void *stream) {
+    RNN_ENTRY();
     const char *name = "rnn_ternary_linear_forward";
     RNN_REQUIRE(batch >= 0 && in_f >= 0 && out_f >= 0, "%s: negative size", name);
     RNN_REQUIRE(batch <= 65535, "%s: batch > 65535 unsupported", name);

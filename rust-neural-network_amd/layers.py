@@ -13,10 +13,87 @@ through `rnn_hip`; nothing here computes on the CPU.
 
 `from_model` takes the flat parameter list of `Module::parameters()` (weights
 `[out, in]`, biases 1-D, in layer order), the reference's input to
-`TernaryModel::from_model`."""
+`TernaryModel::from_model`.
+
+`Module` mirrors the reference's layer trait (src/nn.rs:6-12), with `Linear`,
+`ReLU` and `Sequential` (src/nn.rs:14-145) over the f32 kernels, so that the
+quantized layers, which implement it too, sit in one `Sequential` next to f32
+layers."""
 from __future__ import annotations
 
 import rnn_hip as H
+
+
+# ------------------------------------------------------------------ Module
+class Module:
+    """trait Module (src/nn.rs:6-12): `forward`, `parameters` (the f32 tensors
+    the layer holds, in the order an optimizer or `save_model` sees them) and
+    `set_training` (a no-op unless the layer behaves differently in training,
+    like Dropout; every layer here is inference-only)."""
+
+    def forward(self, x):
+        raise NotImplementedError
+
+    def parameters(self):
+        return []
+
+    def set_training(self, training):
+        pass
+
+    def __call__(self, x):
+        return self.forward(x)
+
+
+class Linear(Module):
+    """nn::Linear (src/nn.rs:14-82): f32 `weight [out, in]` and optional
+    `bias [out]`, forward through Tensor::linear_layer (rnn_linear_layer:
+    x . W^T on the f32 MFMA GEMM, then + bias). Inputs of more than two
+    dimensions are flattened to [leading, in] and restored, as the reference's
+    N-D path does (src/nn.rs:60-78)."""
+
+    def __init__(self, weight, bias=None):
+        self.weight, self.bias = weight, bias
+
+    def forward(self, x):
+        in_f = x.shape[-1]
+        lead = tuple(x.shape[:-1])
+        y = H.linear_layer(x.reshape(-1, in_f).contiguous(), self.weight, self.bias)
+        return y.reshape(*lead, self.weight.shape[0])
+
+    def parameters(self):
+        return [self.weight] + ([self.bias] if self.bias is not None else [])
+
+
+class ReLU(Module):
+    """nn::ReLU (src/nn.rs:134-145): Tensor::relu on the device (rnn_relu)."""
+
+    def forward(self, x):
+        return H.relu(x.contiguous())
+
+
+class Sequential(Module):
+    """nn::Sequential (src/nn.rs:85-132): layers applied in order; `add`
+    appends and returns the model for chaining; `parameters` concatenates the
+    layers' in order; `set_training` reaches every layer."""
+
+    def __init__(self, layers=()):
+        self.layers = list(layers)
+
+    def add(self, module):
+        self.layers.append(module)
+        return self
+
+    def forward(self, x):
+        for layer in self.layers:
+            x = layer.forward(x)
+        return x
+
+    def parameters(self):
+        return [p for layer in self.layers for p in layer.parameters()]
+
+    def set_training(self, training):
+        for layer in self.layers:
+            layer.set_training(training)
 
 
 def pair_parameters(shapes):
@@ -71,19 +148,24 @@ class Int8Weights:
         return _mean_abs_diff(original, self.dequantize())
 
 
-class Int8Linear:
+class Int8Linear(Module):
     """src/int8.rs:117-172. `forward` keeps the reference's semantics (the
     activation quantized with the weight's row scale inside the output loop);
     `forward_w8a8` is the per-row dynamic W8A8 path of the benchmark
-    configurations, with the ReLU optionally fused into the epilogue."""
+    configurations, with the ReLU optionally fused into the epilogue. A layer
+    built with `w8a8=True` uses that path as its Module forward.
+    `parameters()` is the bias: the int8 weight is frozen, not an f32 tensor."""
 
-    def __init__(self, int8_weight, bias=None):
-        self.int8_weight, self.bias = int8_weight, bias
+    def __init__(self, int8_weight, bias=None, w8a8=False):
+        self.int8_weight, self.bias, self.w8a8 = int8_weight, bias, w8a8
 
     @classmethod
-    def from_linear(cls, weight, bias=None):
+    def from_linear(cls, weight, bias=None, w8a8=False):
         """Int8Linear::from_linear (src/int8.rs:124-131)."""
-        return cls(Int8Weights.quantize(weight), bias)
+        return cls(Int8Weights.quantize(weight), bias, w8a8)
+
+    def parameters(self):
+        return [self.bias] if self.bias is not None else []
 
     @property
     def in_features(self):
@@ -95,6 +177,8 @@ class Int8Linear:
 
     def forward(self, x):
         """Int8Linear::forward (src/int8.rs:134-172): x `[batch, in]`."""
+        if self.w8a8:
+            return self.forward_w8a8(x)
         return H.int8_linear_forward(x, self.int8_weight.data, self.int8_weight.scales, self.bias)
 
     def forward_w8a8(self, x, relu=False):
@@ -105,7 +189,7 @@ class Int8Linear:
         return y
 
 
-class Int8Model:
+class Int8Model(Module):
     """The int8 counterpart of `TernaryModel` (not in the reference): every
     weight of a parameter list quantized per row, and a device-resident forward
     that chains the W8A8 layers with the ReLU fused between them (the
@@ -125,6 +209,9 @@ class Int8Model:
         for i, layer in enumerate(self.layers):
             x = layer.forward_w8a8(x, relu=relu_between and i + 1 < len(self.layers))
         return x
+
+    def parameters(self):
+        return [p for layer in self.layers for p in layer.parameters()]
 
     def mem_bytes(self):
         return sum(l.int8_weight.mem_bytes() + (0 if l.bias is None else 4 * l.bias.numel())
@@ -175,22 +262,28 @@ class TernaryTensor:
         return self.value_counts()[2] / max(self.numel, 1)
 
 
-class TernaryLinear:
+class TernaryLinear(Module):
     """src/ternary.rs:209-279. `forward` is the reference's sequential f32
     sum (bit-exact); `forward_int8` is the benchmark configuration's int8
-    ternary GEMM over per-row quantized activations."""
+    ternary GEMM over per-row quantized activations, which a layer built with
+    `int8=True` uses as its Module forward. `parameters()` is the bias."""
 
-    def __init__(self, ternary_weight, bias=None):
-        self.ternary_weight, self.bias = ternary_weight, bias
+    def __init__(self, ternary_weight, bias=None, int8=False):
+        self.ternary_weight, self.bias, self.int8 = ternary_weight, bias, int8
         self.out_features, self.in_features = ternary_weight.shape
 
     @classmethod
-    def from_linear(cls, weight, bias=None, mode=H.TERNARY_ROWS):
+    def from_linear(cls, weight, bias=None, mode=H.TERNARY_ROWS, int8=False):
         """TernaryLinear::from_linear (src/ternary.rs:218-232)."""
-        return cls(TernaryTensor.quantize(weight, mode), bias)
+        return cls(TernaryTensor.quantize(weight, mode), bias, int8)
+
+    def parameters(self):
+        return [self.bias] if self.bias is not None else []
 
     def forward(self, x):
         """TernaryLinear::forward (src/ternary.rs:239-279): x `[batch, in]`."""
+        if self.int8:
+            return self.forward_int8(x)
         return H.ternary_linear_forward(x, self.ternary_weight.packed, self.ternary_weight.scales,
                                         self.out_features, self.bias)
 
@@ -201,7 +294,7 @@ class TernaryLinear:
         return y
 
 
-class TernaryModel:
+class TernaryModel(Module):
     """src/ternary.rs:285-362."""
 
     def __init__(self, layers):
@@ -240,6 +333,9 @@ class TernaryModel:
         for i, layer in enumerate(self.layers):
             x = layer.forward_int8(x, relu=relu_between and i + 1 < len(self.layers))
         return x
+
+    def parameters(self):
+        return [p for layer in self.layers for p in layer.parameters()]
 
 
 # ------------------------------------------------------------------ QuantizedTensor
@@ -312,7 +408,7 @@ class QuantizedTensor:
         return _mean_abs_diff(original, self.dequantize())
 
 
-class QuantizedLinear:
+class QuantizedLinear(Module):
     """src/quantize.rs:718-754: a quantized weight `[out, in]` and optional
     f32 bias. `forward` decodes the weight inside the GEMV (or dequantizes
     once and runs the f32 GEMM for many rows)."""
@@ -332,6 +428,10 @@ class QuantizedLinear:
         w = self.weight
         return H.qt_linear_forward(w.format, x.reshape(-1, self.in_features).contiguous(),
                                    w.data, w.scales, w.group_size, self.out_features, self.bias)
+
+    def parameters(self):
+        """The bias (the quantized weight is frozen, not an f32 tensor)."""
+        return [self.bias] if self.bias is not None else []
 
 
 class QuantizedModel:
@@ -366,3 +466,33 @@ class QuantizedModel:
         """src/quantize.rs:799-807."""
         elems = sum(l.weight.numel() for l in self._layers)
         return elems * 4 / max(self.mem_bytes(), 1)
+
+
+# ------------------------------------------------------------------ RotorQuant
+class RotorQuant(Module):
+    """src/quant.rs:122-252: `dim`, `bits`, one Cl(3,0) rotor per 3-group
+    (`rotors`, device f32 [ceil(dim/3), 4] = {s, p12, p13, p23}) and
+    `padded_dim`. The rotors are given, not drawn: the reference draws them on
+    the host with rand's StdRng (`new` / `with_seed`, :135-162), and the same
+    values are what this layer takes. `forward` is the quantize -> dequantize
+    round trip (`impl Module`, :242-252); `parameters()` is empty."""
+
+    def __init__(self, dim, bits, rotors):
+        if not 2 <= bits <= 8:
+            raise ValueError("bits must be in [2, 8]")  # src/quant.rs:136
+        ng = (dim + 2) // 3
+        if tuple(rotors.shape) != (ng, 4):
+            raise ValueError(f"rotors must be [{ng}, 4], got {tuple(rotors.shape)}")
+        self.dim, self.bits, self.rotors = dim, bits, rotors
+        self.padded_dim = 3 * ng
+
+    def quantize(self, x):
+        """RotorQuant::quantize (src/quant.rs:212-239): any shape whose last
+        dimension is `dim`."""
+        if x.shape[-1] != self.dim:  # src/quant.rs:215-220
+            raise ValueError(f"last dim must be {self.dim}, got {x.shape[-1]}")
+        y, _, _ = H.rotorquant_quantize(x.contiguous(), self.rotors, self.bits)
+        return y
+
+    def forward(self, x):
+        return self.quantize(x)

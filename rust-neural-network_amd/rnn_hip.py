@@ -81,6 +81,9 @@ SIGNATURES = {
                                      ctypes.c_float, _P, _P], _INT),
     "rnn_sgemm": ([_INT, _INT, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P, _I64,
                    ctypes.c_float, _P, _I64, _P], _INT),
+    "rnn_relu": ([_P, _I64, _P, _P], _INT),
+    "rnn_bias_act": ([_P, _P, _I64, _I64, _INT, _P], _INT),
+    "rnn_linear_layer": ([_P, _I64, _I64, _P, _I64, _P, _INT, _P, _P], _INT),
 }
 
 _lib = None
@@ -140,6 +143,33 @@ def _dev(t, dtype, name):
     return t
 
 
+def _need(t, n, name, at_least=False):
+    """Raise unless tensor `t` (when given) holds exactly `n` elements (or at
+    least `n` with at_least): a buffer shorter than the sizes passed to the C
+    ABI would be read or written past its end on the device."""
+    if t is None:
+        return
+    got = t.numel()
+    if got < n or (got != n and not at_least):
+        raise RnnError(RNN_ERR_INVALID_ARG,
+                       f"{name} holds {got} elements, {'at least ' if at_least else ''}{n} needed")
+
+
+def _out(t, dtype, n, name):
+    """A caller-supplied output tensor: on the device, of `dtype`, contiguous,
+    `n` elements."""
+    if t is not None:
+        _dev(t, dtype, name)
+        _need(t, n, name)
+    return t
+
+
+def _dims(t, nd, name):
+    if t.dim() != nd:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"{name} must be {nd}-D, got shape {tuple(t.shape)}")
+    return tuple(t.shape)
+
+
 def _empty(shape, dtype, like):
     import torch
     return torch.empty(shape, dtype=dtype, device=like.device)
@@ -150,9 +180,10 @@ def quant_rows_i8(x, q=None, scale=None, stream=None):
     """Per-row symmetric int8 (Int8Weights::quantize rule). Returns (q, scale)."""
     import torch
     _dev(x, torch.float32, "x")
-    rows, cols = x.shape
-    q = q if q is not None else _empty((rows, cols), torch.int8, x)
-    scale = scale if scale is not None else _empty((rows,), torch.float32, x)
+    rows, cols = _dims(x, 2, "x")
+    q = _out(q, torch.int8, rows * cols, "q") if q is not None else _empty((rows, cols), torch.int8, x)
+    scale = (_out(scale, torch.float32, rows, "scale") if scale is not None
+             else _empty((rows,), torch.float32, x))
     _check(load().rnn_quant_rows_i8(_ptr(x), rows, cols, _ptr(q), _ptr(scale), _stream(stream)))
     return q, scale
 
@@ -160,6 +191,8 @@ def quant_rows_i8(x, q=None, scale=None, stream=None):
 def int8_dequantize(q, scale, stream=None):
     import torch
     _dev(q, torch.int8, "q"), _dev(scale, torch.float32, "scale")
+    rows, _ = _dims(q, 2, "q")
+    _need(scale, rows, "scale")
     w = _empty(q.shape, torch.float32, q)
     _check(load().rnn_int8_dequantize(_ptr(q), _ptr(scale), q.shape[0], q.shape[1], _ptr(w),
                                       _stream(stream)))
@@ -169,7 +202,10 @@ def int8_dequantize(q, scale, stream=None):
 def int8_matmul_f32(wq, ws, x, stream=None):
     import torch
     _dev(wq, torch.int8, "wq"), _dev(ws, torch.float32, "ws"), _dev(x, torch.float32, "x")
-    out_f, in_f = wq.shape
+    out_f, in_f = _dims(wq, 2, "wq")
+    _need(ws, out_f, "ws")
+    if in_f == 0 or x.numel() % in_f != 0:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"x ({x.numel()} elements) is not [m, {in_f}]")
     m = x.numel() // in_f
     y = _empty((m, out_f), torch.float32, x)
     _check(load().rnn_int8_matmul_f32(_ptr(wq), _ptr(ws), out_f, in_f, _ptr(x), m, _ptr(y),
@@ -181,8 +217,11 @@ def int8_linear_forward(x, wq, ws, bias=None, stream=None):
     import torch
     _dev(x, torch.float32, "x"), _dev(wq, torch.int8, "wq"), _dev(ws, torch.float32, "ws")
     _dev(bias, torch.float32, "bias")
-    batch, in_f = x.shape
-    out_f = wq.shape[0]
+    batch, in_f = _dims(x, 2, "x")
+    out_f, w_in = _dims(wq, 2, "wq")
+    if w_in != in_f:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"x has {in_f} features, wq expects {w_in}")
+    _need(ws, out_f, "ws"), _need(bias, out_f, "bias")
     y = _empty((batch, out_f), torch.float32, x)
     _check(load().rnn_int8_linear_forward(_ptr(x), batch, in_f, _ptr(wq), _ptr(ws), out_f,
                                           _ptr(bias), _ptr(y), _stream(stream)))
@@ -197,7 +236,12 @@ def igemm(a_u8, b_i8, m, k, n, workspace=None, c=None, stream=None):
     """igemm contract: a u8 [m,k], b i8 [k,n] -> c i32 [m,n]."""
     import torch
     _dev(a_u8, torch.uint8, "a"), _dev(b_i8, torch.int8, "b")
-    c = c if c is not None else _empty((m, n), torch.int32, a_u8)
+    if min(m, k, n) < 0:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"negative size m={m} k={k} n={n}")
+    _need(a_u8, m * k, "a"), _need(b_i8, k * n, "b")
+    c = _out(c, torch.int32, m * n, "c") if c is not None else _empty((m, n), torch.int32, a_u8)
+    if workspace is not None and not (workspace.is_cuda and workspace.is_contiguous()):
+        raise RnnError(RNN_ERR_INVALID_ARG, "workspace must be a contiguous device tensor")
     wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(load().rnn_igemm(_ptr(a_u8), _ptr(b_i8), _ptr(c), m, k, n, _ptr(workspace), wsb,
                             _stream(stream)))
@@ -210,8 +254,12 @@ def w8a8_linear(aq, sa, wq, sw, bias=None, relu=False, algo=ALGO_AUTO, want_y=Tr
     import torch
     _dev(aq, torch.int8, "aq"), _dev(wq, torch.int8, "wq")
     _dev(sa, torch.float32, "sa"), _dev(sw, torch.float32, "sw"), _dev(bias, torch.float32, "bias")
-    m, k = aq.shape
-    n = wq.shape[0]
+    m, k = _dims(aq, 2, "aq")
+    n, wk = _dims(wq, 2, "wq")
+    if wk != k:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"aq has k={k}, wq has k={wk}")
+    _need(sa, m, "sa"), _need(sw, n, "sw"), _need(bias, n, "bias")
+    _out(y, torch.float32, m * n, "y"), _out(acc, torch.int32, m * n, "acc")
     if want_y and y is None:
         y = _empty((m, n), torch.float32, aq)
     if want_acc and acc is None:
@@ -235,6 +283,7 @@ def ternary_pack(t, stream=None):
 def ternary_unpack(packed, count, stream=None):
     import torch
     _dev(packed, torch.int32, "packed")
+    _need(packed, (count + 15) // 16, "packed", at_least=True)
     t = _empty((count,), torch.int8, packed)
     _check(load().rnn_ternary_unpack(_ptr(packed), count, _ptr(t), _stream(stream)))
     return t
@@ -244,7 +293,7 @@ def ternary_quantize(w, mode=TERNARY_ROWS, stream=None):
     """Returns (packed int32 words [ceil(numel/16)], scales f32 [rows])."""
     import torch
     _dev(w, torch.float32, "w")
-    rows, cols = w.shape
+    rows, cols = _dims(w, 2, "w")
     packed = _empty(((rows * cols + 15) // 16,), torch.int32, w)
     scales = _empty((rows,), torch.float32, w)
     _check(load().rnn_ternary_quantize(_ptr(w), rows, cols, mode, _ptr(packed), _ptr(scales),
@@ -255,6 +304,7 @@ def ternary_quantize(w, mode=TERNARY_ROWS, stream=None):
 def ternary_dequantize(packed, numel, scales, cols, stream=None):
     import torch
     _dev(packed, torch.int32, "packed"), _dev(scales, torch.float32, "scales")
+    _need(packed, (numel + 15) // 16, "packed", at_least=True)
     w = _empty((numel,), torch.float32, packed)
     _check(load().rnn_ternary_dequantize(_ptr(packed), numel, _ptr(scales), scales.numel(), cols,
                                          _ptr(w), _stream(stream)))
@@ -265,7 +315,9 @@ def ternary_linear_forward(x, packed, scales, out_f, bias=None, stream=None):
     import torch
     _dev(x, torch.float32, "x"), _dev(packed, torch.int32, "packed")
     _dev(scales, torch.float32, "scales"), _dev(bias, torch.float32, "bias")
-    batch, in_f = x.shape
+    batch, in_f = _dims(x, 2, "x")
+    _need(packed, (out_f * in_f + 15) // 16, "packed", at_least=True)
+    _need(scales, out_f, "scales", at_least=True), _need(bias, out_f, "bias")
     y = _empty((batch, out_f), torch.float32, x)
     _check(load().rnn_ternary_linear_forward(_ptr(x), batch, in_f, _ptr(packed), _ptr(scales),
                                              out_f, _ptr(bias), _ptr(y), _stream(stream)))
@@ -277,7 +329,10 @@ def ternary_gemm(aq, sa, packed, sw, n, bias=None, relu=False, want_y=True, want
     import torch
     _dev(aq, torch.int8, "aq"), _dev(packed, torch.int32, "packed")
     _dev(sa, torch.float32, "sa"), _dev(sw, torch.float32, "sw"), _dev(bias, torch.float32, "bias")
-    m, k = aq.shape
+    m, k = _dims(aq, 2, "aq")
+    _need(packed, (n * k + 15) // 16, "packed", at_least=True)
+    _need(sa, m, "sa"), _need(sw, n, "sw"), _need(bias, n, "bias")
+    _out(y, torch.float32, m * n, "y")
     if want_y and y is None:
         y = _empty((m, n), torch.float32, aq)
     acc = _empty((m, n), torch.int32, aq) if want_acc else None
@@ -291,7 +346,8 @@ def ternary_gemm(aq, sa, packed, sw, n, bias=None, relu=False, want_y=True, want
 def rotation_matrices(rotors, stream=None):
     import torch
     _dev(rotors, torch.float32, "rotors")
-    n = rotors.shape[0]
+    n = rotors.shape[0] if rotors.dim() > 0 else 0
+    _need(rotors, 4 * n, "rotors")
     out = _empty((n, 3, 3), torch.float32, rotors)
     _check(load().rnn_rotor_rotation_matrices(_ptr(rotors), n, _ptr(out), _stream(stream)))
     return out
@@ -302,8 +358,10 @@ def rotorquant_quantize(x, rotors, bits, want_y=True, want_codes=False, y=None, 
     import torch
     _dev(x, torch.float32, "x"), _dev(rotors, torch.float32, "rotors")
     dim = x.shape[-1]
-    rows = x.numel() // dim
+    rows = x.numel() // dim if dim else 0
     ng = (dim + 2) // 3
+    _need(rotors, 4 * ng, "rotors", at_least=True)
+    _out(y, torch.float32, x.numel(), "y")
     if want_y and y is None:
         y = _empty(tuple(x.shape), torch.float32, x)
     codes = _empty((rows, 3 * ng), torch.int8, x) if want_codes else None
@@ -317,7 +375,10 @@ def rotorquant_dequantize(codes, scales, dim, rotors, stream=None):
     import torch
     _dev(codes, torch.int8, "codes"), _dev(scales, torch.float32, "scales")
     _dev(rotors, torch.float32, "rotors")
+    ng = (dim + 2) // 3
     rows = codes.shape[0]
+    _need(codes, rows * 3 * ng, "codes"), _need(scales, rows * ng, "scales")
+    _need(rotors, 4 * ng, "rotors", at_least=True)
     y = _empty((rows, dim), torch.float32, codes)
     _check(load().rnn_rotorquant_dequantize(_ptr(codes), _ptr(scales), rows, dim, _ptr(rotors),
                                             _ptr(y), _stream(stream)))
@@ -333,6 +394,14 @@ def sgemm(transa, transb, m, n, k, alpha, a, lda, b, ldb, beta, c, ldc, stream=N
     import torch
     for t, nm in ((a, "a"), (b, "b"), (c, "c")):
         _dev(t, torch.float32, nm)
+
+    def span(rows, cols, ld):  # elements a row-major [rows, cols] with row stride ld reaches
+        return 0 if rows == 0 or cols == 0 else (rows - 1) * ld + cols
+    if m > 0 and n > 0:
+        _need(c, span(m, n, ldc), "c", at_least=True)
+        if k > 0 and alpha != 0.0:
+            _need(a, span(k, m, lda) if transa else span(m, k, lda), "a", at_least=True)
+            _need(b, span(n, k, ldb) if transb else span(k, n, ldb), "b", at_least=True)
     _check(load().rnn_sgemm(int(transa), int(transb), m, n, k, float(alpha), _ptr(a), lda,
                             _ptr(b), ldb, float(beta), _ptr(c), ldc, _stream(stream)))
     return c
@@ -342,10 +411,50 @@ def matmul(a, b, stream=None):
     """blas::matmul (src/blas.rs:780-799): C = A.B for contiguous [m,k] @ [k,n]."""
     import torch
     _dev(a, torch.float32, "a"), _dev(b, torch.float32, "b")
-    m, k = a.shape
-    n = b.shape[1]
+    m, k = _dims(a, 2, "a")
+    kb, n = _dims(b, 2, "b")
+    if kb != k:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"inner dimensions differ: {k} vs {kb}")
     c = _empty((m, n), torch.float32, a)
     return sgemm(NO_TRANS, NO_TRANS, m, n, k, 1.0, a, k, b, n, 0.0, c, n, stream)
+
+
+def relu(x, out=None, stream=None):
+    """Tensor::relu (src/tensor.rs:2025-2032): x.max(0.0) elementwise (NaN -> 0).
+    `out` may be x itself."""
+    import torch
+    _dev(x, torch.float32, "x")
+    out = _out(out, torch.float32, x.numel(), "out") if out is not None else torch.empty_like(x)
+    _check(load().rnn_relu(_ptr(x), x.numel(), _ptr(out), _stream(stream)))
+    return out
+
+
+def bias_act(y, bias=None, relu=False, stream=None):
+    """The fused bias add + activation of Tensor::linear_layer
+    (src/tensor.rs:771-786), in place on y [rows, cols]."""
+    import torch
+    _dev(y, torch.float32, "y"), _dev(bias, torch.float32, "bias")
+    rows, cols = _dims(y, 2, "y")
+    _need(bias, cols, "bias")
+    _check(load().rnn_bias_act(_ptr(y), _ptr(bias), rows, cols, int(bool(relu)), _stream(stream)))
+    return y
+
+
+def linear_layer(x, w, bias=None, relu=False, out=None, stream=None):
+    """Tensor::linear_layer (src/tensor.rs:747-800): act(x [batch, in] . W^T +
+    b) with W stored [out, in]; bias may be None (Linear without bias)."""
+    import torch
+    _dev(x, torch.float32, "x"), _dev(w, torch.float32, "w"), _dev(bias, torch.float32, "bias")
+    batch, in_f = _dims(x, 2, "x")
+    out_f, w_in = _dims(w, 2, "w")
+    if w_in != in_f:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"x has {in_f} features, w expects {w_in}")
+    _need(bias, out_f, "bias")
+    out = (_out(out, torch.float32, batch * out_f, "out") if out is not None
+           else _empty((batch, out_f), torch.float32, x))
+    _check(load().rnn_linear_layer(_ptr(x), batch, in_f, _ptr(w), out_f, _ptr(bias),
+                                   int(bool(relu)), _ptr(out), _stream(stream)))
+    return out
 
 
 class HipBackend:
@@ -400,8 +509,9 @@ def qt_linear_forward(fmt, x, data, scales, group, out_f, bias=None, algo=ALGO_A
     import torch
     _dev(x, torch.float32, "x"), _dev(data, torch.uint8, "data")
     _dev(scales, torch.float32, "scales"), _dev(bias, torch.float32, "bias")
-    m, in_f = x.shape
-    y = y if y is not None else _empty((m, out_f), torch.float32, x)
+    m, in_f = _dims(x, 2, "x")
+    _need(bias, out_f, "bias")
+    y = _out(y, torch.float32, m * out_f, "y") if y is not None else _empty((m, out_f), torch.float32, x)
     _check(load().rnn_qt_linear_forward(fmt, _ptr(x), m, in_f, _ptr(data), data.numel(),
                                         _ptr(scales), scales.numel(), group, out_f, _ptr(bias),
                                         _ptr(y), algo, _stream(stream)))
@@ -428,6 +538,8 @@ def rotorquant_kv_pack(codes, scales, bh, seq, dim, bits, kind, stream=None):
     scales), both flat."""
     import torch
     _dev(codes, torch.int8, "codes"), _dev(scales, torch.float32, "scales")
+    ng = (dim + 2) // 3
+    _need(codes, bh * seq * 3 * ng, "codes"), _need(scales, bh * seq * ng, "scales")
     nc, ns = rotorquant_kv_page_elems(bh, seq, dim)
     pc = _empty((nc,), torch.int16, codes)
     ps = _empty((ns,), torch.float32, codes)
@@ -448,8 +560,15 @@ def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, o
     for t, nm in ((k_page[1], "k scales"), (v_page[1], "v scales"), (k_rotors, "k rotors"),
                   (v_rotors, "v rotors")):
         _dev(t, torch.float32, nm)
-    bh, nq, dim = q.shape
-    out = out if out is not None else _empty((bh, nq, dim), torch.float32, q)
+    bh, nq, dim = _dims(q, 3, "q")
+    nc, ns = rotorquant_kv_page_elems(bh, seq, dim)
+    for t, n_, nm in ((k_page[0], nc, "k codes"), (v_page[0], nc, "v codes"),
+                      (k_page[1], ns, "k scales"), (v_page[1], ns, "v scales")):
+        _need(t, n_, nm, at_least=True)
+    ng = (dim + 2) // 3
+    _need(k_rotors, 4 * ng, "k rotors", at_least=True), _need(v_rotors, 4 * ng, "v rotors", at_least=True)
+    out = (_out(out, torch.float32, bh * nq * dim, "out") if out is not None
+           else _empty((bh, nq, dim), torch.float32, q))
     _check(load().rnn_rotorquant_kv_attention(_ptr(q), bh, nq, _ptr(k_page[0]), _ptr(k_page[1]),
                                               _ptr(v_page[0]), _ptr(v_page[1]), _ptr(k_rotors),
                                               _ptr(v_rotors), seq, dim, float(scale), _ptr(out),

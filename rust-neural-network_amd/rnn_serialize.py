@@ -14,8 +14,13 @@ tensors (src/serialize.rs).
   standard entries, `name.qdata` (I8 for `Int8Weights::data`, U32 for
   `TernaryTensor::packed`, U8 for `QuantizedTensor::data`) and `name.scales`
   (F32), plus a `__metadata__` string describing the struct (kind, shape, and
-  for `QuantizedTensor` the format and stored group size). Any safetensors
-  reader loads the entries; `safetensors_import` rebuilds the structs.
+  for `QuantizedTensor` the format and stored group size). Readers that follow
+  the safetensors specification (the `safetensors` library, and
+  `safetensors_import` here, which rebuilds the structs) load such files. The
+  reference's own importer does not: it treats `__metadata__` as a tensor
+  (Err "missing data_offsets") and reads every entry as f32 whatever its dtype
+  (src/serialize.rs:209-236). A file meant for it holds f32 tensors only, which
+  is what an export without quantized tensors writes, byte for byte.
 
 Arrays are numpy; torch tensors (on any device) are accepted and copied to
 the host. Host-side byte handling only: no GPU work happens here.
@@ -111,12 +116,20 @@ def load_model(params, data):
     if len(loaded) != len(params):
         raise ValueError(f"parameter count mismatch: model has {len(params)}, "
                          f"checkpoint has {len(loaded)}")
-    for (_, src), dst in zip(loaded, params):
+    for (name, src), dst in zip(loaded, params):
+        # ndarray's assign (src/serialize.rs:138) broadcasts the source to the
+        # parameter's shape and panics when it cannot; a same-size tensor of
+        # another shape is not reinterpreted ([2,3] into [3,2] is an error).
+        try:
+            view = np.broadcast_to(src, tuple(dst.shape))
+        except ValueError:
+            raise ValueError(f"{name}: checkpoint shape {list(src.shape)} does not broadcast to "
+                             f"parameter shape {list(dst.shape)}") from None
         if hasattr(dst, "copy_"):
             import torch
-            dst.copy_(torch.from_numpy(src.reshape(tuple(dst.shape))).to(dst.device))
+            dst.copy_(torch.from_numpy(np.ascontiguousarray(view)).to(dst.device))
         else:
-            dst[...] = src.reshape(dst.shape)
+            dst[...] = view
     return len(loaded)
 
 

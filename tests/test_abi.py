@@ -142,3 +142,86 @@ def test_build_rejects_kernels_demoted_to_scratch():
                 "remark: gemm.hip:20:0:     ScratchSize [bytes/lane]: 1456\n")
     assert build._scratch_kernels(ok) == []
     assert build._scratch_kernels(bad) == ["_ZN3rnn3badEv (1456 B/lane)"]
+
+
+def test_success_clears_the_error_message(lib):
+    # a failing call leaves its message; the next call that succeeds clears it
+    _status(lib.rnn_quant_rows_i8(FAKE, -1, 4, FAKE, FAKE, None), H.RNN_ERR_INVALID_ARG, "negative")
+    assert lib.rnn_quant_rows_i8(FAKE, 0, 4, FAKE, FAKE, None) == H.RNN_OK  # empty: no launch
+    assert H.last_error() == ""
+
+
+def test_new_elementwise_argument_rules(lib):
+    _status(lib.rnn_relu(FAKE, -1, FAKE, None), H.RNN_ERR_INVALID_ARG, "negative")
+    _status(lib.rnn_bias_act(FAKE, FAKE, 2, 2, 2, None), H.RNN_ERR_INVALID_ARG, "relu must be")
+    _status(lib.rnn_linear_layer(FAKE, 2, 4, FAKE, 3, None, 0, None, None), H.RNN_ERR_INVALID_ARG,
+            "null pointer")
+    assert lib.rnn_bias_act(FAKE, None, 4, 4, 0, None) == H.RNN_OK  # nothing to do: no launch
+
+
+# ------------------------------------------------- binding size checks (no GPU)
+class _Stand:
+    """Quacks like a contiguous device tensor for the binding's argument checks;
+    its pointer is never used, because every case below must fail before the
+    C ABI is called (on this GPU-less host a call would not reach a kernel)."""
+
+    def __init__(self, shape, dtype):
+        self.shape, self.dtype, self.is_cuda = tuple(shape), dtype, True
+
+    def dim(self):
+        return len(self.shape)
+
+    def numel(self):
+        n = 1
+        for d in self.shape:
+            n *= d
+        return n
+
+    def is_contiguous(self):
+        return True
+
+    def data_ptr(self):
+        return 256
+
+    def element_size(self):
+        return 1
+
+
+def _rejects(fn, needle):
+    with pytest.raises(H.RnnError) as e:
+        fn()
+    assert e.value.status == H.RNN_ERR_INVALID_ARG and needle in str(e.value), str(e.value)
+
+
+def test_binding_checks_buffer_sizes_before_the_call():
+    import torch
+    i8, f32, i32, u8 = torch.int8, torch.float32, torch.int32, torch.uint8
+    aq, wq = _Stand((4, 64), i8), _Stand((8, 64), i8)
+    sa, sw = _Stand((4,), f32), _Stand((8,), f32)
+    _rejects(lambda: H.w8a8_linear(aq, sa, _Stand((8, 32), i8), sw), "k=32")
+    _rejects(lambda: H.w8a8_linear(aq, _Stand((3,), f32), wq, sw), "sa holds 3")
+    _rejects(lambda: H.w8a8_linear(aq, sa, wq, _Stand((7,), f32)), "sw holds 7")
+    _rejects(lambda: H.w8a8_linear(aq, sa, wq, sw, bias=_Stand((9,), f32)), "bias holds 9")
+    _rejects(lambda: H.w8a8_linear(aq, sa, wq, sw, y=_Stand((4, 7), f32)), "y holds 28")
+    _rejects(lambda: H.w8a8_linear(aq, sa, wq, sw, y=_Stand((4, 8), i32)), "y must be")
+    _rejects(lambda: H.igemm(_Stand((4, 63), u8), _Stand((64, 8), i8), 4, 64, 8), "a holds 252")
+    _rejects(lambda: H.igemm(_Stand((4, 64), u8), _Stand((64, 8), i8), 4, 64, 8,
+                             c=_Stand((4, 9), i32)), "c holds 36")
+    _rejects(lambda: H.quant_rows_i8(_Stand((4, 64), f32), q=_Stand((4, 60), i8)), "q holds 240")
+    _rejects(lambda: H.ternary_gemm(aq, sa, _Stand((8 * 64 // 16 - 1,), i32), sw, 8), "packed holds")
+    _rejects(lambda: H.qt_linear_forward(3, _Stand((2, 64), f32), _Stand((256,), u8),
+                                         _Stand((4,), f32), 32, 8, y=_Stand((2, 7), f32)), "y holds 14")
+    _rejects(lambda: H.rotorquant_quantize(_Stand((5, 128), f32), _Stand((42, 4), f32), 4),
+             "rotors holds 168")
+    _rejects(lambda: H.rotorquant_quantize(_Stand((5, 128), f32), _Stand((43, 4), f32), 4,
+                                           y=_Stand((5, 127), f32)), "y holds 635")
+    # a cache page shorter than the sequence the attention is told to read
+    nc, ns = 2 * 64 * 8 * 6, 2 * 64 * 4 * 11
+    pages = ((_Stand((nc,), torch.int16), _Stand((ns - 4,), f32)),
+             (_Stand((nc,), torch.int16), _Stand((ns,), f32)))
+    _rejects(lambda: H.rotorquant_kv_attention(_Stand((2, 1, 128), f32), pages[0], pages[1],
+                                               _Stand((43, 4), f32), _Stand((43, 4), f32), 64, 0.1),
+             "k scales holds")
+    _rejects(lambda: H.sgemm(0, 0, 4, 4, 4, 1.0, _Stand((15,), f32), 4, _Stand((16,), f32), 4, 0.0,
+                             _Stand((16,), f32), 4), "a holds 15")
+    _rejects(lambda: H.linear_layer(_Stand((2, 64), f32), _Stand((8, 32), f32)), "w expects 32")

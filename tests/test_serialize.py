@@ -135,3 +135,47 @@ def test_import_errors():
     bad = json.dumps({"__metadata__": {"q": json.dumps({"kind": "quantized", "shape": [2]})}}).encode()
     with pytest.raises(ValueError, match="missing qdata"):
         S.safetensors_import(struct.pack("<Q", len(bad)) + bad)
+
+
+def test_load_model_requires_broadcastable_shapes():
+    # ndarray's assign (src/serialize.rs:138): a same-size tensor of another shape
+    # is an error, not a reshape; a broadcastable source fills the parameter
+    b = S.save_model([np.arange(6, dtype=np.float32).reshape(2, 3)])
+    with pytest.raises(ValueError, match="does not broadcast"):
+        S.load_model([np.zeros((3, 2), np.float32)], b)
+    with pytest.raises(ValueError, match="does not broadcast"):
+        S.load_model([np.zeros(6, np.float32)], b)
+    row = S.save_model([np.array([1, 2, 3], np.float32)])
+    p = np.zeros((2, 3), np.float32)
+    assert S.load_model([p], row) == 1
+    assert p.tolist() == [[1, 2, 3], [1, 2, 3]]
+
+
+def _reference_safetensors_import(data):
+    """A restatement of the reference importer's control flow
+    (src/serialize.rs:195-245): every header key is a tensor entry, each needs
+    data_offsets, and every entry is decoded as little-endian f32."""
+    (hl,) = struct.unpack_from("<Q", data, 0)
+    header = json.loads(data[8:8 + hl])
+    out = []
+    for name, ent in header.items():
+        if not isinstance(ent, dict):
+            raise ValueError("entry is not an object")
+        if "data_offsets" not in ent:
+            raise ValueError("missing data_offsets")
+        s, e = ent["data_offsets"]
+        out.append((name, np.frombuffer(data[8 + hl + s:8 + hl + e][: (e - s) // 4 * 4], "<f4")))
+    return out
+
+
+def test_reference_importer_reads_f32_exports_but_not_quantized_ones():
+    f32 = [("w", np.arange(6, dtype=np.float32).reshape(2, 3))]
+    plain = S.safetensors_export(f32)
+    got = _reference_safetensors_import(plain)
+    assert [n for n, _ in got] == ["w"] and got[0][1].tolist() == list(range(6))
+    q = S.QuantEntry("int8_weights", np.ones((2, 4), np.int8), np.ones(2, np.float32), (2, 4))
+    mixed = S.safetensors_export(f32, [("layer", q)])
+    with pytest.raises(ValueError, match="missing data_offsets"):
+        _reference_safetensors_import(mixed)
+    tensors, quant = S.safetensors_import(mixed)       # this importer reads both
+    assert [n for n, _ in tensors] == ["w"] and list(quant) == ["layer"]
