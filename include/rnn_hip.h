@@ -92,6 +92,19 @@ int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m,
               int64_t k, int64_t n, void *workspace, size_t workspace_bytes,
               void *stream);
 
+/* No counterpart in the reference: rnn_igemm for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same contract and results as rnn_igemm; the workspace is
+ * a file-scope device array of RNN_IGEMM_NOALLOC_MAX_BYTES that each GPU the
+ * library runs on holds until the process ends. Sizes whose
+ * rnn_igemm_workspace_size() exceeds it return RNN_ERR_UNSUPPORTED. Nothing
+ * is allocated and nothing needs clearing between calls. Calls on one GPU
+ * share that GPU's array: calls ordered on one stream are safe, calls that
+ * overlap on one GPU (other streams, other threads) race. */
+#define RNN_IGEMM_NOALLOC_MAX_BYTES (64u << 20)
+int rnn_igemm_noalloc(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m,
+                      int64_t k, int64_t n, void *stream);
+
 /* W8A8 linear (the igemm contract's "caller applies scales"
  * step of src/int8.rs:283-284 fused into the GEMM store, in the multiply
  * order of src/int8.rs:159-162):

@@ -6,6 +6,7 @@
 // (the reference's u8 x i8 [K,N] contract via a pack step + zero-point
 // correction) and rnn_ternary_gemm (B = 2-bit codes decoded in the tile loader).
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1723,6 +1724,39 @@ extern "C" size_t rnn_igemm_workspace_size(int64_t m, int64_t k, int64_t n) {
     return (size_t)(up(m * kp) + up(n * kp) + up(4 * n));
 }
 
+// The pack / transpose / colsum / GEMM sequence of igemm on a workspace of
+// rnn_igemm_workspace_size(m, k, n) bytes (16-byte aligned). Every workspace
+// byte the GEMM reads is written by this call first (the packs write their
+// zero padding too), so the workspace needs no clearing.
+static int igemm_on_workspace(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k,
+                              int64_t n, void *workspace, hipStream_t st, const char *name) {
+    const int64_t kp = igemm_kp(k);
+    auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
+    int8_t *ap = static_cast<int8_t *>(workspace);
+    int8_t *bt = ap + up(m * kp);
+    int32_t *cs = reinterpret_cast<int32_t *>(bt + up(n * kp));
+    const int cus = device_cu_count();
+    RNN_REQUIRE(ceil_div(kp, 64) <= 65535, "%s: k too large", name);
+    pack_a_u8_kernel<<<(unsigned)std::min<int64_t>(ceil_div(m * kp, 256), 8 * cus), 256, 0, st>>>(
+        a, m, k, kp, ap);
+    RNN_TRY(check_launch(name));
+    dim3 g((unsigned)ceil_div(n, 64), (unsigned)ceil_div(kp, 64));
+    transpose_b_kernel<<<g, 256, 0, st>>>(b, k, n, kp, bt);
+    RNN_TRY(check_launch(name));
+    colsum_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(b, k, n, cs);
+    RNN_TRY(check_launch(name));
+    Epilogue epi{nullptr, nullptr, nullptr, nullptr, c, cs, m, n, 0};
+    if (m <= 16) return launch_gemv(ap, bt, m, n, kp, epi, st, name);
+    return launch_tiled<128, 128, 64, 64, false>(ap, bt, m, n, kp, epi, st, name);
+}
+
+// C = 0 for an empty reduction (a fill kernel, safe under graph capture).
+static int igemm_empty(int32_t *c, int64_t m, int64_t n, hipStream_t st, const char *name) {
+    fill_i32_kernel<<<(unsigned)std::min<int64_t>(ceil_div(m * n, 256), 8 * device_cu_count()), 256,
+                      0, st>>>(c, m * n, 0);
+    return check_launch(name);
+}
+
 extern "C" int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k,
                          int64_t n, void *workspace, size_t workspace_bytes, void *stream) {
     RNN_ENTRY();
@@ -1731,53 +1765,65 @@ extern "C" int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t 
     if (m == 0 || n == 0) return RNN_OK;
     RNN_REQUIRE(c != nullptr, "%s: null c", name);
     hipStream_t st = as_stream(stream);
-    if (k == 0) {  // empty reduction: C = 0 (a fill kernel, safe under graph capture)
-        fill_i32_kernel<<<(unsigned)std::min<int64_t>(ceil_div(m * n, 256), 8 * device_cu_count()),
-                          256, 0, st>>>(c, m * n, 0);
-        return check_launch(name);
-    }
+    if (k == 0) return igemm_empty(c, m, n, st, name);
     RNN_REQUIRE(a && b, "%s: null operand", name);
     const size_t need = rnn_igemm_workspace_size(m, k, n);
-    bool owned = false;
-    if (workspace == nullptr) {
-        RNN_TRY(check_hip(hipMallocAsync(&workspace, need, st), name));
-        owned = true;
-    } else {
+    if (workspace != nullptr) {
         RNN_REQUIRE(workspace_bytes >= need, "%s: workspace %zu < %zu bytes", name,
                     workspace_bytes, need);
         RNN_REQUIRE(aligned16(workspace), "%s: workspace must be 16-byte aligned", name);
+        return igemm_on_workspace(a, b, c, m, k, n, workspace, st, name);
     }
-    const int64_t kp = igemm_kp(k);
-    auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
-    int8_t *ap = static_cast<int8_t *>(workspace);
-    int8_t *bt = ap + up(m * kp);
-    int32_t *cs = reinterpret_cast<int32_t *>(bt + up(n * kp));
-    const int cus = device_cu_count();
-    int rc = RNN_OK;
-    pack_a_u8_kernel<<<(unsigned)std::min<int64_t>(ceil_div(m * kp, 256), 8 * cus), 256, 0, st>>>(
-        a, m, k, kp, ap);
-    rc = check_launch(name);
-    if (rc == RNN_OK && ceil_div(kp, 64) > 65535)
-        rc = set_error(RNN_ERR_UNSUPPORTED, "%s: k too large", name);
-    if (rc == RNN_OK) {
-        dim3 g((unsigned)ceil_div(n, 64), (unsigned)ceil_div(kp, 64));
-        transpose_b_kernel<<<g, 256, 0, st>>>(b, k, n, kp, bt);
-        rc = check_launch(name);
+    RNN_TRY(check_hip(hipMallocAsync(&workspace, need, st), name));
+    int rc = igemm_on_workspace(a, b, c, m, k, n, workspace, st, name);
+    int rf = check_hip(hipFreeAsync(workspace, st), name);
+    return rc != RNN_OK ? rc : rf;
+}
+
+// ------------------------------------------------------ igemm, no allocation
+// The workspace of rnn_igemm_noalloc: a file-scope device array, one copy per
+// GPU, held until the process ends. Host code never uses its name as an
+// address (on the host it is only a stand-in for the symbol): the device
+// address comes from hipGetSymbolAddress, once per device, with that device
+// current, and is kept in g_scratch_dev.
+static __device__ __align__(256) int8_t scratch[RNN_IGEMM_NOALLOC_MAX_BYTES];
+
+static std::mutex g_scratch_mu;
+static void *g_scratch_dev[64];
+
+static int scratch_address(void **out, const char *name) {
+    int dev = -1;
+    RNN_TRY(check_hip(hipGetDevice(&dev), name));
+    RNN_REQUIRE(dev >= 0 && dev < 64, "%s: device ordinal %d out of range", name, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev[dev] == nullptr) {
+        void *p = nullptr;
+        RNN_TRY(check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), name));
+        RNN_REQUIRE(p != nullptr && aligned16(p), "%s: scratch symbol has no device address", name);
+        g_scratch_dev[dev] = p;
     }
-    if (rc == RNN_OK) {
-        colsum_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(b, k, n, cs);
-        rc = check_launch(name);
-    }
-    if (rc == RNN_OK) {
-        Epilogue epi{nullptr, nullptr, nullptr, nullptr, c, cs, m, n, 0};
-        if (m <= 16)
-            rc = launch_gemv(ap, bt, m, n, kp, epi, st, name);
-        else
-            rc = launch_tiled<128, 128, 64, 64, false>(ap, bt, m, n, kp, epi, st, name);
-    }
-    if (owned) {
-        int rf = check_hip(hipFreeAsync(workspace, st), name);
-        if (rc == RNN_OK) rc = rf;
-    }
-    return rc;
+    *out = g_scratch_dev[dev];
+    return RNN_OK;
+}
+
+extern "C" int rnn_igemm_noalloc(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m,
+                                 int64_t k, int64_t n, void *stream) {
+    RNN_ENTRY();
+    const char *name = "rnn_igemm_noalloc";
+    RNN_REQUIRE(m >= 0 && k >= 0 && n >= 0, "%s: negative size", name);
+    if (m == 0 || n == 0) return RNN_OK;
+    RNN_REQUIRE(c != nullptr, "%s: null c", name);
+    hipStream_t st = as_stream(stream);
+    if (k == 0) return igemm_empty(c, m, n, st, name);
+    RNN_REQUIRE(a && b, "%s: null operand", name);
+    const size_t need = rnn_igemm_workspace_size(m, k, n);
+    if (need > (size_t)RNN_IGEMM_NOALLOC_MAX_BYTES)
+        return set_error(RNN_ERR_UNSUPPORTED,
+                         "%s: m=%lld k=%lld n=%lld needs %zu bytes of workspace, more than the "
+                         "%zu-byte device array (use rnn_igemm)",
+                         name, (long long)m, (long long)k, (long long)n, need,
+                         (size_t)RNN_IGEMM_NOALLOC_MAX_BYTES);
+    void *ws = nullptr;
+    RNN_TRY(scratch_address(&ws, name));
+    return igemm_on_workspace(a, b, c, m, k, n, ws, st, name);
 }

@@ -60,6 +60,7 @@ SIGNATURES = {
     "rnn_int8_linear_forward": ([_P, _I64, _I64, _P, _P, _I64, _P, _P, _P], _INT),
     "rnn_igemm_workspace_size": ([_I64, _I64, _I64], ctypes.c_size_t),
     "rnn_igemm": ([_P, _P, _P, _I64, _I64, _I64, _P, ctypes.c_size_t, _P], _INT),
+    "rnn_igemm_noalloc": ([_P, _P, _P, _I64, _I64, _I64, _P], _INT),
     "rnn_w8a8_linear": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _UINT, _P, _P, _P], _INT),
     "rnn_ternary_pack": ([_P, _I64, _P, _P], _INT),
     "rnn_ternary_unpack": ([_P, _I64, _P, _P], _INT),
@@ -245,6 +246,21 @@ def igemm(a_u8, b_i8, m, k, n, workspace=None, c=None, stream=None):
     wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _check(load().rnn_igemm(_ptr(a_u8), _ptr(b_i8), _ptr(c), m, k, n, _ptr(workspace), wsb,
                             _stream(stream)))
+    return c
+
+
+IGEMM_NOALLOC_MAX_BYTES = 64 << 20  # RNN_IGEMM_NOALLOC_MAX_BYTES
+
+
+def igemm_noalloc(a_u8, b_i8, m, k, n, c, stream=None):
+    """igemm into a caller-allocated c (int32 [m, n]) with the library's
+    device-array workspace: no allocation anywhere in the call."""
+    import torch
+    _dev(a_u8, torch.uint8, "a"), _dev(b_i8, torch.int8, "b")
+    if min(m, k, n) < 0:
+        raise RnnError(RNN_ERR_INVALID_ARG, f"negative size m={m} k={k} n={n}")
+    _need(a_u8, m * k, "a"), _need(b_i8, k * n, "b"), _out(c, torch.int32, m * n, "c")
+    _check(load().rnn_igemm_noalloc(_ptr(a_u8), _ptr(b_i8), _ptr(c), m, k, n, _stream(stream)))
     return c
 
 
