@@ -3,19 +3,25 @@
 Headline line (value): W8A8 prefill GEMM, M=2048 K=4096 N=14336, int8 x int8 ->
 int32 -> fp32 per-channel/per-row dequant epilogue, inputs resident in HBM, in
 TOPS (2*M*N*K int ops per step). The same JSON line carries the roofline of that
-kernel, the CPU baseline (the oracle's AVX-512 VNNI igemm path over the whole
-workload) and the other configurations as `components`: decode GEMV (GB/s, weight
-buffers rotated past the 256 MB MALL), ternary GEMM (TOPS; both timed by HIP-graph
-replay), the RotorQuant K+V round trip (GB/s) and the f32 BlasBackend GEMM
-(TFLOP/s, beside torch.matmul's library GEMM on the same operands).
+kernel (with the HBM traffic and MFMA-busy / clock counters of its committed
+rocprofv3 passes), the CPU baseline (the oracle's AVX-512 VNNI igemm path over
+the whole workload) and the other configurations as `components`, each with its
+own CPU baseline where the reference has a CPU path: decode GEMV (GB/s, weight
+buffers rotated past the 256 MB MALL, beside a same-bytes read-only floor timed
+the same way), the 784-256-128-10 int8 MLP (end-to-end us), ternary GEMM (TOPS),
+the RotorQuant K+V round trip (GB/s), attention over the RotorQuant KV cache,
+the QuantizedLinear GEMV, igemm at the reference's published 512^3 shape, the f32
+BlasBackend GEMM and the copy ceiling.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import platform
 import statistics
 import sys
 import time
@@ -30,10 +36,26 @@ PEAK_INT8_TOPS = 5033.0   # MI355X dense int8 MFMA (datasheet, no sparsity)
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters.json")
+PROBE_LIB = os.path.join(ROOT, "rust-neural-network_amd", "librnn_probe.so")
+# From idle the GPU needs ~10 ms of load to raise its clocks; every timed
+# figure below is taken after this long of untimed launches of its own kernel.
+SETTLE_S = 0.25
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def settle(fn, seconds=SETTLE_S):
+    """Untimed launches of fn() for `seconds`, so the clocks have settled for
+    this kernel before it is timed."""
+    import torch
+    t_end = time.time() + seconds
+    while time.time() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
 
 
 def timed(fn, steps, warmup):
@@ -62,13 +84,96 @@ def gen_f32(shape, seed, dev, scale=1.0):
     return x * scale if scale != 1.0 else x
 
 
-def traffic_for(name):
+def _profile_entry(path, name):
     try:
-        with open(TRAFFIC_FILE) as f:
-            t = json.load(f).get(name)
-        return None if t is None else t.get("bytes_per_launch")
+        with open(path) as f:
+            return json.load(f).get(name)
     except (OSError, ValueError):
         return None
+
+
+def traffic_for(name):
+    t = _profile_entry(TRAFFIC_FILE, name)
+    return None if t is None else t.get("bytes_per_launch")
+
+
+def counters_for(name):
+    """MFMA-busy fraction and effective clock of a kernel from its committed
+    rocprofv3 counter pass (profiles/counters.json), or None."""
+    c = _profile_entry(COUNTERS_FILE, name)
+    if c is None:
+        return None
+    return {k: c[k] for k in ("mfma_busy", "clock_ghz", "lds_bank_conflict_cycles", "source")
+            if k in c}
+
+
+# ---------------------------------------------------------------- CPU side
+def cpu_threads():
+    """Worker threads for the reference's rayon-parallel igemm: one per logical
+    core this process may run on, capped by OMP_NUM_THREADS where the host sets
+    it (the GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = None
+    return {"model": model, "nproc": os.cpu_count(), "affinity": aff,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_time(fn, max_repeats=5, budget_s=4.0):
+    """Median wall time of fn() over up to `max_repeats` runs (at least one),
+    stopping once `budget_s` seconds are spent."""
+    times = []
+    start = time.perf_counter()
+    while len(times) < max_repeats and (not times or time.perf_counter() - start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_w8a8(O, aq, sa, wq, sw, threads, bias=None, relu=False):
+    """The reference CPU path of one W8A8 layer: igemm (src/int8.rs:285-314:
+    AVX-512 VNNI when the host has it, B repacked on every call, 4-row blocks
+    over threads) on a_u8 = a_s8 + 128 and B = W^T, then the zero-point
+    correction and the per-row/per-channel dequant epilogue."""
+    import numpy as np
+    m, k = aq.shape
+    n = wq.shape[0]
+    b_kn = np.ascontiguousarray(wq.T)
+    colsum128 = 128 * b_kn.astype(np.int64).sum(axis=0).astype(np.int32)
+
+    def run():
+        a_u8 = aq.view(np.uint8) ^ np.uint8(0x80)
+        c, vnni = O.igemm(a_u8, b_kn, m, k, n, threads)
+        acc = (c - colsum128).astype(np.int32)
+        y = (acc.astype(np.float32) * sa[:, None]) * sw[None, :]
+        if bias is not None:
+            y = y + bias[None, :]
+        if relu:
+            y = np.maximum(y, np.float32(0.0))
+        return y, vnni
+    return run
 
 
 # ---------------------------------------------------------------- prefill
@@ -83,6 +188,7 @@ def bench_prefill(H, W, dev, steps, warmup):
     aq, sa = H.quant_rows_i8(x)
     y = torch.empty((m, n), dtype=torch.float32, device=dev)
     fn = lambda: H.w8a8_linear(aq, sa, wq, sw, y=y)  # noqa: E731
+    settle(fn)
     ms = timed(fn, steps, warmup)
     ops = 2.0 * m * n * k
     tops = ops / (ms * 1e-3) / 1e12
@@ -90,7 +196,30 @@ def bench_prefill(H, W, dev, steps, warmup):
     return ms, tops, state
 
 
-# ---------------------------------------------------------------- GEMV
+def cpu_baseline(state, budget_s=20.0):
+    """The reference CPU path for the whole prefill workload (all 2048 rows),
+    see cpu_w8a8."""
+    import numpy as np
+
+    import oracle as O
+    m, k, n = state["m"], state["k"], state["n"]
+    aq, sa = state["aq"].cpu().numpy(), state["sa"].cpu().numpy()
+    wq, sw = state["wq"].cpu().numpy(), state["sw"].cpu().numpy()
+    threads = cpu_threads()
+    run = cpu_w8a8(O, aq, sa, wq, sw, threads)
+    y, vnni = run()
+    t, reps = cpu_time(run, 5, budget_s)
+    ops = 2.0 * m * n * k
+    return {"value": round(ops / t / 1e12, 4), "unit": "TOPS", "cores": threads,
+            "kind": "port",
+            "sample": f"the full W8A8 prefill workload {m}x{k}x{n} (no subsampling): oracle igemm "
+                      f"({'AVX-512 VNNI' if vnni else 'scalar'}, B repacked per call as "
+                      f"src/int8.rs:296 does, 4-row blocks over {threads} threads) + zero-point + "
+                      f"dequant epilogue, median of {reps} runs, {t:.3f} s per run",
+            "cpu": cpu_info(), "y_checksum": float(np.float64(y).sum())}
+
+
+# ---------------------------------------------------------------- graph timing
 def graph_timed(launch, n_launch, replays=5, settle_s=0.1):
     """Average ms per launch of `launch(i)` for i in range(n_launch), captured
     once into a HIP graph and replayed (events on the replay stream), so the
@@ -126,9 +255,46 @@ def graph_timed(launch, n_launch, replays=5, settle_s=0.1):
     return e0.elapsed_time(e1) / (replays * n_launch)
 
 
-def bench_gemv(H, W, dev, steps):
+class ReadFloor:
+    """The same-bytes read-only floor: librnn_probe.so's streaming read of a
+    buffer (16-byte non-temporal loads, 4 to 32 in flight per lane; the fastest
+    of those four variants is the floor), launched and timed exactly as the
+    kernel it is set beside."""
+
+    def __init__(self, dev):
+        import torch
+        self.lib = ctypes.CDLL(PROBE_LIB)
+        self.lib.rnn_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint32,
+                                            ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        self.sink = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def read(self, t, nbytes, per_lane):
+        import torch
+        nbytes = nbytes // 16 * 16
+        rc = self.lib.rnn_probe_read(ctypes.c_void_p(t.data_ptr()), nbytes, 0x9E3779B9,
+                                     ctypes.c_void_p(self.sink.data_ptr()), per_lane,
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError("rnn_probe_read failed")
+
+
+def _floor(floor, bufs, nbytes, n_launch):
+    if floor is None:
+        return None
+    copies = len(bufs)
+    return min(graph_timed(lambda i: floor.read(bufs[i % copies], nbytes, per), n_launch,
+                           replays=3, settle_s=0.03)
+               for per in (4, 8, 16, 32))
+
+
+# ---------------------------------------------------------------- GEMV
+def bench_gemv(H, W, dev, steps, floor, with_cpu):
+    import numpy as np
     import torch
+
+    import oracle as O
     out = {}
+    threads = cpu_threads()
     for (m, k, n) in W.GEMV_SHAPES:
         wbytes = k * n
         copies = max(2, -(-640 * 2**20 // wbytes))  # > 2.5x the 256 MB MALL
@@ -148,10 +314,25 @@ def bench_gemv(H, W, dev, steps):
                          n_launch)
         nbytes = k * n + 4 * n + m * k + 4 * m + 4 * m * n
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out[f"m{m}_k{k}_n{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
-                                  "weight_copies": copies, "launches_timed": n_launch,
-                                  "timing": "HIP graph replay, events / launches"}
+        ent = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+               "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+               "weight_copies": copies, "launches_timed": 5 * n_launch,
+               "timing": "HIP graph replay, events / launches"}
+        fl = _floor(floor, ws, k * n, n_launch)
+        if fl is not None:
+            ent["read_floor_us"] = round(fl * 1e3, 3)
+            ent["frac_of_read_floor"] = round(fl / ms, 4)
+        if with_cpu:
+            run = cpu_w8a8(O, aq.cpu().numpy(), sa.cpu().numpy(), ws[0].cpu().numpy(),
+                           sws[0].cpu().numpy(), threads)
+            t, reps = cpu_time(run, 3, 2.0)
+            ent["cpu_baseline"] = {
+                "us": round(t * 1e6, 1), "GB/s": round(nbytes / t / 1e9, 2),
+                "cores": min(threads, -(-m // 4)), "kind": "port",
+                "sample": f"oracle igemm (src/int8.rs:285-314, B repacked per call, {-(-m // 4)} "
+                          f"4-row block(s) over {threads} threads) + epilogue, full shape, median "
+                          f"of {reps}"}
+        out[f"m{m}_k{k}_n{n}"] = ent
         del ws, sws
         torch.cuda.empty_cache()
     return out
@@ -164,12 +345,14 @@ QT_FORMATS = [("INT4_g128", 3, 128), ("GGUF_Q4_0", 6, 32), ("GGUF_Q8_0", 8, 32),
               ("NF4_g64", 4, 64)]
 
 
-def bench_qt_gemv(H, dev, steps):
+def bench_qt_gemv(H, dev, steps, floor):
     """QuantizedLinear::forward (src/quantize.rs:744-754) at decode shapes:
     the fused GEMV that decodes INT4/GGUF/BF16/NF4 weights in registers (the
     VALU GEMV for m <= 4, the f32-MFMA GEMV for m >= 5, as AUTO picks). Bytes per
     launch = weight codes + f32 scales + x (4 m k) + y (4 m n); weights
-    rotate over copies past the MALL as for the W8A8 GEMV."""
+    rotate over copies past the MALL as for the W8A8 GEMV. For m >= 5 the
+    binding roof can be the f32 MFMA rate (2*16*k*n flops with rows padded to
+    16), so that fraction is given beside the HBM one."""
     import torch
     out = {}
     for name, fmt, gs in QT_FORMATS:
@@ -192,19 +375,78 @@ def bench_qt_gemv(H, dev, steps):
                                                            g, n, y=y), n_launch)
             nbytes = wbytes + 4 * m * k + 4 * m * n
             gbs = nbytes / (ms * 1e-3) / 1e9
-            out[f"{name}_m{m}_k{k}_n{n}"] = {
-                "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
-                "weight_copies": copies, "launches_timed": n_launch,
-                "timing": "HIP graph replay, events / launches"}
+            ent = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+                   "weight_copies": copies, "launches_timed": 5 * n_launch,
+                   "timing": "HIP graph replay, events / launches"}
+            if m >= 5:
+                tf = 2.0 * 16 * k * n / (ms * 1e-3) / 1e12
+                ent["TFLOP/s_f32_mfma"] = round(tf, 2)
+                ent["frac_fp32_mfma_peak"] = round(tf / PEAK_FP32_MFMA_TFLOPS, 4)
+            fl = _floor(floor, ds, nb, n_launch)
+            if fl is not None:
+                ent["read_floor_us"] = round(fl * 1e3, 3)
+                ent["frac_of_read_floor"] = round(fl / ms, 4)
+            out[f"{name}_m{m}_k{k}_n{n}"] = ent
             del ds, ss
             torch.cuda.empty_cache()
     return out
 
 
-# ---------------------------------------------------------------- ternary
-def bench_ternary(H, W, dev, steps):
+# ---------------------------------------------------------------- MLP
+def bench_mlp(H, W, dev, steps, with_cpu):
+    """the 784-256-128-10 int8 MLP, batch 32, W8A8 per layer
+    (activations quantized per row, int32 accumulate, fp32 dequant + bias, ReLU
+    fused between layers): six launches end to end. Timed by HIP-graph replay
+    of the whole forward (device latency) and as plain calls from Python (with
+    the binding's per-call host cost)."""
+    import numpy as np
     import torch
+
+    import layers as L
+    import oracle as O
+    params = []
+    for i, (fi, fo) in enumerate(zip(W.MLP_LAYERS[:-1], W.MLP_LAYERS[1:])):
+        params += [W.weights(fo, fi, seed=10 + i), W.weights(1, fo, seed=20 + i)[0]]
+    model = L.Int8Model.from_model([torch.from_numpy(p).to(dev) for p in params])
+    x_np = W.activations(W.MLP_BATCH, W.MLP_LAYERS[0], seed=1)
+    x = torch.from_numpy(x_np).to(dev)
+    ms_graph = graph_timed(lambda i: model.forward(x), max(steps, 100))
+    settle(lambda: model.forward(x), 0.05)
+    ms_eager = timed(lambda: model.forward(x), max(steps, 100), 20)
+    y = model.forward(x).cpu().numpy()
+    ops = 2.0 * W.MLP_BATCH * sum(a * b for a, b in zip(W.MLP_LAYERS[:-1], W.MLP_LAYERS[1:]))
+    ent = {"us_graph": round(ms_graph * 1e3, 2), "us_eager": round(ms_eager * 1e3, 2),
+           "ops": ops, "launches": 6, "batch": W.MLP_BATCH, "layers": list(W.MLP_LAYERS),
+           "timing": "us_graph: HIP graph replay of the whole forward; us_eager: Python calls, "
+                     "events over back-to-back forwards"}
+    if with_cpu:
+        threads = cpu_threads()
+        qw = [O.quant_rows_i8(params[2 * i]) for i in range(3)]
+
+        def run():
+            h = x_np
+            for i in range(3):
+                aq, sa = O.quant_rows_i8(h)
+                h, _ = cpu_w8a8(O, aq, sa, qw[i][0], qw[i][1], threads, params[2 * i + 1],
+                                i < 2)()
+            return h
+        h = run()
+        ent["max_abs_diff_vs_cpu"] = float(np.abs(h - y).max())
+        t, reps = cpu_time(run, 20, 1.0)
+        ent["cpu_baseline"] = {"us": round(t * 1e6, 1), "cores": threads, "kind": "port",
+                               "sample": f"the whole forward on the oracle: per layer per-row "
+                                         f"quantization + igemm (src/int8.rs:285-314) + "
+                                         f"epilogue, median of {reps}"}
+    return ent
+
+
+# ---------------------------------------------------------------- ternary
+def bench_ternary(H, W, dev, steps, with_cpu):
+    import numpy as np
+    import torch
+
+    import oracle as O
     c = W.TERNARY
     m, k, n = c["m"], c["k"], c["n"]
     packed, scales = H.ternary_quantize(gen_f32((n, k), 3, dev), H.TERNARY_ABSMEAN)
@@ -217,14 +459,35 @@ def bench_ternary(H, W, dev, steps):
     ops = 2.0 * m * n * k
     tops = ops / (ms * 1e-3) / 1e12
     nbytes = n * k // 4 + 4 * n + m * k + 4 * m + 4 * m * n
-    return {"us": round(ms * 1e3, 3), "TOPS": round(tops, 1),
-            "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4), "ops": ops, "bytes": nbytes,
-            "launches_timed": 5 * n_launch, "timing": "HIP graph replay, events / launches"}
+    ent = {"us": round(ms * 1e3, 3), "TOPS": round(tops, 1),
+           "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4), "ops": ops, "bytes": nbytes,
+           "launches_timed": 5 * n_launch, "timing": "HIP graph replay, events / launches",
+           "traffic": traffic_for("ternary_gemm"), "counters": counters_for("ternary_gemm")}
+    if with_cpu:
+        rows = 8
+        x = gen_f32((rows, k), 5, dev).cpu().numpy()
+        p_np = packed.cpu().numpy().view(np.uint32)
+        s_np = scales.cpu().numpy()
+        t, reps = cpu_time(lambda: O.ternary_linear_f32(x, p_np, s_np, n), 3, 4.0)
+        full = t * m / rows
+        ent["cpu_baseline"] = {
+            "us": round(full * 1e6, 1), "TOPS": round(ops / full / 1e12, 5), "cores": 1,
+            "kind": "port",
+            "sample": f"TernaryLinear::forward (src/ternary.rs:239-279, serial f32 shift-and-add as "
+                      f"the reference runs it) on {rows} of the {m} rows, scaled x{m // rows}; "
+                      f"{t:.3f} s per sample, median of {reps}"}
+    return ent
 
 
 # ---------------------------------------------------------------- RotorQuant
-def bench_rotorquant(H, W, dev, steps):
+def bench_rotorquant(H, W, dev, steps, with_cpu):
+    """RotorQuant K+V [8,32,4096,128] f32, 4-bit, fused quantize + dequantize:
+    one launch per tensor, timed by HIP-graph replay after the same clock
+    settle as the other HBM-bound components. Bytes = one f32 read + one f32
+    write per element."""
     import torch
+
+    import oracle as O
     c = W.ROTORQUANT
     shape = (c["batch"], c["heads"], c["seq"], c["head_dim"])
     dim, bits = c["head_dim"], c["bits"]
@@ -237,26 +500,42 @@ def bench_rotorquant(H, W, dev, steps):
         kv.append(x)
         outs.append(torch.empty_like(x))
         rots.append(torch.from_numpy(W.rotors(ng, seed)).to(dev))
-
-    def step():
-        for x, y, r in zip(kv, outs, rots):
-            H.rotorquant_quantize(x, r, bits, y=y)
-
-    ms = timed(step, max(steps // 2, 10), 3)
+    n_launch = 2 * max(10, steps // 2)
+    ms = graph_timed(lambda i: H.rotorquant_quantize(kv[i % 2], rots[i % 2], bits, y=outs[i % 2]),
+                     n_launch, replays=3, settle_s=0.2)
     nbytes = sum(2 * x.numel() * 4 for x in kv)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_step": nbytes,
-            "launches_per_step": 2}
+    us_step = 2 * ms * 1e3
+    gbs = nbytes / (us_step * 1e-6) / 1e9
+    ent = {"us_per_step": round(us_step, 2), "GB/s": round(gbs, 1),
+           "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_step": nbytes,
+           "launches_per_step": 2, "launches_timed": 3 * n_launch,
+           "timing": "HIP graph replay after a 0.2 s settle, events / launches",
+           "traffic": traffic_for("rotorquant_kv")}
+    if with_cpu:
+        rows = 16384
+        xs = [kv[i].reshape(-1, dim)[:rows].cpu().numpy() for i in range(2)]
+        rs = [r.cpu().numpy() for r in rots]
+        t, reps = cpu_time(lambda: [O.rotorquant_quantize(xs[i], rs[i], bits) for i in range(2)],
+                           3, 3.0)
+        total_rows = 2 * kv[0].numel() // dim
+        full = t * total_rows / (2 * rows)
+        ent["cpu_baseline"] = {
+            "us_per_step": round(full * 1e6, 1), "GB/s": round(nbytes / full / 1e9, 3), "cores": 1,
+            "kind": "port",
+            "sample": f"RotorQuant::quantize (src/quant.rs:212-239, serial as the reference runs "
+                      f"it) on {rows} rows of K and of V, scaled x{total_rows // (2 * rows)}; "
+                      f"{t:.3f} s per sample, median of {reps}"}
+    return ent
 
 
 def bench_rq_attention(H, W, dev, steps):
     """Decode attention over the RotorQuant KV cache (the RotorQuant config's
     K and V, [8, 32, 4096, 128], 4-bit, as pages): one query per (batch,
-    head). Bytes per launch = both pages (6 bytes per position and group) +
-    q + out. Beside it, torch's f32 scaled_dot_product_attention over the
-    reconstructed K and V (what a cache without the codes would read), timed
-    the same way, for context."""
+    head). Algorithmic bytes per position = 6 per group (a 4-bit code triple in
+    a u16 and an f32 scale) for K and for V; the K page pads codes to 8 groups
+    and scales to 4, so the bytes it reads are given beside. Beside it, torch's
+    f32 scaled_dot_product_attention over the reconstructed K and V (what a
+    cache without the codes would read), timed the same way, for context."""
     import torch
     c = W.ROTORQUANT
     b, h, seq, dim, bits = c["batch"], c["heads"], c["seq"], c["head_dim"], c["bits"]
@@ -279,22 +558,60 @@ def bench_rq_attention(H, W, dev, steps):
     def step():
         H.rotorquant_kv_attention(q, pages[0], pages[1], rots[0], rots[1], seq, scale, out=out)
 
+    settle(step, 0.1)
     ms = timed(step, max(steps // 2, 20), 10)
-    # bytes the kernel reads: K pages pad each position to 8 groups of codes
-    # and 4 of scales, V pages hold exactly ng of each
-    npos = bh * -(-seq // 64) * 64
-    nbytes = npos * (2 * 8 * -(-ng // 8) + 4 * 4 * -(-ng // 4)) + npos * 6 * ng + 2 * q.numel() * 4
+    npos = bh * seq
+    nbytes = 2 * npos * 6 * ng + 2 * q.numel() * 4
+    npos_t = bh * -(-seq // 64) * 64
+    read = npos_t * (2 * 8 * -(-ng // 8) + 4 * 4 * -(-ng // 4)) + npos_t * 6 * ng + 2 * q.numel() * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
     qf = q.view(b, h, 1, dim)
-    ms_f32 = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
-        qf, recon[0], recon[1], scale=scale), max(steps // 2, 20), 10)
+    sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(  # noqa: E731
+        qf, recon[0], recon[1], scale=scale)
+    settle(sdpa, 0.1)
+    ms_f32 = timed(sdpa, max(steps // 2, 20), 10)
     del recon
     torch.cuda.empty_cache()
     return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-            "bytes": nbytes, "kernel": "rq_kv_attn_kernel (scores and V in the rotated domain)",
+            "bytes": nbytes, "bytes_read_with_padding": read,
+            "kernel": "rq_kv_attn_kernel (scores and V in the rotated domain)",
             "f32_kv_sdpa_us": round(ms_f32 * 1e3, 2),
             "f32_kv_bytes": 2 * bh * seq * dim * 4,
             "shape": {"batch": b, "heads": h, "seq": seq, "head_dim": dim, "bits": bits, "nq": 1}}
+
+
+# ---------------------------------------------------------------- igemm 512^3
+def bench_igemm_512(H, dev, steps, with_cpu):
+    """The reference's only published hot-path number: igemm (u8 x i8 [K,N] ->
+    i32) at 512x512x512 in 1.96 ms on an AVX-512 VNNI CPU (README.md:657-659,
+    harness benches/core_ops.rs:123-160, inputs (i%251) as u8 and (i%255) as
+    i8). rnn_igemm on the same inputs: pack A, transpose B, column sums and the
+    MFMA GEMM, four launches, with a caller workspace; timed by graph replay."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+    m = k = n = 512
+    a_np = (np.arange(m * k) % 251).astype(np.uint8).reshape(m, k)
+    b_np = (np.arange(k * n) % 255).astype(np.int8).reshape(k, n)   # (i % 255) as i8 wraps
+    a, b = torch.from_numpy(a_np).to(dev), torch.from_numpy(b_np).to(dev)
+    ws = torch.empty(H.igemm_workspace_size(m, k, n), dtype=torch.uint8, device=dev)
+    c = torch.empty((m, n), dtype=torch.int32, device=dev)
+    ms = graph_timed(lambda i: H.igemm(a, b, m, k, n, workspace=ws, c=c), max(steps, 100))
+    ops = 2.0 * m * n * k
+    ent = {"us": round(ms * 1e3, 3), "TOPS": round(ops / (ms * 1e-3) / 1e12, 2),
+           "reference_published_ms": 1.96, "speedup_vs_published": round(1.96 / ms, 1),
+           "launches": 4, "timing": "HIP graph replay, events / calls"}
+    if with_cpu:
+        threads = cpu_threads()
+        ref = O.igemm_scalar(a_np, b_np, m, k, n)
+        ent["bit_exact_vs_scalar"] = bool(np.array_equal(c.cpu().numpy(), ref))
+        t, reps = cpu_time(lambda: O.igemm(a_np, b_np, m, k, n, threads), 5, 2.0)
+        ent["cpu_baseline"] = {"us": round(t * 1e6, 1), "cores": threads, "kind": "port",
+                               "sample": f"oracle igemm (AVX-512 VNNI restatement of "
+                                         f"src/int8.rs:285-314) on the same inputs, median of "
+                                         f"{reps}"}
+    return ent
 
 
 # ---------------------------------------------------------------- f32 GEMM
@@ -311,7 +628,9 @@ def bench_sgemm(H, dev, steps):
     b = gen_f32((k, n), 22, dev)
     c = torch.empty((m, n), dtype=torch.float32, device=dev)
     n_iter = max(steps // 4, 20)
-    ms = timed(lambda: H.sgemm(H.NO_TRANS, H.NO_TRANS, m, n, k, 1.0, a, k, b, n, 0.0, c, n), n_iter, 10)
+    fn = lambda: H.sgemm(H.NO_TRANS, H.NO_TRANS, m, n, k, 1.0, a, k, b, n, 0.0, c, n)  # noqa: E731
+    settle(fn, 0.1)
+    ms = timed(fn, n_iter, 10)
     tf32 = torch.backends.cuda.matmul.allow_tf32
     torch.backends.cuda.matmul.allow_tf32 = False
     try:
@@ -338,62 +657,59 @@ def bench_copy(dev, steps):
     import torch
     src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
-    ms = timed(lambda: dst.copy_(src), max(steps, 20), 5)
+    fn = lambda: dst.copy_(src)  # noqa: E731
+    settle(fn, 0.1)
+    ms = timed(fn, max(steps, 20), 5)
     gbs = 2 * COPY_BYTES / (ms * 1e-3) / 1e9
     return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_launch": 2 * COPY_BYTES}
 
 
-# ---------------------------------------------------------------- CPU baseline
-def cpu_baseline(state, max_repeats=5, budget_s=20.0):
-    """The reference CPU path for the whole prefill workload (all 2048 rows):
-    igemm (src/int8.rs:285-314: AVX-512 VNNI when the host has it, B repacked
-    on every call, 4-row blocks over threads) on a_u8 = a_s8 + 128 and
-    B = W^T, then the zero-point correction and the per-row/per-channel
-    dequant epilogue. Median of up to `max_repeats` runs, stopping once
-    `budget_s` seconds of wall time are spent."""
-    import numpy as np
+# ---------------------------------------------------------------- clock probe
+def bench_clock_probe(dev):
+    """The shader clock under a plain int8 MFMA load: librnn_probe.so's
+    mfma_clock_kernel (constant operands, one wave per SIMD on every CU) reads
+    the shader-clock and 100 MHz real-time counters at the start and end of
+    each block. It pins what "clock" means for the counter-derived figures
+    (SQ_BUSY_CYCLES per shader engine over the launch) of the GEMM profiles,
+    and gives the int8 MFMA rate the chip reaches with no memory traffic."""
+    import torch
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.rnn_probe_mfma_clock.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    blocks = torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = 20000
+    out = torch.zeros(4 * blocks, dtype=torch.int64, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    import oracle as O
-    m, k, n = state["m"], state["k"], state["n"]
-    aq = state["aq"].cpu().numpy()
-    sa = state["sa"].cpu().numpy()
-    wq = state["wq"].cpu().numpy()
-    sw = state["sw"].cpu().numpy()
-    b_kn = np.ascontiguousarray(wq.T)                   # weight layout prep, not timed
-    colsum128 = 128 * b_kn.astype(np.int64).sum(axis=0).astype(np.int32)
-    threads = max(1, min(16, os.cpu_count() or 1))
-    times = []
-    used_vnni = False
-    start = time.perf_counter()
-    while len(times) < max_repeats and (not times or time.perf_counter() - start < budget_s):
-        t0 = time.perf_counter()
-        a_u8 = (aq.view(np.uint8) ^ np.uint8(0x80))
-        c, used_vnni = O.igemm(a_u8, b_kn, m, k, n, threads)
-        acc = (c - colsum128).astype(np.int32)
-        y = (acc.astype(np.float32) * sa[:, None]) * sw[None, :]
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    ops = 2.0 * m * n * k
-    return {"value": round(ops / t / 1e12, 4), "unit": "TOPS", "cores": threads,
-            "kind": "port",
-            "sample": f"the full W8A8 prefill workload {m}x{k}x{n} (no subsampling): oracle igemm "
-                      f"({'AVX-512 VNNI' if used_vnni else 'scalar'}, B repacked per call as "
-                      f"src/int8.rs:296 does) + zero-point + dequant epilogue, {threads} threads, "
-                      f"median of {len(times)} runs, {t:.3f} s per run",
-            "y_checksum": float(np.float64(y).sum())}
+    def run():
+        if lib.rnn_probe_mfma_clock(blocks, iters, ctypes.c_void_p(out.data_ptr()),
+                                    ctypes.c_void_p(sink.data_ptr()), st) != 0:
+            raise RuntimeError("rnn_probe_mfma_clock failed")
+    settle(run, 0.2)
+    ms = timed(run, 5, 1)
+    o = out.cpu().numpy().reshape(blocks, 4).astype("float64")
+    ghz = sorted(((o[:, 1] - o[:, 0]) / (o[:, 3] - o[:, 2]) * 0.1).tolist())
+    ops = 2.0 * 16 * 16 * 64 * 8 * iters * 4 * blocks
+    return {"ghz_median": round(ghz[len(ghz) // 2], 3), "ghz_min": round(ghz[0], 3),
+            "ghz_max": round(ghz[-1], 3), "int8_TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+            "us": round(ms * 1e3, 1), "blocks": blocks,
+            "method": "s_memtime / s_memrealtime deltas per block (100 MHz real-time clock)"}
+
+
+COMPONENTS = ["gemv", "mlp", "ternary", "rotorquant", "rq_attention", "qt_gemv", "igemm512",
+              "sgemm", "copy", "clock"]
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # The warmup covers the clock ramp: from idle the first ~100 prefill
-    # launches run up to 25% slower while the GPU raises its clocks.
+    # Every timed figure follows a SETTLE_S clock settle of its own kernel;
+    # --warmup launches come after it and are untimed too.
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--only", default="all",
-                    choices=["all", "prefill", "gemv", "qt_gemv", "ternary", "rotorquant", "rq_attention",
-                             "sgemm", "copy"])
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", default="all", choices=["all", "prefill"] + COMPONENTS)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -410,6 +726,8 @@ def main():
     H.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    with_cpu = not args.no_cpu
+    floor = ReadFloor(dev) if os.path.exists(PROBE_LIB) else None
 
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
@@ -427,38 +745,49 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS,
                          "unit": "TFLOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
                          "traffic": traffic_for("w8a8_prefill_gemm"),
+                         "counters": counters_for("w8a8_prefill_gemm"),
                          "op_kind": "int8 MFMA ops, 2 per multiply-accumulate (T int-op/s)",
                          "ops_per_launch": ops,
                          "kernel": "gemm_pp_kernel<L128Cfg<256,224,4,2,0,1>> (ping-pong, v_mfma_i32_16x16x64_i8, 128-byte LDS rows)",
-                         "timing": "HIP events on the launch stream, average over the timed "
-                                   "launches"},
+                         "timing": f"HIP events on the launch stream, average over the timed "
+                                   f"launches; {SETTLE_S} s clock settle and {args.warmup} "
+                                   f"warmup launches before them"},
         })
-        if not args.no_cpu:
+        if with_cpu:
             log("cpu baseline: oracle igemm over the whole workload")
             result["cpu_baseline"] = cpu_baseline(state)
         del state
         torch.cuda.empty_cache()
     if args.only in ("all", "gemv"):
         log("decode GEMV: 6 shapes")
-        components["w8a8_decode_gemv"] = bench_gemv(H, W, dev, args.steps)
-    if args.only in ("all", "qt_gemv"):
-        log("QuantizedLinear GEMV: INT4/GGUF/BF16 weights, decode shapes")
-        components["quantized_linear_gemv"] = bench_qt_gemv(H, dev, args.steps)
+        components["w8a8_decode_gemv"] = bench_gemv(H, W, dev, args.steps, floor, with_cpu)
+    if args.only in ("all", "mlp"):
+        log("int8 MLP 784-256-128-10, batch 32")
+        components["int8_mlp_784_256_128_10"] = bench_mlp(H, W, dev, args.steps, with_cpu)
     if args.only in ("all", "ternary"):
         log("ternary GEMM 512x4096x4096")
-        components["ternary_gemm"] = bench_ternary(H, W, dev, args.steps)
+        components["ternary_gemm"] = bench_ternary(H, W, dev, args.steps, with_cpu)
     if args.only in ("all", "rotorquant"):
         log("RotorQuant K+V [8,32,4096,128] 4-bit round trip")
-        components["rotorquant_kv"] = bench_rotorquant(H, W, dev, args.steps)
+        components["rotorquant_kv"] = bench_rotorquant(H, W, dev, args.steps, with_cpu)
     if args.only in ("all", "rq_attention"):
         log("attention over the RotorQuant KV cache [8,32,4096,128], 4-bit, one query per head")
         components["rotorquant_kv_attention"] = bench_rq_attention(H, W, dev, args.steps)
+    if args.only in ("all", "qt_gemv"):
+        log("QuantizedLinear GEMV: INT4/GGUF/BF16 weights, decode shapes")
+        components["quantized_linear_gemv"] = bench_qt_gemv(H, dev, args.steps, floor)
+    if args.only in ("all", "igemm512"):
+        log("igemm 512x512x512 (the reference's published shape)")
+        components["igemm_512"] = bench_igemm_512(H, dev, args.steps, with_cpu)
     if args.only in ("all", "sgemm"):
         log("f32 GEMM 4096x4096x4096 (BlasBackend::sgemm)")
         components["f32_sgemm"] = bench_sgemm(H, dev, args.steps)
     if args.only in ("all", "copy"):
         log("streaming copy ceiling: 512 MiB device-to-device")
         components["copy_ceiling"] = bench_copy(dev, args.steps)
+    if args.only in ("all", "clock") and os.path.exists(PROBE_LIB):
+        log("MFMA clock probe")
+        components["mfma_clock_probe"] = bench_clock_probe(dev)
     if components:
         result["components"] = components
     if "value" not in result:  # a single non-headline component was requested

@@ -1,0 +1,118 @@
+// read_floor.hip -- measurement helper for bench.py, not part of the C ABI of
+// include/rnn_hip.h: a streaming read of a device buffer at the best rate a
+// plain kernel reaches (16-byte non-temporal loads, 4 in flight per lane,
+// grid sized to keep every CU busy), so the decode GEMV and QuantizedLinear
+// GEMV can be set beside a same-bytes, read-only floor timed the same way.
+// Built into librnn_probe.so.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBlock = 256;
+
+// Block b reads the PER * 4 KiB slab [b * PER * 4096, (b+1) * PER * 4096): each
+// load instruction of the block covers 4 KiB contiguous (16 bytes per lane),
+// and a lane issues all PER of its loads before using any, so a block keeps
+// PER * 4 KiB in flight -- the access pattern of a one-shot weight stream.
+// The XOR of every 16-byte chunk is formed per block; the sink is written only
+// when it equals `magic`, which keeps the loads alive without a store per block.
+template <int PER>
+__global__ __launch_bounds__(kBlock) void read_floor_kernel(const u32x4 *__restrict__ p, int64_t n16,
+                                                           uint32_t magic, uint32_t *sink) {
+    const int64_t base = (int64_t)blockIdx.x * PER * kBlock + threadIdx.x;
+    u32x4 v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int64_t i = base + u * kBlock;
+        v[u] = __builtin_nontemporal_load(p + (i < n16 ? i : n16 - 1));
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+        if (base + u * kBlock < n16) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int off = 32; off > 0; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
+    __shared__ uint32_t red[kBlock / 64];
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t b = 0;
+        for (int w = 0; w < kBlock / 64; ++w) b ^= red[w];
+        if (b == magic) atomicXor(sink, b);
+    }
+}
+
+template <int PER>
+void launch(const void *p, int64_t n16, uint32_t magic, uint32_t *sink, hipStream_t st) {
+    const int64_t g = (n16 + PER * kBlock - 1) / (PER * kBlock);
+    read_floor_kernel<PER><<<(unsigned)g, kBlock, 0, st>>>(reinterpret_cast<const u32x4 *>(p), n16,
+                                                          magic, sink);
+}
+
+}  // namespace
+
+// Reads `bytes` (a multiple of 16, 16-byte aligned) from p with `per_lane`
+// (4, 8, 16 or 32) 16-byte loads in flight per lane. Each block XORs its
+// chunks; a block whose XOR equals `magic` XORs it into *sink. Returns 0, or 1
+// for bad arguments / a failed launch.
+extern "C" int rnn_probe_read(const void *p, int64_t bytes, uint32_t magic, uint32_t *sink,
+                              int per_lane, void *stream) {
+    if (bytes < 0 || bytes % 16 != 0 || ((uintptr_t)p & 15) != 0 || sink == nullptr) return 1;
+    if (bytes == 0) return 0;
+    const int64_t n16 = bytes / 16;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    switch (per_lane) {
+    case 4: launch<4>(p, n16, magic, sink, st); break;
+    case 8: launch<8>(p, n16, magic, sink, st); break;
+    case 16: launch<16>(p, n16, magic, sink, st); break;
+    case 32: launch<32>(p, n16, magic, sink, st); break;
+    default: return 1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// ---------------------------------------------------------------- clock probe
+// A fixed amount of int8 MFMA work on constant operands, one wave per SIMD on
+// every CU, with the shader-clock counter (s_memtime) and the 100 MHz
+// real-time counter (s_memrealtime) read at the start and end of each block:
+// out[4*b .. 4*b+3] = {clk0, clk1, rt0, rt1}. The ratio of the two deltas is
+// the shader clock while the block ran, an independent check of clock figures
+// derived from rocprofv3 counters (SQ_BUSY_CYCLES) over the same launch.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void mfma_clock_kernel(int iters, uint64_t *out, int *sink) {
+    const uint64_t clk0 = __builtin_amdgcn_s_memtime();
+    const uint64_t rt0 = __builtin_amdgcn_s_memrealtime();
+    i32x4 a = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    i32x4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = i32x4{0, 0, 0, 0};
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, a, acc[j], 0, 0, 0);
+    }
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += acc[j].x;
+    __syncthreads();
+    const uint64_t clk1 = __builtin_amdgcn_s_memtime();
+    const uint64_t rt1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        out[4 * blockIdx.x + 0] = clk0;
+        out[4 * blockIdx.x + 1] = clk1;
+        out[4 * blockIdx.x + 2] = rt0;
+        out[4 * blockIdx.x + 3] = rt1;
+    }
+    if (s == 0x7fffffff) sink[0] = s;
+}
+
+// `blocks` workgroups of 4 waves run `iters` x 8 MFMAs each; out holds
+// 4 * blocks u64. Returns 0, or 1 for bad arguments / a failed launch.
+extern "C" int rnn_probe_mfma_clock(int blocks, int iters, uint64_t *out, int *sink, void *stream) {
+    if (blocks <= 0 || iters <= 0 || out == nullptr || sink == nullptr) return 1;
+    mfma_clock_kernel<<<(unsigned)blocks, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(iters, out,
+                                                                                          sink);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}

@@ -57,7 +57,10 @@ class Linear(Module):
     def forward(self, x):
         in_f = x.shape[-1]
         lead = tuple(x.shape[:-1])
-        y = H.linear_layer(x.reshape(-1, in_f).contiguous(), self.weight, self.bias)
+        rows = 1
+        for d in lead:
+            rows *= d
+        y = H.linear_layer(x.reshape(rows, in_f).contiguous(), self.weight, self.bias)
         return y.reshape(*lead, self.weight.shape[0])
 
     def parameters(self):
