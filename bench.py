@@ -454,14 +454,22 @@ def bench_ternary(H, W, dev, steps, with_cpu):
     y = torch.empty((m, n), dtype=torch.float32, device=dev)
     # a launch (~13 us) is shorter than the Python binding's per-call host
     # cost, so launches are replayed from a HIP graph as for the GEMV
+    # the codes in the GEMM's own 2-bit layout (a one-time weight preparation)
+    packed_mfma = H.ternary_prepack(packed, n, k)
     n_launch = max(steps, 100)
-    ms = graph_timed(lambda i: H.ternary_gemm(aq, sa, packed, scales, n, y=y), n_launch)
+    ms = graph_timed(lambda i: H.ternary_gemm(aq, sa, packed_mfma, scales, n, y=y,
+                                              mfma_layout=True), n_launch)
+    ms_ref_layout = graph_timed(lambda i: H.ternary_gemm(aq, sa, packed, scales, n, y=y), n_launch)
     ops = 2.0 * m * n * k
     tops = ops / (ms * 1e-3) / 1e12
     nbytes = n * k // 4 + 4 * n + m * k + 4 * m + 4 * m * n
     ent = {"us": round(ms * 1e3, 3), "TOPS": round(tops, 1),
            "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4), "ops": ops, "bytes": nbytes,
            "launches_timed": 5 * n_launch, "timing": "HIP graph replay, events / launches",
+           "weights": "2-bit codes in the MFMA layout of rnn_ternary_prepack (decoded by byte "
+                      "permutes); us_reference_layout: the same GEMM on TernaryTensor::packed "
+                      "as the reference lays it out (decoded through an LDS table)",
+           "us_reference_layout": round(ms_ref_layout * 1e3, 3),
            "traffic": traffic_for("ternary_gemm"), "counters": counters_for("ternary_gemm")}
     if with_cpu:
         rows = 8

@@ -48,6 +48,7 @@ enum rnn_status {
 #define RNN_ALGO_TILED_DMA 0x30u    /* force the LDS-DMA pipelined big-tile GEMM (k % 128 == 0, n % 4 == 0) */
 #define RNN_ALGO_GEMV_MFMA 0x40u    /* rnn_qt_linear_forward: force the f32-MFMA GEMV (m <= 16) */
 #define RNN_ALGO_MASK 0xF0u
+#define RNN_FLAG_TERNARY_MFMA_LAYOUT 0x100u /* rnn_ternary_gemm: codes are in the layout of rnn_ternary_prepack */
 
 int rnn_abi_version(void);
 const char *rnn_last_error(void);
@@ -111,7 +112,10 @@ int rnn_igemm_noalloc(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m,
  *   acc[m,n] = sum_k aq[m,k]*wq[n,k]   (wrapping int32)
  *   y[m,n]   = ((float)acc * sa[m]) * sw[n] (+ bias[n]) (relu if flagged)
  * aq [m,k] int8 row quantized (rnn_quant_rows_i8), wq [n,k] int8 (the
- * Int8Weights layout, src/int8.rs:14-17), k must be a multiple of 16.
+ * Int8Weights layout, src/int8.rs:14-17). Any k and any operand alignment
+ * (the igemm contract, src/int8.rs:288-296): k % 16 != 0 or unaligned operands
+ * take a tiled kernel that assembles its chunks from byte loads (the forced
+ * GEMV and LDS-DMA algos need k % 16 == 0 and 16-byte alignment).
  * bias, y and acc_out may each be NULL (not both y and acc_out). */
 int rnn_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *wq,
                     const float *sw, const float *bias, int64_t m, int64_t k,
@@ -153,14 +157,28 @@ int rnn_ternary_linear_forward(const float *x, int64_t batch, int64_t in_f,
 
 /* Ternary GEMM on int8 MFMA (BASELINE ternary config): t[n,k] unpacked from
  * the 2-bit codes inside the kernel, acc = sum_k aq[m,k]*t[n,k], epilogue as
- * rnn_w8a8_linear with sw[n]. k must be a multiple of 16 (rows word aligned).
- * flags: RNN_FLAG_RELU and an algo (AUTO: the LDS-DMA kernel when k % 128 == 0,
- * n % 4 == 0 and buffers are 16-byte aligned, else TILED; TILED or TILED_DMA
- * force one). */
+ * rnn_w8a8_linear with sw[n].
+ * flags: RNN_FLAG_RELU, RNN_FLAG_TERNARY_MFMA_LAYOUT when `packed` comes
+ * from rnn_ternary_prepack (k % 16 == 0), and an algo (AUTO: the LDS-DMA
+ * kernel when k % 128 == 0, n % 4 == 0 and buffers are 16-byte aligned, else
+ * TILED; TILED or TILED_DMA force one). Any k is accepted in the reference
+ * layout: rows that start mid-word (k % 16 != 0) or unaligned activations take
+ * a tiled kernel that gathers codes from arbitrary bit offsets. */
 int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_t *packed,
                      const float *sw, const float *bias, int64_t m, int64_t k,
                      int64_t n, unsigned flags, float *y, int32_t *acc_out,
                      void *stream);
+
+/* The packed codes of a ternary weight [rows, cols] (TernaryTensor::packed,
+ * cols % 16 == 0 so that rows are whole words) rearranged for the GEMM: within
+ * each 32-bit word, the code of column k0 + 4r + b moves from bits 2(4r+b) to
+ * bits 8b + 2r. Same size (rows*cols/16 words), still 2 bits per weight;
+ * rnn_ternary_gemm with RNN_FLAG_TERNARY_MFMA_LAYOUT reads this layout and
+ * decodes it with byte permutes instead of a lookup table. A one-time weight
+ * preparation (like the reference's per-call pack_b_vnni, src/int8.rs:195-218,
+ * but done once); no counterpart in the reference. out may not alias packed. */
+int rnn_ternary_prepack(const uint32_t *packed, int64_t rows, int64_t cols,
+                        uint32_t *out, void *stream);
 
 /* ------------------------------------------------------- RotorQuant (a10-a12) */
 

@@ -108,6 +108,34 @@ __device__ __forceinline__ v4i ternary_word_to_i8x16(uint32_t w) {
     return r;
 }
 
+// The MFMA layout of packed ternary codes (rnn_ternary_prepack): within each
+// 32-bit word of 16 codes (k = k0 .. k0+15) the code of k0 + 4r + b sits at
+// bits 8b + 2r, so (w >> 2r) & 0x03030303 holds the codes of k0+4r .. k0+4r+3
+// one per byte, and one byte permute maps each code through a 4-entry table
+// (00 -> 0, 01 -> +1, 10 -> -1, 11 -> 0, src/ternary.rs:9-14, :63-75) held in
+// a constant: bytes {0x00, 0x01, 0xFF, 0x00}. Selector values 0-3 pick those
+// bytes, so 16 codes decode in 11 VALU operations with no LDS table.
+constexpr uint32_t kTerPermTable = 0x00FF0100u;
+__device__ __forceinline__ v4i ternary_perm_decode(uint32_t w) {
+    v4i r;
+    r.x = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, w & 0x03030303u);
+    r.y = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, (w >> 2) & 0x03030303u);
+    r.z = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, (w >> 4) & 0x03030303u);
+    r.w = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, (w >> 6) & 0x03030303u);
+    return r;
+}
+
+// Reference word (code t at bits 2t) -> MFMA-layout word (code 4r + b at bits
+// 8b + 2r): a fixed permutation of the 16 two-bit fields.
+__host__ __device__ __forceinline__ uint32_t ternary_word_to_mfma_layout(uint32_t w) {
+    uint32_t o = 0;
+    for (int t = 0; t < 16; ++t) {
+        const int r = t >> 2, b = t & 3;
+        o |= ((w >> (2 * t)) & 3u) << (8 * b + 2 * r);
+    }
+    return o;
+}
+
 // ------------------------------------------------------------ tiled GEMM
 // Block tile BM x BN, K step 64 (one MFMA K), (BM/WM) x (BN/WN) waves, each
 // wave a WM x WN tile of 16x16 MFMA blocks. Operand tiles live in LDS as
@@ -131,7 +159,42 @@ struct TileGemm {
     static_assert(TERNARY || BN * kBK / 16 % NT == 0, "B tile must split evenly");
 };
 
-template <int BM, int BN, int WM, int WN, bool TERNARY>
+// RAGGED: any K and any operand alignment (the igemm contract's "any K",
+// src/int8.rs:288-296). Every chunk is assembled from byte loads (k >= K reads
+// as 0), and ternary code words are gathered from arbitrary bit offsets of the
+// flat row-major codes (a row of K codes starts at code n*K, so rows are not
+// word aligned unless K % 16 == 0). Slower; used only for such shapes.
+__device__ __forceinline__ v4i load16_ragged(const int8_t *row, int64_t k0, int64_t K) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int64_t k = k0 + 4 * q + b;
+            v |= (k < K ? (uint32_t)(uint8_t)row[k] : 0u) << (8 * b);
+        }
+        w[q] = v;
+    }
+    return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
+// The 16 codes of row n at k0 .. k0+15 (codes past the row's K read as 0) as
+// one word in the packed layout (code t at bits 2t).
+__device__ __forceinline__ uint32_t ternary_word_ragged(const uint32_t *Bp, int64_t n, int64_t k0,
+                                                        int64_t N, int64_t K) {
+    const int64_t left = K - k0;
+    if (left <= 0) return 0u;
+    const int64_t c0 = n * K + k0, w0 = c0 >> 4, words = (N * K + 15) / 16;
+    const int sh = (int)(c0 & 15) * 2;
+    const uint32_t lo = Bp[w0];
+    const uint32_t hi = (sh != 0 && w0 + 1 < words) ? Bp[w0 + 1] : 0u;
+    uint32_t v = sh ? (lo >> sh) | (hi << (32 - sh)) : lo;
+    if (left < 16) v &= (1u << (2 * left)) - 1u;
+    return v;
+}
+
+template <int BM, int BN, int WM, int WN, bool TERNARY, bool RAGGED = false, bool PERM = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_tiled_kernel(
     const int8_t *__restrict__ A, const void *__restrict__ Bv, int64_t M, int64_t N, int64_t K,
     Epilogue epi) {
@@ -161,7 +224,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_tiled_kernel(
             const int r = c / 4, ch = c % 4;
             const int64_t gm = std::min<int64_t>(bm0 + r, M - 1);
             const int64_t gk = k0 + ch * 16;
-            ra[i] = gk < K ? *reinterpret_cast<const v4i *>(A + gm * K + gk) : v4i{0, 0, 0, 0};
+            if constexpr (RAGGED)
+                ra[i] = load16_ragged(A + gm * K, gk, K);
+            else
+                ra[i] = gk < K ? *reinterpret_cast<const v4i *>(A + gm * K + gk) : v4i{0, 0, 0, 0};
         }
         if constexpr (!TERNARY) {
 #pragma unroll
@@ -170,7 +236,23 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_tiled_kernel(
                 const int r = c / 4, ch = c % 4;
                 const int64_t gn = std::min<int64_t>(bn0 + r, N - 1);
                 const int64_t gk = k0 + ch * 16;
-                rb[i] = gk < K ? *reinterpret_cast<const v4i *>(B8 + gn * K + gk) : v4i{0, 0, 0, 0};
+                if constexpr (RAGGED)
+                    rb[i] = load16_ragged(B8 + gn * K, gk, K);
+                else
+                    rb[i] = gk < K ? *reinterpret_cast<const v4i *>(B8 + gn * K + gk)
+                                   : v4i{0, 0, 0, 0};
+            }
+        } else if constexpr (RAGGED) {
+#pragma unroll
+            for (int i = 0; i < C::B_ROWS; ++i) {
+                const int r = tid + i * C::NT;
+                if (r < BN) {
+                    const int64_t gn = std::min<int64_t>(bn0 + r, N - 1);
+                    rt[i].x = (int)ternary_word_ragged(Bp, gn, k0, N, K);
+                    rt[i].y = (int)ternary_word_ragged(Bp, gn, k0 + 16, N, K);
+                    rt[i].z = (int)ternary_word_ragged(Bp, gn, k0 + 32, N, K);
+                    rt[i].w = (int)ternary_word_ragged(Bp, gn, k0 + 48, N, K);
+                }
             }
         } else {
 #pragma unroll
@@ -217,7 +299,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_tiled_kernel(
 #pragma unroll
                     for (int ch = 0; ch < 4; ++ch)
                         *reinterpret_cast<v4i *>(&Bs[buf][r * kBK + ((ch ^ swz(r)) * 16)]) =
-                            ternary_word_to_i8x16(w[ch]);
+                            PERM ? ternary_perm_decode(w[ch]) : ternary_word_to_i8x16(w[ch]);
                 }
             }
         }
@@ -811,10 +893,13 @@ __device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
 // start of that stage, so no table lookup sits just before the MFMAs that use
 // it.
 template <int BM_, int BN_, int WGM_, int WGN_, int PRE, int IL, int KS_ = 1, bool TER_ = false,
-          int DEC_ = 0>
+          int DEC_ = 0, bool PERM_ = false>
 struct L128Cfg {
     static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, KS = KS_;
     static constexpr bool TER = TER_;
+    // PERM (ternary only): the weights are in the MFMA layout of
+    // rnn_ternary_prepack and decode by byte permutes, with no LDS table
+    static constexpr bool PERM = PERM_;
     static constexpr int DEC = DEC_;
     static constexpr int NW = WGM * WGN, NT = NW * 64;          // per K group
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
@@ -829,7 +914,7 @@ struct L128Cfg {
     static constexpr int NDMA = WPW + APW;                      // DMA slots per stage
     static constexpr int GROUP_LDS = RA * A_SLOT + RW * W_SLOT;
     static constexpr int LDS_BYTES = KS * GROUP_LDS;
-    static constexpr int LUT_BYTES = TER ? 1024 * kTerLutCopies : 0;  // decode table copies
+    static constexpr int LUT_BYTES = TER && !PERM ? 1024 * kTerLutCopies : 0;  // decode table copies
     static constexpr int HALF = FM * FN;                        // MFMAs per 64-K half
     static constexpr int T0 = HALF + PRE;                       // barrier slot
     // fragment-read slots of a half: weight fragments (ternary: code words,
@@ -842,6 +927,10 @@ struct L128Cfg {
     static_assert(LDS_BYTES + LUT_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(KS == 1 || (KS - 1) * PART <= LDS_BYTES, "split-K partials fit in LDS");
     static_assert(DEC > 0 || (RD <= HALF && T0 + RD <= 2 * HALF), "fragment-read slots");
+    static_assert(!PERM || TER, "the MFMA code layout is a ternary layout");
+    // the ternary weight-row DMA and the early-word schedule are written for
+    // one row of waves per K group
+    static_assert(!TER || WGM == 1, "ternary tiles: one row of waves");
     static_assert(DEC == 0 || (TER && FN + FM <= T0 && T0 + FM < 2 * HALF &&
                                DEC >= 1 && T0 + DEC + FN <= 2 * HALF),
                   "early-word slots: second-half decodes and activations before the barrier, "
@@ -875,6 +964,9 @@ using PrefillCfg = L128Cfg<256, 224, 4, 2, 0, 1>;
 // 128 x 64 tiles with the plain schedule.
 using L128Ter = L128Cfg<64, 128, 1, 4, 0, 3, 2, true, 3>;
 static_assert(L128Ter::window_ok(), "DMA window");
+// The same tiles and schedule on weights in the MFMA code layout.
+using L128TerPerm = L128Cfg<64, 128, 1, 4, 0, 5, 2, true, 3, true>;
+static_assert(L128TerPerm::window_ok(), "DMA window");
 
 template <class C, bool OUT_Y, bool OUT_ACC>
 __global__ __launch_bounds__(C::KS *C::NT)
@@ -956,6 +1048,14 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
     const int wm = wid / C::WGN, wn = wid % C::WGN;
     const int fr = lane & 15, fq = lane >> 4;
     const uint32_t *const lut_lane = lut + lane % kTerLutCopies;  // this lane's table copy
+    // 2-bit codes -> the int8 MFMA operand: byte permutes (MFMA layout) or the
+    // replicated LDS table (reference layout)
+    auto decode = [&](uint32_t w) -> v4i {
+        if constexpr (C::PERM)
+            return ternary_perm_decode(w);
+        else
+            return ternary_lut_decode_rep<kTerLutCopies>(lut_lane, w);
+    };
     // fragment rows start at multiples of 16, so the row swizzles depend on fr
     const int a_row = (wm * C::WM + fr) * kL, b_row = (wn * C::WN + fr) * C::W_ROW;
     const int ch0 = 16 * (fq ^ swz8(fr)), ch1 = 16 * ((4 + fq) ^ swz8(fr));
@@ -981,7 +1081,7 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
         } else if constexpr (u < C::FN + C::FM) {
             read_a(aslot, u - C::FN, ch, f);
         } else if constexpr (C::TER && u < C::RD) {
-            f.b[u - C::FN - C::FM] = ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f.w[u - C::FN - C::FM]);
+            f.b[u - C::FN - C::FM] = decode(f.w[u - C::FN - C::FM]);
         }
     };
 
@@ -1007,7 +1107,7 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
         if (C::head(q)) dma_op(q, -1, 2);
     // the decode table is built while the first loads are in flight (the
     // barrier below publishes it)
-    if constexpr (C::TER) {
+    if constexpr (C::TER && !C::PERM) {
         for (int t = threadIdx.x; t < 256 * kTerLutCopies; t += C::KS * C::NT)
             lut[t] = ternary_lut_entry((uint32_t)(t / kTerLutCopies));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1032,7 +1132,7 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
 #pragma unroll
         for (int j = 0; j < C::FM; ++j) read_a(sa, j, ch0, f0);
 #pragma unroll
-        for (int i = 0; i < C::FN; ++i) f0.b[i] = ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f0.w[i]);
+        for (int i = 0; i < C::FN; ++i) f0.b[i] = decode(f0.w[i]);
     } else {
         static_for<C::RD>([&](auto uc) { read_slot(uc, sa, sw, ch0, wb0, f0); });
     }
@@ -1068,7 +1168,7 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
                 // both halves, its first-half activations and, DEC MFMAs in,
                 // its first-half decodes
                 if constexpr (t < C::FN)
-                    f1.b[t] = ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f1.w[t]);
+                    f1.b[t] = decode(f1.w[t]);
                 else if constexpr (t < C::FN + C::FM)
                     read_a(a_cur, t - C::FN, ch1, f1);
                 if constexpr (t == C::T0) {
@@ -1080,7 +1180,7 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
                 if constexpr (t > C::T0 && t <= C::T0 + C::FM) read_a(a_nxt, t - C::T0 - 1, ch0, f0);
                 if constexpr (t >= C::T0 + C::DEC && t < C::T0 + C::DEC + C::FN)
                     f0.b[t - C::T0 - C::DEC] =
-                        ternary_lut_decode_rep<kTerLutCopies>(lut_lane, f0.w[t - C::T0 - C::DEC]);
+                        decode(f0.w[t - C::T0 - C::DEC]);
             } else {
                 // second half of this stage -> f1 (weight fragments first:
                 // they were released earliest by the previous stage's MFMAs)
@@ -1104,7 +1204,51 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
     // last MFMA results -> accumulator reads (16-cycle MFMA: >= 18 wait states)
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
-    if constexpr (C::KS > 1) {
+    if constexpr (C::KS == 2 && C::FM % 2 == 0) {
+        // The two K groups exchange halves of their wave tiles through the
+        // (now idle) stage buffers: group 0 keeps the first FM/2 row blocks
+        // and hands over the rest, group 1 the reverse. Each adds the
+        // partner's partial sums to the half it keeps (exact: wrapping int32
+        // addition is associative) and writes that half of the output, so the
+        // epilogue is split over all 8 waves.
+        constexpr int HF = C::FM / 2;
+        constexpr int WPART = C::FN * HF * 64;  // v4i per wave and group
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // every group is done with its stages
+        v4i *red = reinterpret_cast<v4i *>(smem_all);
+        auto finish = [&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            constexpr int give = g == 0 ? HF : 0, keep = g == 0 ? 0 : HF;
+            v4i *dst = red + (g * C::NW + wid) * WPART + lane;
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+                for (int j = 0; j < HF; ++j) dst[(i * HF + j) * 64] = acc[i][give + j];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            const v4i *srcp = red + ((1 - g) * C::NW + wid) * WPART + lane;
+            v4i half[C::FN][HF];
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+                for (int j = 0; j < HF; ++j) {
+                    const v4i p = srcp[(i * HF + j) * 64];
+                    const v4i a = acc[i][keep + j];
+                    half[i][j].x = (int)((uint32_t)a.x + (uint32_t)p.x);
+                    half[i][j].y = (int)((uint32_t)a.y + (uint32_t)p.y);
+                    half[i][j].z = (int)((uint32_t)a.z + (uint32_t)p.z);
+                    half[i][j].w = (int)((uint32_t)a.w + (uint32_t)p.w);
+                }
+            tile_epilogue<HF, C::FN, OUT_Y, OUT_ACC>(epi, half, bm0 + wm * C::WM + fr + 16 * keep,
+                                                     bn0 + wn * C::WN + 4 * fq);
+        };
+        if (kg == 0)
+            finish(std::integral_constant<int, 0>{});
+        else
+            finish(std::integral_constant<int, 1>{});
+        return;
+    } else if constexpr (C::KS > 1) {
         // groups 1..KS-1 park their partial sums in the (now idle) stage
         // buffers, lane-contiguous 16-byte slots; group 0 adds them (exact:
         // wrapping int32 addition is associative)
@@ -1464,17 +1608,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wl_kernel(
 }
 
 // ------------------------------------------------------------ igemm packing
-// A u8 [M,K] -> s8 [M,Kp] (x ^ 0x80 == x - 128; pad k >= K with 0).
-__global__ void pack_a_u8_kernel(const uint8_t *__restrict__ a, int64_t M, int64_t K, int64_t Kp,
-                                 int8_t *__restrict__ out) {
-    const int64_t total = M * Kp;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t m = i / Kp, k = i % Kp;
-        out[i] = k < K ? (int8_t)(a[m * K + k] ^ 0x80u) : (int8_t)0;
-    }
-}
-
 // B i8 [K,N] -> B^T [N,Kp] through a 64x64 LDS tile (zero pad k >= K).
 __global__ __launch_bounds__(256) void transpose_b_kernel(const int8_t *__restrict__ b, int64_t K,
                                                           int64_t N, int64_t Kp,
@@ -1499,24 +1632,61 @@ __global__ void fill_i32_kernel(int32_t *__restrict__ p, int64_t n, int32_t v) {
         p[i] = v;
 }
 
-// colsum[n] = sum_k b[k,n] (wrapping int32; order-independent).
-__global__ void colsum_kernel(const int8_t *__restrict__ b, int64_t K, int64_t N,
-                              int32_t *__restrict__ colsum) {
-    const int64_t n = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+// colsum[n] = sum_k b[k,n] (wrapping int32; order-independent), as the row
+// sums of the transposed B^T [N, Kp] (zero padded): one wave per row, each
+// lane summing 16 contiguous bytes per step, then a wave reduction.
+__global__ __launch_bounds__(256) void colsum_rows_kernel(const int8_t *__restrict__ bt, int64_t N,
+                                                        int64_t Kp, int32_t *__restrict__ colsum) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (n >= N) return;
+    const int8_t *row = bt + n * Kp;
     uint32_t s = 0;
-    for (int64_t k = 0; k < K; ++k) s += (uint32_t)(int32_t)b[k * N + n];
-    colsum[n] = (int32_t)s;
+    for (int64_t k = 16 * lane; k < Kp; k += 16 * 64) {
+        const v4i v = *reinterpret_cast<const v4i *>(row + k);
+        const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) s += (uint32_t)(int32_t)(int8_t)(w[q] >> (8 * b));
+    }
+    for (int off = 32; off > 0; off >>= 1) s += (uint32_t)__shfl_xor((int)s, off, 64);
+    if (lane == 0) colsum[n] = (int32_t)s;
+}
+
+// A u8 [M,K] -> s8 [M,Kp] (x ^ 0x80 == x - 128; pad k >= K with 0), 16 output
+// bytes per thread (Kp is a multiple of 64).
+__global__ void pack_a_u8_v16_kernel(const uint8_t *__restrict__ a, int64_t M, int64_t K,
+                                     int64_t Kp, int8_t *__restrict__ out) {
+    const int64_t chunks = M * (Kp / 16);
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < chunks;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = i / (Kp / 16), k0 = (i % (Kp / 16)) * 16;
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int64_t k = k0 + 4 * q + b;
+                const uint32_t x = k < K ? (uint32_t)(a[m * K + k] ^ 0x80u) : 0u;
+                v |= x << (8 * b);
+            }
+            w[q] = v;
+        }
+        *reinterpret_cast<v4i *>(out + m * Kp + k0) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
 }
 
 // ------------------------------------------------------------ dispatch
-template <int BM, int BN, int WM, int WN, bool TERNARY>
+template <int BM, int BN, int WM, int WN, bool TERNARY, bool RAGGED = false, bool PERM = false>
 static int launch_tiled(const int8_t *A, const void *B, int64_t M, int64_t N, int64_t K,
                         const Epilogue &epi, hipStream_t st, const char *name) {
     using C = TileGemm<BM, BN, WM, WN, TERNARY>;
     RNN_REQUIRE(ceil_div(M, BM) <= 65535, "%s: M too large", name);
     dim3 grid((unsigned)ceil_div(N, BN), (unsigned)ceil_div(M, BM));
-    gemm_tiled_kernel<BM, BN, WM, WN, TERNARY><<<grid, C::NT, 0, st>>>(A, B, M, N, K, epi);
+    gemm_tiled_kernel<BM, BN, WM, WN, TERNARY, RAGGED, PERM><<<grid, C::NT, 0, st>>>(A, B, M, N, K,
+                                                                                   epi);
     return check_launch(name);
 }
 
@@ -1647,10 +1817,6 @@ extern "C" int rnn_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *
     RNN_REQUIRE(y || acc_out, "%s: y and acc_out both null", name);
     RNN_REQUIRE(!y || (sa && sw), "%s: y requires sa and sw", name);
     RNN_REQUIRE(k == 0 || (aq && wq), "%s: null operand", name);
-    if (k % 16 != 0 || !aligned16(aq) || !aligned16(wq))
-        return set_error(RNN_ERR_UNSUPPORTED,
-                         "%s: k must be a multiple of 16 and operands 16-byte aligned (k=%lld)",
-                         name, (long long)k);
     Epilogue epi{sa, sw, bias, y, acc_out, nullptr, m, n, (flags & RNN_FLAG_RELU) ? 1 : 0};
     const unsigned algo = flags & RNN_ALGO_MASK;
     RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_TILED || algo == RNN_ALGO_GEMV ||
@@ -1658,6 +1824,16 @@ extern "C" int rnn_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *
                 "%s: unknown algo 0x%x", name, algo);
     if (algo == RNN_ALGO_GEMV)
         RNN_REQUIRE(m <= 16, "%s: RNN_ALGO_GEMV needs m <= 16", name);
+    if (k % 16 != 0 || !aligned16(aq) || !aligned16(wq)) {
+        // any k and alignment: the byte-assembling tiled kernel (AUTO / TILED)
+        if (algo == RNN_ALGO_GEMV || algo == RNN_ALGO_TILED_DMA)
+            return set_error(RNN_ERR_UNSUPPORTED,
+                             "%s: the forced GEMV / LDS-DMA kernels need k %% 16 == 0 and 16-byte "
+                             "aligned operands (k=%lld)",
+                             name, (long long)k);
+        return launch_tiled<128, 128, 64, 64, false, true>(aq, wq, m, n, k, epi, as_stream(stream),
+                                                           name);
+    }
     const bool dma = dma_ok(aq, wq, n, k, epi);
     if (algo == RNN_ALGO_TILED_DMA && !dma)
         return set_error(RNN_ERR_UNSUPPORTED,
@@ -1679,20 +1855,35 @@ extern "C" int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_
     RNN_ENTRY();
     const char *name = "rnn_ternary_gemm";
     RNN_REQUIRE(m >= 0 && k >= 0 && n >= 0, "%s: negative size", name);
-    RNN_REQUIRE((flags & ~(RNN_FLAG_RELU | RNN_ALGO_MASK)) == 0, "%s: unknown flags 0x%x", name,
-                flags);
+    RNN_REQUIRE((flags & ~(RNN_FLAG_RELU | RNN_FLAG_TERNARY_MFMA_LAYOUT | RNN_ALGO_MASK)) == 0,
+                "%s: unknown flags 0x%x", name, flags);
     const unsigned algo = flags & RNN_ALGO_MASK;
+    const bool mfma_layout = (flags & RNN_FLAG_TERNARY_MFMA_LAYOUT) != 0;
     RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_TILED || algo == RNN_ALGO_TILED_DMA,
                 "%s: algo 0x%x not available for the ternary GEMM", name, algo);
     if (m == 0 || n == 0) return RNN_OK;
     RNN_REQUIRE(y || acc_out, "%s: y and acc_out both null", name);
     RNN_REQUIRE(!y || (sa && sw), "%s: y requires sa and sw", name);
     RNN_REQUIRE(k == 0 || (aq && packed), "%s: null operand", name);
-    if (k % 16 != 0 || !aligned16(aq) || ((uintptr_t)packed & 3) != 0)
-        return set_error(RNN_ERR_UNSUPPORTED,
-                         "%s: k must be a multiple of 16 and aq 16-byte aligned (k=%lld)", name,
-                         (long long)k);
+    RNN_REQUIRE(((uintptr_t)packed & 3) == 0, "%s: packed must be 4-byte aligned (u32 words)",
+                name);
+    RNN_REQUIRE(!mfma_layout || k % 16 == 0,
+                "%s: the MFMA code layout needs k %% 16 == 0 (k=%lld)", name, (long long)k);
     Epilogue epi{sa, sw, bias, y, acc_out, nullptr, m, n, (flags & RNN_FLAG_RELU) ? 1 : 0};
+    hipStream_t st = as_stream(stream);
+    if (k % 16 != 0 || !aligned16(aq)) {
+        // rows not word aligned, or unaligned activations: the tiled kernel that
+        // gathers codes from arbitrary bit offsets (AUTO / TILED)
+        if (algo == RNN_ALGO_TILED_DMA)
+            return set_error(RNN_ERR_UNSUPPORTED,
+                             "%s: RNN_ALGO_TILED_DMA needs k %% 128 == 0 and 16-byte aligned "
+                             "buffers (k=%lld)",
+                             name, (long long)k);
+        if (mfma_layout)  // k % 16 == 0 here: only the activations are unaligned
+            return launch_tiled<128, 128, 64, 64, true, true, true>(aq, packed, m, n, k, epi, st,
+                                                                    name);
+        return launch_tiled<128, 128, 64, 64, true, true>(aq, packed, m, n, k, epi, st, name);
+    }
     const int8_t *pb = reinterpret_cast<const int8_t *>(packed);
     // LDS-DMA path: packed rows are K/4 bytes, 16-byte aligned when k % 64 == 0
     const bool dma = dma_ok(aq, pb, n, k, epi);
@@ -1701,18 +1892,50 @@ extern "C" int rnn_ternary_gemm(const int8_t *aq, const float *sa, const uint32_
                          "%s: RNN_ALGO_TILED_DMA needs k %% 128 == 0, n %% 4 == 0 and 16-byte "
                          "aligned buffers (k=%lld, n=%lld)",
                          name, (long long)k, (long long)n);
-    hipStream_t st = as_stream(stream);
-    // 128x64 tiles (4 waves of 64x32): a 512x4096 output is 256 tiles, one per
-    // CU; each weight code word is decoded once per 128 activation rows. With
-    // one wave per SIMD, each 64-K step's dependent chain (code word read, LDS
-    // table lookups, MFMAs) is exposed, so K is split over 2 wave groups when
-    // it divides (8 waves per CU, int32 partial sums added in LDS).
+    // 64x128 tiles of two K groups of 4 waves (64x32 each): a 512x4096 output
+    // is 256 tiles, one per CU, and each weight code word is decoded once per
+    // CU. Codes in the reference layout decode through the replicated LDS
+    // table; codes in the MFMA layout through byte permutes.
+    const bool l128 = k % (kL * L128Ter::KS) == 0 && l128_fits(m, n, k, true);
     if (algo == RNN_ALGO_TILED_DMA || (algo == RNN_ALGO_AUTO && dma)) {
-        if (k % (kL * L128Ter::KS) == 0 && l128_fits(m, n, k, true))
-            return launch_l128<L128Ter>(aq, pb, m, n, k, epi, st, name);
-        return launch_dma<128, 64, 2, 2, 4, true>(aq, pb, m, n, k, epi, st, name);
+        if (l128 && mfma_layout) return launch_l128<L128TerPerm>(aq, pb, m, n, k, epi, st, name);
+        if (l128) return launch_l128<L128Ter>(aq, pb, m, n, k, epi, st, name);
+        if (!mfma_layout) return launch_dma<128, 64, 2, 2, 4, true>(aq, pb, m, n, k, epi, st, name);
+        if (algo == RNN_ALGO_TILED_DMA)
+            return set_error(RNN_ERR_UNSUPPORTED,
+                             "%s: RNN_ALGO_TILED_DMA on the MFMA code layout needs k %% 256 == 0 "
+                             "(k=%lld)",
+                             name, (long long)k);
     }
+    if (mfma_layout)
+        return launch_tiled<128, 128, 64, 64, true, false, true>(aq, packed, m, n, k, epi, st, name);
     return launch_tiled<128, 128, 64, 64, true>(aq, packed, m, n, k, epi, st, name);
+}
+
+// ------------------------------------------------------- ternary MFMA layout
+// One thread per 32-bit word: the 16 two-bit codes are moved to the MFMA
+// layout (ternary_word_to_mfma_layout). Rows stay word-aligned (K % 16 == 0),
+// so the words keep their positions and a row is still K/16 words.
+__global__ void ternary_prepack_kernel(const uint32_t *__restrict__ in, int64_t words,
+                                       uint32_t *__restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = ternary_word_to_mfma_layout(in[i]);
+}
+
+extern "C" int rnn_ternary_prepack(const uint32_t *packed, int64_t rows, int64_t cols,
+                                   uint32_t *out, void *stream) {
+    RNN_ENTRY();
+    const char *name = "rnn_ternary_prepack";
+    RNN_REQUIRE(rows >= 0 && cols >= 0, "%s: negative size", name);
+    RNN_REQUIRE(cols % 16 == 0, "%s: cols must be a multiple of 16 (row-aligned words), got %lld",
+                name, (long long)cols);
+    const int64_t words = rows * cols / 16;
+    if (words == 0) return RNN_OK;
+    RNN_REQUIRE(packed && out, "%s: null pointer", name);
+    const unsigned g = (unsigned)std::min<int64_t>(ceil_div(words, 256), 8 * device_cu_count());
+    ternary_prepack_kernel<<<g, 256, 0, as_stream(stream)>>>(packed, words, out);
+    return check_launch(name);
 }
 
 static int64_t igemm_kp(int64_t k) { return (k + 63) / 64 * 64; }
@@ -1737,16 +1960,19 @@ static int igemm_on_workspace(const uint8_t *a, const int8_t *b, int32_t *c, int
     int32_t *cs = reinterpret_cast<int32_t *>(bt + up(n * kp));
     const int cus = device_cu_count();
     RNN_REQUIRE(ceil_div(kp, 64) <= 65535, "%s: k too large", name);
-    pack_a_u8_kernel<<<(unsigned)std::min<int64_t>(ceil_div(m * kp, 256), 8 * cus), 256, 0, st>>>(
-        a, m, k, kp, ap);
+    pack_a_u8_v16_kernel<<<(unsigned)std::min<int64_t>(ceil_div(m * kp / 16, 256), 8 * cus), 256, 0,
+                           st>>>(a, m, k, kp, ap);
     RNN_TRY(check_launch(name));
     dim3 g((unsigned)ceil_div(n, 64), (unsigned)ceil_div(kp, 64));
     transpose_b_kernel<<<g, 256, 0, st>>>(b, k, n, kp, bt);
     RNN_TRY(check_launch(name));
-    colsum_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(b, k, n, cs);
+    colsum_rows_kernel<<<(unsigned)ceil_div(n, 4), 256, 0, st>>>(bt, n, kp, cs);
     RNN_TRY(check_launch(name));
     Epilogue epi{nullptr, nullptr, nullptr, nullptr, c, cs, m, n, 0};
     if (m <= 16) return launch_gemv(ap, bt, m, n, kp, epi, st, name);
+    // 64x64 tiles while 128x128 tiles would leave most CUs idle
+    if (ceil_div(m, 128) * ceil_div(n, 128) < cus)
+        return launch_tiled<64, 64, 32, 32, false>(ap, bt, m, n, kp, epi, st, name);
     return launch_tiled<128, 128, 64, 64, false>(ap, bt, m, n, kp, epi, st, name);
 }
 

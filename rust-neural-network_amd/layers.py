@@ -291,9 +291,21 @@ class TernaryLinear(Module):
                                         self.out_features, self.bias)
 
     def forward_int8(self, x, relu=False):
+        """int8 activations x 2-bit weights on int8 MFMA. When in_features %
+        16 == 0 the codes are rearranged once (rnn_ternary_prepack) into the
+        layout the GEMM decodes with byte permutes; the reference-layout
+        `packed` field is kept as the source of truth."""
         aq, sa = H.quant_rows_i8(x)
-        y, _ = H.ternary_gemm(aq, sa, self.ternary_weight.packed, self.ternary_weight.scales,
-                              self.out_features, self.bias, relu=relu)
+        tw = self.ternary_weight
+        if self.in_features % 16 == 0:
+            if getattr(self, "_mfma_packed", None) is None:
+                self._mfma_packed = H.ternary_prepack(tw.packed, self.out_features,
+                                                      self.in_features)
+            y, _ = H.ternary_gemm(aq, sa, self._mfma_packed, tw.scales, self.out_features,
+                                  self.bias, relu=relu, mfma_layout=True)
+        else:
+            y, _ = H.ternary_gemm(aq, sa, tw.packed, tw.scales, self.out_features, self.bias,
+                                  relu=relu)
         return y
 
 

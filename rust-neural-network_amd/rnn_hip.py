@@ -27,6 +27,7 @@ ALGO_TILED = 0x10
 ALGO_GEMV = 0x20
 ALGO_TILED_DMA = 0x30
 ALGO_GEMV_MFMA = 0x40
+FLAG_TERNARY_MFMA_LAYOUT = 0x100
 
 TERNARY_ROWS = 0
 TERNARY_ABSMEAN = 1
@@ -68,6 +69,7 @@ SIGNATURES = {
     "rnn_ternary_dequantize": ([_P, _I64, _P, _I64, _I64, _P, _P], _INT),
     "rnn_ternary_linear_forward": ([_P, _I64, _I64, _P, _P, _I64, _P, _P, _P], _INT),
     "rnn_ternary_gemm": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _UINT, _P, _P, _P], _INT),
+    "rnn_ternary_prepack": ([_P, _I64, _I64, _P, _P], _INT),
     "rnn_rotor_rotation_matrices": ([_P, _I64, _P, _P], _INT),
     "rnn_rotorquant_quantize": ([_P, _I64, _I64, _INT, _P, _P, _P, _P, _P], _INT),
     "rnn_rotorquant_dequantize": ([_P, _P, _I64, _I64, _P, _P, _P], _INT),
@@ -340,8 +342,19 @@ def ternary_linear_forward(x, packed, scales, out_f, bias=None, stream=None):
     return y
 
 
+def ternary_prepack(packed, rows, cols, stream=None):
+    """The MFMA code layout of a ternary weight [rows, cols] (cols % 16 == 0):
+    same size, read by ternary_gemm(..., mfma_layout=True)."""
+    import torch
+    _dev(packed, torch.int32, "packed")
+    _need(packed, rows * cols // 16, "packed", at_least=True)
+    out = _empty((rows * cols // 16,), torch.int32, packed)
+    _check(load().rnn_ternary_prepack(_ptr(packed), rows, cols, _ptr(out), _stream(stream)))
+    return out
+
+
 def ternary_gemm(aq, sa, packed, sw, n, bias=None, relu=False, want_y=True, want_acc=False,
-                 y=None, stream=None, algo=ALGO_AUTO):
+                 y=None, stream=None, algo=ALGO_AUTO, mfma_layout=False):
     import torch
     _dev(aq, torch.int8, "aq"), _dev(packed, torch.int32, "packed")
     _dev(sa, torch.float32, "sa"), _dev(sw, torch.float32, "sw"), _dev(bias, torch.float32, "bias")
@@ -352,9 +365,9 @@ def ternary_gemm(aq, sa, packed, sw, n, bias=None, relu=False, want_y=True, want
     if want_y and y is None:
         y = _empty((m, n), torch.float32, aq)
     acc = _empty((m, n), torch.int32, aq) if want_acc else None
+    flags = (FLAG_RELU if relu else 0) | (FLAG_TERNARY_MFMA_LAYOUT if mfma_layout else 0) | algo
     _check(load().rnn_ternary_gemm(_ptr(aq), _ptr(sa), _ptr(packed), _ptr(sw), _ptr(bias), m, k,
-                                   n, (FLAG_RELU if relu else 0) | algo, _ptr(y), _ptr(acc),
-                                   _stream(stream)))
+                                   n, flags, _ptr(y), _ptr(acc), _stream(stream)))
     return y, acc
 
 

@@ -58,14 +58,18 @@ def test_gemm_argument_rules(lib):
     # float output needs the scales
     _status(lib.rnn_w8a8_linear(FAKE, None, FAKE, FAKE, None, 4, 16, 4, 0, FAKE, None, None),
             H.RNN_ERR_INVALID_ARG, "requires sa")
-    # k must be a multiple of 16
-    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 4, 17, 4, 0, FAKE, None, None),
-            H.RNN_ERR_UNSUPPORTED, "multiple of 16")
+    # any k runs on the byte-assembling kernel, but the forced GEMV / LDS-DMA need k % 16 == 0
+    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 4, 17, 4, H.ALGO_GEMV, FAKE, None,
+                                None), H.RNN_ERR_UNSUPPORTED, "k % 16 == 0")
+    _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 40, 17, 4, H.ALGO_TILED_DMA, FAKE,
+                                None, None), H.RNN_ERR_UNSUPPORTED, "k % 16 == 0")
     # GEMV forced beyond 16 rows
     _status(lib.rnn_w8a8_linear(FAKE, FAKE, FAKE, FAKE, None, 17, 16, 4, H.ALGO_GEMV, FAKE, None,
                                 None), H.RNN_ERR_INVALID_ARG, "m <= 16")
-    _status(lib.rnn_ternary_gemm(FAKE, FAKE, FAKE, FAKE, None, 4, 20, 4, 0, FAKE, None, None),
-            H.RNN_ERR_UNSUPPORTED, "multiple of 16")
+    _status(lib.rnn_ternary_gemm(FAKE, FAKE, FAKE, FAKE, None, 4, 20, 4, H.ALGO_TILED_DMA, FAKE,
+                                 None, None), H.RNN_ERR_UNSUPPORTED, "k % 128 == 0")
+    _status(lib.rnn_ternary_gemm(FAKE, FAKE, ctypes.c_void_p(258), FAKE, None, 4, 32, 4, 0, FAKE,
+                                 None, None), H.RNN_ERR_INVALID_ARG, "4-byte aligned")
 
 
 def test_sgemm_argument_rules(lib):

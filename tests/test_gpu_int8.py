@@ -286,3 +286,30 @@ def test_w8a8_mlp_784_256_128_10(dev, hip):
         h, _ = hip.w8a8_linear(aq_d, sa_d, to_dev(wq, dev), to_dev(sw, dev), to_dev(b, dev),
                                relu=relu)
     assert_f32_equal(host(h), h_ref)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 5), (3, 7, 17), (5, 100, 33), (40, 257, 65),
+                                   (32, 787, 256), (130, 300, 129)])
+def test_w8a8_any_k_and_unaligned_operands(dev, hip, m, k, n):
+    """k % 16 != 0 and operands at odd byte addresses: the reference's igemm
+    takes any K (src/int8.rs:288-296), and AUTO routes such calls to the
+    byte-assembling tiled kernel. int32 and fp32 bit-exact."""
+    import torch
+    aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=3 * m + k)
+    for relu, b in ((False, None), (True, bias)):
+        y, acc = run_w8a8(dev, hip, aq, sa, wq, sw, b, relu, hip.ALGO_AUTO)
+        ye, acce = O.w8a8_linear(aq, sa, wq, sw, b, relu)
+        assert np.array_equal(acc, acce)
+        assert_f32_equal(y, ye)
+    # the same operands one byte past an aligned address (k % 16 == 0 here too)
+    for mm, kk, nn in ((m, k, n), (8, 64, 24)):
+        aq2, sa2, wq2, sw2, _ = w8a8_case(mm, kk, nn, seed=mm + kk)
+        abuf = torch.zeros(mm * kk + 1, dtype=torch.int8, device=dev)
+        wbuf = torch.zeros(nn * kk + 1, dtype=torch.int8, device=dev)
+        abuf[1:] = to_dev(aq2.reshape(-1), dev)
+        wbuf[1:] = to_dev(wq2.reshape(-1), dev)
+        y2, acc2 = hip.w8a8_linear(abuf[1:].view(mm, kk), to_dev(sa2, dev), wbuf[1:].view(nn, kk),
+                                   to_dev(sw2, dev), want_acc=True)
+        ye2, acce2 = O.w8a8_linear(aq2, sa2, wq2, sw2)
+        assert np.array_equal(host(acc2), acce2)
+        assert_f32_equal(host(y2), ye2)

@@ -128,12 +128,84 @@ def test_ternary_gemm_full_config_sampled(dev, hip):
     x = W.activations(m, k, seed=8)
     aq, sa = O.quant_rows_i8(x)
     sw = np.full(n, g, np.float32)
-    y, acc = hip.ternary_gemm(to_dev(aq, dev), to_dev(sa, dev), to_dev(p.view(np.int32), dev),
-                              to_dev(sw, dev), n, want_acc=True)
     rows = np.unique(np.concatenate([np.arange(0, m, 16) + 15, [0, 1]]))
     ye, acce = O.ternary_gemm_i8(aq[rows], sa[rows], p, sw, n)
     ridx = torch.as_tensor(rows, device=dev)
-    assert np.array_equal(host(acc[ridx]), acce)
-    assert_f32_equal(host(y[ridx]), ye)
     rowsum = aq.astype(np.int64) @ t.astype(np.int64).sum(axis=0)
-    assert np.array_equal(host(acc.to(torch.int64).sum(dim=1)), rowsum)
+    pd = to_dev(p.view(np.int32), dev)
+    # the reference code layout, then the MFMA layout of rnn_ternary_prepack
+    for codes, mfma in ((pd, False), (hip.ternary_prepack(pd, n, k), True)):
+        y, acc = hip.ternary_gemm(to_dev(aq, dev), to_dev(sa, dev), codes, to_dev(sw, dev), n,
+                                  want_acc=True, mfma_layout=mfma)
+        assert np.array_equal(host(acc[ridx]), acce)
+        assert_f32_equal(host(y[ridx]), ye)
+        assert np.array_equal(host(acc.to(torch.int64).sum(dim=1)), rowsum)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 3), (5, 7, 9), (37, 50, 29), (64, 300, 70),
+                                   (200, 1001, 33)])
+def test_ternary_gemm_any_k(dev, hip, m, k, n):
+    """k % 16 != 0: rows of the flat packed codes start mid-word
+    (src/ternary.rs:46-60), and AUTO takes the kernel that gathers each row's
+    codes from arbitrary bit offsets. int32 and fp32 bit-exact, code 11
+    included; also with the activations one byte past an aligned address."""
+    import torch
+    t, p = rand_ternary(n, k, seed=m + k, with_code3=True)
+    aq = W.rng(m + k).integers(-128, 128, (m, k)).astype(np.int8)
+    sa = W.rng(m + 1).random(m).astype(np.float32)
+    sw = np.full(n, np.float32(0.7979), np.float32)
+    bias = W.rng(3).standard_normal(n).astype(np.float32)
+    abuf = torch.zeros(m * k + 1, dtype=torch.int8, device=dev)
+    abuf[1:] = to_dev(aq.reshape(-1), dev)
+    for relu, b in ((False, None), (True, bias)):
+        ye, acce = O.ternary_gemm_i8(aq, sa, p, sw, n, b, relu)
+        for a_dev in (to_dev(aq, dev), abuf[1:].view(m, k)):
+            y, acc = hip.ternary_gemm(a_dev, to_dev(sa, dev), to_dev(p.view(np.int32), dev),
+                                      to_dev(sw, dev), n, None if b is None else to_dev(b, dev),
+                                      relu=relu, want_acc=True)
+            assert np.array_equal(host(acc), acce)
+            assert_f32_equal(host(y), ye)
+
+
+def mfma_layout_np(p):
+    """The MFMA code layout, restated independently: code t of each word (bits
+    2t) moves to bits 8*(t % 4) + 2*(t // 4)."""
+    p = p.astype(np.uint64)
+    out = np.zeros_like(p)
+    for t in range(16):
+        out |= ((p >> np.uint64(2 * t)) & np.uint64(3)) << np.uint64(8 * (t % 4) + 2 * (t // 4))
+    return out.astype(np.uint32)
+
+
+def test_ternary_prepack_layout(dev, hip):
+    g = W.rng(77)
+    p = g.integers(0, 2**32, 4096, dtype=np.uint64).astype(np.uint32)   # codes 11 included
+    got = host(hip.ternary_prepack(to_dev(p.view(np.int32), dev), 64, 1024)).view(np.uint32)
+    np.testing.assert_array_equal(got, mfma_layout_np(p))
+    with pytest.raises(hip.RnnError):
+        hip.ternary_prepack(to_dev(p.view(np.int32), dev), 64, 1000)        # cols % 16 != 0
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 256, 16), (64, 512, 128), (512, 4096, 512), (37, 48, 29),
+                                   (200, 1024, 300), (17, 256, 4)])
+def test_ternary_gemm_mfma_layout(dev, hip, m, k, n):
+    """The GEMM on prepacked codes (RNN_FLAG_TERNARY_MFMA_LAYOUT) against the
+    oracle on the reference layout: the LDS-DMA kernel (k % 256 == 0) and the
+    tiled kernel (other k, unaligned activations), int32 and fp32 bit-exact."""
+    import torch
+    t, p = rand_ternary(n, k, seed=3 * m + n, with_code3=True)
+    pm = hip.ternary_prepack(to_dev(p.view(np.int32), dev), n, k)
+    aq = W.rng(m + k).integers(-128, 128, (m, k)).astype(np.int8)
+    sa = W.rng(m + 2).random(m).astype(np.float32)
+    sw = np.full(n, np.float32(0.7979), np.float32)
+    bias = W.rng(4).standard_normal(n).astype(np.float32)
+    abuf = torch.zeros(m * k + 1, dtype=torch.int8, device=dev)
+    abuf[1:] = to_dev(aq.reshape(-1), dev)
+    for relu, b in ((False, None), (True, bias)):
+        ye, acce = O.ternary_gemm_i8(aq, sa, p, sw, n, b, relu)
+        for a_dev in (to_dev(aq, dev), abuf[1:].view(m, k)):
+            y, acc = hip.ternary_gemm(a_dev, to_dev(sa, dev), pm, to_dev(sw, dev), n,
+                                      None if b is None else to_dev(b, dev), relu=relu,
+                                      want_acc=True, mfma_layout=True)
+            assert np.array_equal(host(acc), acce)
+            assert_f32_equal(host(y), ye)
