@@ -414,12 +414,19 @@ def bench_mlp(H, W, dev, steps, with_cpu):
     ms_graph = graph_timed(lambda i: model.forward(x), max(steps, 100))
     settle(lambda: model.forward(x), 0.05)
     ms_eager = timed(lambda: model.forward(x), max(steps, 100), 20)
+    ms_layers = graph_timed(lambda i: model.forward_per_layer(x), max(steps, 100))
     y = model.forward(x).cpu().numpy()
+    same = bool(np.array_equal(y, model.forward_per_layer(x).cpu().numpy()))
     ops = 2.0 * W.MLP_BATCH * sum(a * b for a, b in zip(W.MLP_LAYERS[:-1], W.MLP_LAYERS[1:]))
     ent = {"us_graph": round(ms_graph * 1e3, 2), "us_eager": round(ms_eager * 1e3, 2),
-           "ops": ops, "launches": 6, "batch": W.MLP_BATCH, "layers": list(W.MLP_LAYERS),
+           "us_graph_per_layer_launches": round(ms_layers * 1e3, 2),
+           "per_layer_bit_identical": same,
+           "ops": ops, "launches": 1, "batch": W.MLP_BATCH, "layers": list(W.MLP_LAYERS),
+           "kernel": "w8a8_mlp_kernel (rnn_w8a8_mlp: the whole chain in one launch, "
+                     "activations in LDS between layers)",
            "timing": "us_graph: HIP graph replay of the whole forward; us_eager: Python calls, "
-                     "events over back-to-back forwards"}
+                     "events over back-to-back forwards; us_graph_per_layer_launches: the same "
+                     "chain as 6 launches (quantize + GEMM per layer)"}
     if with_cpu:
         threads = cpu_threads()
         qw = [O.quant_rows_i8(params[2 * i]) for i in range(3)]

@@ -122,6 +122,23 @@ int rnn_w8a8_linear(const int8_t *aq, const float *sa, const int8_t *wq,
                     int64_t n, unsigned flags, float *y, int32_t *acc_out,
                     void *stream);
 
+/* Int8Model::forward in one launch: a chain of nlayers W8A8 layers over x
+ * [m, dims[0]] (the 784-256-128-10 MLP of the benchmark configurations).
+ * Layer l: the running activation's rows are quantized per row
+ * (rnn_quant_rows_i8's rule), multiplied by wq[l] [dims[l+1], dims[l]] int8
+ * (the Int8Weights layout) into int32, dequantized as
+ * ((acc * sa[m]) * sw[l][n]) + bias[l][n] (src/int8.rs:159-162), and, between
+ * layers when relu = 1, passed through max(., 0) (src/tensor.rs:2025-2032).
+ * y [m, dims[nlayers]]. Bit-identical to chaining rnn_quant_rows_i8 and
+ * rnn_w8a8_linear; the activation stays in LDS between layers. dims, wq, sw
+ * and bias are HOST arrays (bias may be NULL, or hold NULL entries) of device
+ * pointers. RNN_ERR_UNSUPPORTED for chains the single launch does not take:
+ * more than 4 layers, a width over 1024, dims[l] % 16 != 0 or a weight that
+ * is not 16-byte aligned (chain the per-layer calls instead). */
+int rnn_w8a8_mlp(const float *x, int64_t m, int nlayers, const int64_t *dims,
+                 const int8_t *const *wq, const float *const *sw,
+                 const float *const *bias, int relu, float *y, void *stream);
+
 /* ---------------------------------------------------------- ternary (a7-a9) */
 
 /* pack_ternary (src/ternary.rs:46-60): 16 codes per u32, LSB first,

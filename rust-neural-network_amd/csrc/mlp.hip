@@ -1,0 +1,260 @@
+// mlp.hip -- a chain of W8A8 layers (Int8Model::forward, the 784-256-128-10
+// MLP of the benchmark configurations) in one launch.
+//
+// Per layer: the running activation's rows are quantized per row
+// (scale = max|x|/127, q = round(x/scale) clamped; the rule of
+// rnn_quant_rows_i8), multiplied by the layer's int8 weight [n, k] on
+// v_mfma_i32_16x16x64_i8 into exact int32, dequantized in the reference's
+// order ((acc * sa[m]) * sw[n] + bias[n], src/int8.rs:159-162) and, between
+// layers, passed through max(., 0) (src/tensor.rs:2025-2032). The result is
+// bit-identical to chaining rnn_quant_rows_i8 and rnn_w8a8_linear per layer.
+//
+// A workgroup owns 16 rows for the whole chain: the activation stays in LDS
+// (f32 for the quantization pass, int8 codes for the MFMAs), so a layer's
+// output never goes to HBM and the chain costs one launch instead of two per
+// layer. Each of the 8 waves takes 16-column tiles of a layer; a tile's
+// weight fragments (16 bytes per lane per 64-k block) come straight from
+// global memory (each weight byte is read by one wave of each workgroup), and
+// the wave's next tile is requested before the current one's MFMAs.
+#include "common.hpp"
+#include "numerics.hpp"
+
+namespace rnn {
+
+constexpr int kMlpMaxLayers = 4;
+constexpr int kMlpMaxDim = 1024;   // widest layer input or output
+constexpr int kMlpRows = 16;       // rows per workgroup (one MFMA row block)
+constexpr int kMlpWaves = 8;
+constexpr int kMlpMaxKb = kMlpMaxDim / 64;  // 64-k blocks of the widest input
+
+struct MlpLayer {
+    const int8_t *wq;   // [n, k] int8, 16-byte aligned, k % 16 == 0
+    const float *sw;    // [n]
+    const float *bias;  // [n] or null
+    int n, k;
+};
+
+struct MlpArgs {
+    MlpLayer layer[kMlpMaxLayers];
+    int nlayers;
+    int relu;  // ReLU between layers (not after the last)
+};
+
+constexpr int kMlpPrefetchKb = 4;
+
+// Workgroup barrier for LDS traffic only. __syncthreads() also orders global
+// memory, which makes every wave wait for all of its outstanding loads; here
+// the weight loads requested ahead must stay in flight across the barriers.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}  // next-layer blocks requested ahead (k <= 256)
+
+// The weight fragments of 16-column tile t of a layer for this lane (row =
+// lane & 15, q = lane >> 4): 16 bytes of column 16 t + row at k = 64 kb + 16 q,
+// zero past K (columns past N re-read the last column; their outputs are
+// dropped).
+template <int NKB>
+__device__ __forceinline__ void mlp_load_tile(const MlpLayer &L, int t, int lane, v4i (&b)[NKB]) {
+    const int row = lane & 15, q = lane >> 4;
+    const int n = min(16 * t + row, L.n - 1);
+    const int8_t *wr = L.wq + (int64_t)n * L.k;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+        const int k = 64 * kb + 16 * q;
+        b[kb] = k < L.k ? *reinterpret_cast<const v4i *>(wr + k) : v4i{0, 0, 0, 0};
+    }
+}
+
+__global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *__restrict__ x,
+                                                                  int64_t M, MlpArgs args,
+                                                                  float *__restrict__ y) {
+    __shared__ float xf[kMlpRows][kMlpMaxDim];                            // running activation
+    __shared__ __attribute__((aligned(16))) int8_t xq[kMlpRows][kMlpMaxDim + 64];  // its codes
+    __shared__ float sa[kMlpRows];                                        // row scales
+    const int tid = threadIdx.x, wid = tid / 64, lane = tid % 64;
+    const int row = lane & 15, q = lane >> 4;
+    const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
+    const int mr = (int)std::min<int64_t>(kMlpRows, M - r0);  // valid rows
+
+    // The weights of the wave's first tile of layer 0 are requested right
+    // after the input rows, and each layer requests the next layer's first
+    // tile (when its k <= 256) before its quantization pass, so weight latency
+    // overlaps the x load, the quantization passes and the epilogues. Loads
+    // complete in issue order, so each wait is placed behind the loads it
+    // needs and in front of the ones that may stay in flight.
+    v4i cur[kMlpMaxKb], ahead[kMlpMaxKb], nxt[kMlpPrefetchKb];
+    bool have_cur = wid < (args.layer[0].n + 15) / 16;
+    // the second tile of layer 0 too (layer 0 is usually the widest)
+    bool have_ahead = wid + kMlpWaves < (args.layer[0].n + 15) / 16;
+
+    // the input rows (rows past M read as zeros; their outputs are dropped):
+    // every load of the thread is issued before the first LDS write, from a
+    // clamped (always valid) address, and masked afterwards
+    const int k0 = args.layer[0].k;
+    if (k0 % 4 == 0 && ((uintptr_t)x & 15) == 0) {
+        constexpr int XV = kMlpRows * kMlpMaxDim / 4 / (kMlpWaves * 64);
+        const int k4 = k0 / 4, total = kMlpRows * k4;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + r0 * k0);
+        const int last4 = mr * k4 - 1;  // the last valid float4 of the block's rows
+        float4 v[XV];
+#pragma unroll
+        for (int i = 0; i < XV; ++i) v[i] = x4[min(tid + i * kMlpWaves * 64, last4)];
+        if (have_cur) mlp_load_tile<kMlpMaxKb>(args.layer[0], wid, lane, cur);
+        if (have_ahead) mlp_load_tile<kMlpMaxKb>(args.layer[0], wid + kMlpWaves, lane, ahead);
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int t = tid + i * kMlpWaves * 64;
+            if (t < total) {
+                const int r = t / k4, c = 4 * (t % k4);
+                const bool ok = r < mr;
+                xf[r][c] = ok ? v[i].x : 0.0f, xf[r][c + 1] = ok ? v[i].y : 0.0f;
+                xf[r][c + 2] = ok ? v[i].z : 0.0f, xf[r][c + 3] = ok ? v[i].w : 0.0f;
+            }
+        }
+    } else {
+        for (int t = tid; t < kMlpRows * k0; t += kMlpWaves * 64) {
+            const int r = t / k0, c = t % k0;
+            xf[r][c] = r < mr ? x[(r0 + r) * k0 + c] : 0.0f;
+        }
+        if (have_cur) mlp_load_tile<kMlpMaxKb>(args.layer[0], wid, lane, cur);
+        if (have_ahead) mlp_load_tile<kMlpMaxKb>(args.layer[0], wid + kMlpWaves, lane, ahead);
+    }
+    lds_barrier();
+
+    for (int l = 0; l < args.nlayers; ++l) {
+        const MlpLayer L = args.layer[l];
+        const int K = L.k, N = L.n, kb_n = (K + 63) / 64;
+        const bool last = l + 1 == args.nlayers;
+        const bool relu = !last && args.relu;
+        const int ntiles = (N + 15) / 16;
+        // next layer's first tile, requested now
+        bool have_nxt = false;
+        if (!last) {
+            const MlpLayer Ln = args.layer[l + 1];
+            have_nxt = Ln.k <= 64 * kMlpPrefetchKb && wid < (Ln.n + 15) / 16;
+            if (have_nxt) mlp_load_tile<kMlpPrefetchKb>(Ln, wid, lane, nxt);
+        }
+        // quantize: one wave per row, max over the row (order-independent),
+        // then the codes, zero-padded to whole 64-k blocks. Four elements per
+        // lane per step, so that four independent LDS reads and divisions
+        // are in flight instead of one dependent chain.
+        for (int r = wid; r < kMlpRows; r += kMlpWaves) {
+            float mx = 0.0f;
+            for (int c0 = 0; c0 < 64 * kb_n; c0 += 256) {
+                float v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int c = c0 + 64 * u + lane;
+                    v[u] = c < K ? xf[r][c] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fabsf(v[u]));
+            }
+            mx = wave_max(mx);
+            const float s = mx > 0.0f ? mx / 127.0f : 1.0f;
+            if (lane == 0) sa[r] = s;
+            for (int c0 = 0; c0 < 64 * kb_n; c0 += 256) {
+                float v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int c = c0 + 64 * u + lane;
+                    v[u] = c < K ? xf[r][c] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int c = c0 + 64 * u + lane;
+                    if (c < 64 * kb_n) xq[r][c] = c < K ? quant_i8(v[u], s) : (int8_t)0;
+                }
+            }
+        }
+        lds_barrier();
+        if (!have_cur && wid < ntiles) mlp_load_tile<kMlpMaxKb>(L, wid, lane, cur);
+        for (int t = wid; t < ntiles; t += kMlpWaves) {
+            const int col = 16 * t + row;
+            const int cc = min(col, N - 1);
+            const float w = L.sw[cc];                      // before the tile requested ahead
+            const float bb = L.bias ? L.bias[cc] : 0.0f;
+            const bool more = t + kMlpWaves < ntiles;
+            if (more && !(t == wid && have_ahead))
+                mlp_load_tile<kMlpMaxKb>(L, t + kMlpWaves, lane, ahead);
+            v4i acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int kb = 0; kb < kMlpMaxKb; ++kb) {
+                if (kb < kb_n) {
+                    const v4i a = *reinterpret_cast<const v4i *>(&xq[row][64 * kb + 16 * q]);
+                    // D[m][n]: A = activation rows, B = weight columns
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, cur[kb], acc, 0, 0, 0);
+                }
+            }
+            // lane holds column 16 t + row, rows 4 q .. 4 q + 3; the
+            // reference's order: ((acc * sa[m]) * sw[n]) + bias[n], then ReLU
+            if (col < N) {
+                const int32_t av[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = 4 * q + e;
+                    float v = (float)av[e] * sa[m] * w;
+                    if (L.bias) v = v + bb;
+                    if (relu) v = fmaxf(v, 0.0f);
+                    if (last) {
+                        if (m < mr) y[(r0 + m) * N + col] = v;
+                    } else {
+                        xf[m][col] = v;
+                    }
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (int kb = 0; kb < kMlpMaxKb; ++kb) cur[kb] = ahead[kb];
+            }
+        }
+        lds_barrier();
+        have_cur = have_nxt;
+        have_ahead = false;
+        if (have_nxt) {
+#pragma unroll
+            for (int kb = 0; kb < kMlpPrefetchKb; ++kb) cur[kb] = nxt[kb];
+#pragma unroll
+            for (int kb = kMlpPrefetchKb; kb < kMlpMaxKb; ++kb) cur[kb] = v4i{0, 0, 0, 0};
+        }
+    }
+}
+
+}  // namespace rnn
+
+using namespace rnn;
+
+extern "C" int rnn_w8a8_mlp(const float *x, int64_t m, int nlayers, const int64_t *dims,
+                            const int8_t *const *wq, const float *const *sw,
+                            const float *const *bias, int relu, float *y, void *stream) {
+    RNN_ENTRY();
+    const char *name = "rnn_w8a8_mlp";
+    RNN_REQUIRE(m >= 0, "%s: negative m", name);
+    RNN_REQUIRE(nlayers >= 1 && dims && wq && sw, "%s: need at least one layer", name);
+    RNN_REQUIRE(relu == 0 || relu == 1, "%s: relu must be 0 or 1", name);
+    if (nlayers > kMlpMaxLayers)
+        return set_error(RNN_ERR_UNSUPPORTED, "%s: at most %d layers in one launch (got %d)", name,
+                         kMlpMaxLayers, nlayers);
+    MlpArgs args{};
+    args.nlayers = nlayers;
+    args.relu = relu;
+    for (int l = 0; l < nlayers; ++l) {
+        const int64_t k = dims[l], n = dims[l + 1];
+        RNN_REQUIRE(k > 0 && n > 0, "%s: layer %d has a zero or negative size", name, l);
+        RNN_REQUIRE(wq[l] && sw[l], "%s: layer %d: null weight or scales", name, l);
+        if (k > kMlpMaxDim || n > kMlpMaxDim || k % 16 != 0 || ((uintptr_t)wq[l] & 15) != 0)
+            return set_error(RNN_ERR_UNSUPPORTED,
+                             "%s: layer %d (%lld -> %lld): the one-launch chain needs widths <= "
+                             "%d, in-features %% 16 == 0 and 16-byte aligned weights",
+                             name, l, (long long)k, (long long)n, kMlpMaxDim);
+        args.layer[l] = MlpLayer{wq[l], sw[l], bias ? bias[l] : nullptr, (int)n, (int)k};
+    }
+    if (m == 0) return RNN_OK;
+    RNN_REQUIRE(x && y, "%s: null x or y", name);
+    const int64_t blocks = ceil_div(m, kMlpRows);
+    RNN_REQUIRE(blocks <= 0x7fffffffLL, "%s: m too large", name);
+    w8a8_mlp_kernel<<<(unsigned)blocks, kMlpWaves * 64, 0, as_stream(stream)>>>(x, m, args, y);
+    return check_launch(name);
+}

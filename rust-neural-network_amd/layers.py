@@ -208,7 +208,20 @@ class Int8Model(Module):
                    for w, b in pairs)
 
     def forward(self, x, relu_between=True):
-        """W8A8 through every layer; ReLU after each layer but the last."""
+        """W8A8 through every layer; ReLU after each layer but the last. Chains
+        of up to 4 layers of width <= 1024 run as one launch (rnn_w8a8_mlp,
+        the activation kept in LDS between layers); others launch per layer.
+        Both give the same bits."""
+        try:
+            return H.w8a8_mlp(x.contiguous(), [(l.int8_weight.data, l.int8_weight.scales, l.bias)
+                                               for l in self.layers], relu=relu_between)
+        except H.RnnError as e:
+            if e.status != H.RNN_ERR_UNSUPPORTED:
+                raise
+        return self.forward_per_layer(x, relu_between)
+
+    def forward_per_layer(self, x, relu_between=True):
+        """One quantize + W8A8 GEMM launch pair per layer."""
         for i, layer in enumerate(self.layers):
             x = layer.forward_w8a8(x, relu=relu_between and i + 1 < len(self.layers))
         return x

@@ -85,6 +85,7 @@ SIGNATURES = {
     "rnn_sgemm": ([_INT, _INT, _I64, _I64, _I64, ctypes.c_float, _P, _I64, _P, _I64,
                    ctypes.c_float, _P, _I64, _P], _INT),
     "rnn_relu": ([_P, _I64, _P, _P], _INT),
+    "rnn_w8a8_mlp": ([_P, _I64, _INT, _P, _P, _P, _P, _INT, _P, _P], _INT),
     "rnn_bias_act": ([_P, _P, _I64, _I64, _INT, _P], _INT),
     "rnn_linear_layer": ([_P, _I64, _I64, _P, _I64, _P, _INT, _P, _P], _INT),
 }
@@ -286,6 +287,39 @@ def w8a8_linear(aq, sa, wq, sw, bias=None, relu=False, algo=ALGO_AUTO, want_y=Tr
     _check(load().rnn_w8a8_linear(_ptr(aq), _ptr(sa), _ptr(wq), _ptr(sw), _ptr(bias), m, k, n,
                                   flags, _ptr(y), _ptr(acc), _stream(stream)))
     return y, acc
+
+
+def w8a8_mlp(x, layers, relu=True, y=None, stream=None):
+    """A chain of W8A8 layers in one launch (rnn_w8a8_mlp): `layers` is a list
+    of (wq [n, k] int8, sw [n] f32, bias [n] f32 or None); x [m, k0] f32.
+    Bit-identical to quant_rows_i8 + w8a8_linear per layer, ReLU between
+    layers when `relu`. Raises RnnError (RNN_ERR_UNSUPPORTED) for chains the
+    single launch does not take (more than 4 layers, widths over 1024,
+    in-features not a multiple of 16)."""
+    import torch
+    _dev(x, torch.float32, "x")
+    m, k0 = _dims(x, 2, "x")
+    nl = len(layers)
+    dims = [k0]
+    for i, (wq, sw, b) in enumerate(layers):
+        _dev(wq, torch.int8, f"wq[{i}]"), _dev(sw, torch.float32, f"sw[{i}]")
+        _dev(b, torch.float32, f"bias[{i}]")
+        n, k = _dims(wq, 2, f"wq[{i}]")
+        if k != dims[-1]:
+            raise RnnError(RNN_ERR_INVALID_ARG, f"layer {i} takes {k} features, gets {dims[-1]}")
+        _need(sw, n, f"sw[{i}]"), _need(b, n, f"bias[{i}]")
+        dims.append(n)
+    y = (_out(y, torch.float32, m * dims[-1], "y") if y is not None
+         else _empty((m, dims[-1]), torch.float32, x))
+    d = (ctypes.c_int64 * (nl + 1))(*dims)
+    w = (ctypes.c_void_p * nl)(*[l[0].data_ptr() for l in layers])
+    s_ = (ctypes.c_void_p * nl)(*[l[1].data_ptr() for l in layers])
+    b_ = (ctypes.c_void_p * nl)(*[0 if l[2] is None else l[2].data_ptr() for l in layers])
+    _check(load().rnn_w8a8_mlp(_ptr(x), m, nl, ctypes.cast(d, ctypes.c_void_p),
+                               ctypes.cast(w, ctypes.c_void_p), ctypes.cast(s_, ctypes.c_void_p),
+                               ctypes.cast(b_, ctypes.c_void_p), int(bool(relu)), _ptr(y),
+                               _stream(stream)))
+    return y
 
 
 # ------------------------------------------------------------------ ternary

@@ -89,3 +89,46 @@ def test_ternary_model_from_model(dev):
         h, _ = O.ternary_gemm_i8(aq, sa, O.pack_ternary(tq), ts, params[w_i].shape[0],
                                  None if b_i is None else params[b_i], i < 2)
     np.testing.assert_array_equal(host(model.forward(to_dev(x, dev))), h)
+
+
+@pytest.mark.parametrize("m,dims,relu", [(32, (784, 256, 128, 10), True), (1, (64, 48), False),
+                                         (40, (1024, 1024, 16), True), (17, (32, 80, 112, 96, 5), True),
+                                         (5, (16, 7), True)])
+def test_w8a8_mlp_one_launch_matches_chain(dev, hip, m, dims, relu):
+    """rnn_w8a8_mlp against the oracle chain (per-row quantization + W8A8 +
+    epilogue per layer, ReLU between), bit for bit; rows beyond a multiple of
+    16 and widths that are not multiples of 16 included; the per-layer launches
+    must give the same bits."""
+    params = []
+    for i, (fi, fo) in enumerate(zip(dims[:-1], dims[1:])):
+        params += [W.weights(fo, fi, seed=60 + i), W.weights(1, fo, seed=70 + i)[0]]
+    x = W.activations(m, dims[0], seed=80 + m)
+    layers = []
+    for i in range(len(dims) - 1):
+        wq, sw = O.quant_rows_i8(params[2 * i])
+        layers.append((to_dev(wq, dev), to_dev(sw, dev), to_dev(params[2 * i + 1], dev)))
+    got = host(hip.w8a8_mlp(to_dev(x, dev), layers, relu=relu))
+    h = x
+    for i in range(len(dims) - 1):
+        wq, sw = O.quant_rows_i8(params[2 * i])
+        aq, sa = O.quant_rows_i8(h)
+        h, _ = O.w8a8_linear(aq, sa, wq, sw, params[2 * i + 1], relu and i < len(dims) - 2)
+    np.testing.assert_array_equal(got, h)
+    model = L.Int8Model([L.Int8Linear(L.Int8Weights(w, s, w.shape), b) for w, s, b in layers])
+    np.testing.assert_array_equal(host(model.forward_per_layer(to_dev(x, dev), relu)), h)
+
+
+def test_w8a8_mlp_unsupported_chains_fall_back(dev, hip):
+    w = [W.weights(24, 40, seed=90), W.weights(8, 24, seed=91)]    # 40 % 16 != 0
+    qs = [O.quant_rows_i8(a) for a in w]
+    layers = [(to_dev(q, dev), to_dev(s, dev), None) for q, s in qs]
+    x = W.activations(3, 40, seed=92)
+    with pytest.raises(hip.RnnError) as e:
+        hip.w8a8_mlp(to_dev(x, dev), layers)
+    assert e.value.status == hip.RNN_ERR_UNSUPPORTED
+    model = L.Int8Model([L.Int8Linear(L.Int8Weights(q, s, q.shape), None) for q, s, _ in layers])
+    h = x
+    for i, (q, s) in enumerate(qs):
+        aq, sa = O.quant_rows_i8(h)
+        h, _ = O.w8a8_linear(aq, sa, q, s, None, i == 0)
+    np.testing.assert_array_equal(host(model.forward(to_dev(x, dev))), h)
