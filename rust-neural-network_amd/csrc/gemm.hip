@@ -1607,6 +1607,161 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wl_kernel(
     epi.store_ops(em, n0 + en, (int32_t)sum, eo);
 }
 
+// Decode GEMV over balanced row ranges: workgroup b of G (8 waves, at most
+// one per CU) owns weight rows [b*N/G, (b+1)*N/G), processed as up to TPW
+// 16-row tiles. Its loads are all issued up front, in this order: the
+// activation fragments of each wave's K range (K/8 bytes of rows < 16; rows
+// past M read row M-1 and are zeroed before use), loaded once for all tiles
+// (the per-tile kernels below load them once per tile, as many bytes as the
+// weights at M = 16), the epilogue operands, then every weight byte of every
+// tile, tile by tile, so the row range is in flight from the start. Weights
+// are read through a buffer descriptor that ends at the last
+// row of the range: the rows that pad the last tile to 16 read zeros and
+// fetch nothing. Balanced ranges keep every CU's byte count within one row of
+// the others (16-row tiles dealt out whole leave up to 12% of the CUs'
+// time idle, e.g. 688 tiles over 256 CUs). Each wave takes K/8 of a tile:
+// whole-line weight loads (4 rows x 256 bytes per instruction,
+// non-temporal), regrouped into MFMA fragments through the wave's 4 KiB LDS
+// slice, 256 bytes of each row at a time (16-byte chunk c of row r at c ^ r),
+// 16x16x64 MFMAs against the activation
+// fragments held in registers for all tiles, then the 8 partial tiles are
+// summed through LDS (exact: wrapping int32) and the epilogue runs once per
+// output. Barriers order LDS only, so the later tiles' loads stay in flight
+// while earlier tiles compute. K = 2048 * H bytes (H = 1, 2).
+constexpr int kGlWaves = 8;
+
+__device__ __forceinline__ void lds_only_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int TPW, int H>
+__global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
+    const int8_t *__restrict__ A, const int8_t *__restrict__ W, int64_t M, int64_t N,
+    Epilogue epi) {
+    constexpr int KW = 256 * H;        // K bytes per wave and tile
+    constexpr int K = kGlWaves * KW;   // 2048 or 4096
+    constexpr int KB = KW / 64;        // MFMA k-steps per wave and tile
+    __shared__ __attribute__((aligned(16))) int8_t stage[kGlWaves][16 * 256];
+    __shared__ int32_t part[kGlWaves][16][16];
+    const int tid = threadIdx.x, wid = tid / 64, lane = tid % 64;
+    const int row = lane & 15, q = lane >> 4;
+    // The K slice of wave w. The older wave of each SIMD (waves 0-3) issues
+    // first, so its slices should not be one contiguous half of every row:
+    // with one workgroup per CU, slices are interleaved (0, 2, 4, 6 for waves
+    // 0-3); with several tiles per workgroup, rotated by the workgroup, so
+    // that the CUs' concurrent requests spread over the whole rows. (Measured,
+    // K = 4096, M = 16: N = 4096 6.5 us with slices in wave order, 5.7
+    // interleaved; N = 11008 12.5 in wave order, 11.0 rotated; the barriers
+    // between tiles' loads gave 12.5 -> 11.5 before the rotation.)
+    const int k0 = (TPW == 1 ? 2 * (wid & 3) + (wid >> 2) : (wid + blockIdx.x) & 7) * KW;
+    // (32-bit: the launch keeps N <= 64 rows per CU)
+    const uint32_t r0 = blockIdx.x * (uint32_t)N / gridDim.x;
+    const int nrows = (int)((blockIdx.x + 1) * (uint32_t)N / gridDim.x - r0);
+
+    // 1. activation fragments of this wave's K range (lane: row m, chunk q)
+    v4i a[KB];
+    const int8_t *ap = A + (row < M ? row : M - 1) * (int64_t)K + k0 + 16 * q;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) a[kb] = *reinterpret_cast<const v4i *>(ap + 64 * kb);
+    // 2. epilogue operands of the outputs this thread finishes (one per tile)
+    const int em = (tid / 16) & 15, en = tid % 16;
+    EpiOps eo[TPW];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) eo[i] = epi.load_ops(em, r0 + std::min(16 * i + en, nrows - 1));
+    // 3. every weight byte of the row range; offsets past nrows rows read 0
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(W + (int64_t)r0 * K), 0, nrows * K, 0x00020000);
+    v4i w[TPW][4][H];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+                w[i][g][h] = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                             wr, (16 * i + 4 * g + q) * K + k0 + 256 * h + 16 * row, 0, 2 /* nt */));
+        // tile-major issue: a SIMD issues its older wave's loads first, so
+        // without this barrier the CU would request waves 0-3's bytes of
+        // every tile before waves 4-7's bytes of the first
+        if (i + 1 < TPW) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // keep every load above ahead of the first wait
+    __builtin_amdgcn_sched_barrier(0);
+
+    const v4i zero = {0, 0, 0, 0};
+    int8_t *st = stage[wid];
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+        // (no early exit for a tile past the range: it multiplies zeros and
+        // stores nothing. A branch here would let the compiler sink the
+        // weight loads behind it, out of the prologue.)
+        // regroup: lane (q, row) holds row 4g + q, chunk 16h + row of this
+        // wave's K range; stored at (chunk - 16h) ^ row
+        // 256 bytes of each row at a time (4 KiB per wave); one wave's LDS
+        // operations complete in order, so no barrier is needed between the
+        // writes, the reads and the next half's writes
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int rw = 4 * g + q;
+                *reinterpret_cast<v4i *>(st + rw * 256 + 16 * (row ^ rw)) = w[i][g][h];
+            }
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const int ch = 4 * kb + q;
+                const v4i b = *reinterpret_cast<const v4i *>(st + row * 256 + 16 * (ch ^ row));
+                const v4i af = row < M ? a[4 * h + kb] : zero;  // rows past M are zero
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, b, acc, 0, 0, 0);
+            }
+        }
+        part[wid][4 * q + 0][row] = acc.x;
+        part[wid][4 * q + 1][row] = acc.y;
+        part[wid][4 * q + 2][row] = acc.z;
+        part[wid][4 * q + 3][row] = acc.w;
+        lds_only_barrier();
+        if (tid < 256 && 16 * i + en < nrows) {
+            uint32_t sum = 0;
+#pragma unroll
+            for (int v = 0; v < kGlWaves; ++v) sum += (uint32_t)part[v][em][en];
+            epi.store_ops(em, r0 + 16 * i + en, (int32_t)sum, eo[i]);
+        }
+        lds_only_barrier();  // part is rewritten by the next tile
+    }
+}
+
+template <int H>
+static bool launch_gemv_rows_h(const int8_t *A, const int8_t *W, int64_t M, int64_t N, int grid,
+                               int tpw, const Epilogue &epi, hipStream_t st) {
+    switch (tpw) {
+    case 1: gemv_rows_kernel<1, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
+    case 2: gemv_rows_kernel<2, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
+    case 3: gemv_rows_kernel<3, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
+    case 4: gemv_rows_kernel<4, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
+    default: return false;
+    }
+}
+
+// The balanced-row GEMV for M <= 16, K in {2048, 4096} and at most 64 rows
+// per CU; false when the shape is outside that.
+static bool launch_gemv_rows(const int8_t *A, const int8_t *W, int64_t M, int64_t N, int64_t K,
+                             const Epilogue &epi, hipStream_t st) {
+    if (M < 1 || M > 16 || (K != 2048 && K != 4096)) return false;
+    const int64_t grid = std::min<int64_t>(device_cu_count(), ceil_div(N, 16));
+    const int64_t tpw = ceil_div(ceil_div(N, grid), 16);  // tiles of the largest range
+    if (tpw > 4 || N * grid >= (int64_t(1) << 32)) return false;
+    return K == 4096 ? launch_gemv_rows_h<2>(A, W, M, N, (int)grid, (int)tpw, epi, st)
+                     : launch_gemv_rows_h<1>(A, W, M, N, (int)grid, (int)tpw, epi, st);
+}
+
 // ------------------------------------------------------------ igemm packing
 // B i8 [K,N] -> B^T [N,Kp] through a 64x64 LDS tile (zero pad k >= K).
 __global__ __launch_bounds__(256) void transpose_b_kernel(const int8_t *__restrict__ b, int64_t K,
@@ -1785,7 +1940,17 @@ static int launch_gemv(const int8_t *A, const int8_t *W, int64_t M, int64_t N, i
     // against fragment-layout activation loads, K = 4096: M = 8 5.19 vs
     // 6.04 us (N 4096), 10.17 vs 11.31 (N 11008); M = 16 6.21 vs 6.75
     // (N 4096), 14.96 vs 13.57 (N 11008, 688 workgroups: not taken).
+    //
+    // The balanced-row kernel (activations loaded once per workgroup) takes
+    // M > 8, and M <= 4 while the rows fit one tile per CU. Measured against
+    // the kernels below, K = 4096 (us): M = 16 5.84 vs 6.18 (N 4096), 11.03
+    // vs 13.59 (N 11008), 13.79 vs 16.97 (N 14336); M = 1 4.97 vs 5.19
+    // (N 4096); not taken: M = 1 10.02 vs 9.15 and M = 8 10.34 vs 10.15
+    // (N 11008), M = 8 5.26 vs 5.19 (N 4096).
     const unsigned wgs = (unsigned)ceil_div(N, 16);
+    if ((M > 8 || (M <= 4 && (int64_t)wgs <= device_cu_count())) &&
+        launch_gemv_rows(A, W, M, N, K, epi, st))
+        return check_launch(name);
     if (K % 4096 == 0 && M <= 4)
         gemv_wl_kernel<4, 4><<<wgs, 256, 0, st>>>(A, W, M, N, K, epi);
     else if (K % 4096 == 0 && M <= 8)

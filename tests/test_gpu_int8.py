@@ -112,7 +112,8 @@ def test_igemm_lcg_shapes(dev, hip, shape):
     assert np.array_equal(got, O.igemm_scalar(a, b, m, k, n))
 
 
-@pytest.mark.parametrize("m,k,n", [(512, 512, 512), (17, 300, 1000), (300, 4096, 129)])
+@pytest.mark.parametrize("m,k,n", [(512, 512, 512), (17, 300, 1000), (300, 4096, 129),
+                                   (7, 2048, 300), (16, 4096, 5000)])
 def test_igemm_full_u8_range(dev, hip, m, k, n):
     # benches/core_ops.rs:152-153 inputs: a = i % 251 (u8), b = i % 255 (as i8)
     a = (np.arange(m * k) % 251).astype(np.uint8).reshape(m, k)
@@ -236,6 +237,28 @@ def test_w8a8_gemv_whole_line_variants(dev, hip, m, k, n):
     accumulator-only output (no scales) -- int32 and fp32 bit-exact against
     the oracle."""
     aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=7 * m + n, outliers=0.01)
+    ye, acce = O.w8a8_linear(aq, sa, wq, sw, bias, True)
+    d = [to_dev(a, dev) for a in (aq, sa, wq, sw, bias)]
+    y, acc = hip.w8a8_linear(*d, relu=True, want_acc=True)
+    assert np.array_equal(host(acc), acce)
+    assert_f32_equal(host(y), ye)
+    _, acc2 = hip.w8a8_linear(d[0], None, d[2], None, None, want_y=False, want_acc=True)
+    assert np.array_equal(host(acc2), acce)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 4100), (3, 2048, 11008), (5, 4096, 14336),
+                                   (8, 2048, 16), (9, 4096, 4096), (16, 4096, 12289),
+                                   (16, 2048, 7), (13, 4096, 16400), (4, 4096, 1), (2, 4096, 300),
+                                   (11, 2048, 16383)])
+def test_w8a8_gemv_balanced_rows(dev, hip, m, k, n):
+    """The balanced-row GEMV (M <= 16, K = 2048 or 4096, up to 64 rows per
+    workgroup on a 256-CU part): 1-4 tiles per workgroup, row ranges that are
+    not multiples of 16 (the last tile padded with zero rows read past the
+    range's buffer descriptor), fewer rows than CUs, rows past M, and a shape
+    with more than 64 rows per CU (the per-tile kernel) -- int32 and fp32
+    bit-exact against the oracle, with bias + ReLU and with the accumulator
+    alone."""
+    aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=5 * m + n + k, outliers=0.01)
     ye, acce = O.w8a8_linear(aq, sa, wq, sw, bias, True)
     d = [to_dev(a, dev) for a in (aq, sa, wq, sw, bias)]
     y, acc = hip.w8a8_linear(*d, relu=True, want_acc=True)
