@@ -35,6 +35,7 @@ METRIC = "W8A8 GEMM TOPS (% int8 MFMA peak); GEMV & RotorQuant GB/s (% HBM peak)
 PEAK_INT8_TOPS = 5033.0   # MI355X dense int8 MFMA (datasheet, no sparsity)
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix
+PEAK_BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 COUNTERS_FILE = os.path.join(ROOT, "profiles", "counters.json")
 PROBE_LIB = os.path.join(ROOT, "rust-neural-network_amd", "librnn_probe.so")
@@ -345,6 +346,16 @@ QT_FORMATS = [("INT4_g128", 3, 128), ("GGUF_Q4_0", 6, 32), ("GGUF_Q8_0", 8, 32),
               ("NF4_g64", 4, 64)]
 
 
+def qt_bf16_path(fmt, k, g):
+    """Whether AUTO takes the bf16 MFMA GEMV for m >= 5 (the conditions of
+    rnn_qt_linear_forward for INT4 / GGUF Q4 / INT8 / GGUF Q8_0 / BF16)."""
+    kinds = {3: 32, 6: 32, 7: 32, 2: 16, 8: 16, 1: 8}   # format -> elements per 16 bytes
+    if fmt not in kinds:
+        return False
+    ep = kinds[fmt]
+    return k % (32 * ep) == 0 and (fmt == 1 or (g % (4 * ep) == 0 and k % g == 0) or g % k == 0)
+
+
 def bench_qt_gemv(H, dev, steps, floor):
     """QuantizedLinear::forward (src/quantize.rs:744-754) at decode shapes:
     the fused GEMV that decodes INT4/GGUF/BF16/NF4 weights in registers (the
@@ -371,16 +382,24 @@ def bench_qt_gemv(H, dev, steps, floor):
             x = gen_f32((m, k), 9, dev)
             y = torch.empty((m, n), dtype=torch.float32, device=dev)
             n_launch = copies * max(1, -(-max(steps, 100) // copies))
+            ws = torch.zeros(H.qt_linear_workspace_size(k, n), dtype=torch.uint8, device=dev)
             ms = graph_timed(lambda i: H.qt_linear_forward(fmt, x, ds[i % copies], ss[i % copies],
-                                                           g, n, y=y), n_launch)
+                                                           g, n, y=y, workspace=ws), n_launch)
             nbytes = wbytes + 4 * m * k + 4 * m * n
             gbs = nbytes / (ms * 1e-3) / 1e9
             ent = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
                    "weight_copies": copies, "launches_timed": 5 * n_launch,
                    "timing": "HIP graph replay, events / launches"}
-            if m >= 5:
+            if m >= 5 and qt_bf16_path(fmt, k, g):
+                # three bf16 MFMAs per product (x split in three parts)
+                tf = 3 * 2.0 * 16 * k * n / (ms * 1e-3) / 1e12
+                ent["kernel"] = "bf16 MFMA GEMV (split x, caller workspace)"
+                ent["TFLOP/s_bf16_mfma"] = round(tf, 2)
+                ent["frac_bf16_mfma_peak"] = round(tf / PEAK_BF16_MFMA_TFLOPS, 4)
+            elif m >= 5:
                 tf = 2.0 * 16 * k * n / (ms * 1e-3) / 1e12
+                ent["kernel"] = "f32 MFMA GEMV"
                 ent["TFLOP/s_f32_mfma"] = round(tf, 2)
                 ent["frac_fp32_mfma_peak"] = round(tf / PEAK_FP32_MFMA_TFLOPS, 4)
             fl = _floor(floor, ds, nb, n_launch)

@@ -47,6 +47,7 @@ enum rnn_status {
 #define RNN_ALGO_GEMV 0x20u         /* force the skinny GEMV (m <= 16)        */
 #define RNN_ALGO_TILED_DMA 0x30u    /* force the LDS-DMA pipelined big-tile GEMM (k % 128 == 0, n % 4 == 0) */
 #define RNN_ALGO_GEMV_MFMA 0x40u    /* rnn_qt_linear_forward: force the f32-MFMA GEMV (m <= 16) */
+#define RNN_ALGO_GEMV_BF16 0x50u    /* rnn_qt_linear_forward: force the bf16-MFMA GEMV (m <= 16) */
 #define RNN_ALGO_MASK 0xF0u
 #define RNN_FLAG_TERNARY_MFMA_LAYOUT 0x100u /* rnn_ternary_gemm: codes are in the layout of rnn_ternary_prepack */
 
@@ -316,9 +317,16 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
  * in_f, and 16-byte aligned x and data, a fused GEMV that decodes the codes
  * in registers (NF4 and NVFP4 through a 16-entry table; weights read once):
  * for m >= 5 with in_f a multiple of 512 (4-bit), 256 (8-bit) or 128
- * (16-bit) the GEMV on f32 MFMA that takes all m rows at once
- * (RNN_ALGO_GEMV_MFMA forces it), else the VALU GEMV (m <= 4, or per 4 rows);
- * otherwise dequantize
+ * (16-bit) a GEMV on MFMA that takes all m rows at once: for INT4, GGUF Q4,
+ * INT8, GGUF Q8_0 and BF16 weights whose groups are multiples of 128 (4-bit),
+ * 64 (8-bit) elements dividing in_f (or whole rows), with in_f a multiple of
+ * 1024 (4-bit), 512 (8-bit) or 256 (bf16), the bf16 MFMA GEMV (x split
+ * exactly into three bf16 parts in registers, codes exact in bf16, each
+ * group's sum scaled once, K split over up to 8 workgroups whose partial
+ * sums are added in a fixed order in stream-ordered scratch;
+ * RNN_ALGO_GEMV_BF16 forces it), else
+ * the f32 MFMA GEMV (RNN_ALGO_GEMV_MFMA forces it); else the VALU GEMV
+ * (m <= 4, or per 4 rows); otherwise dequantize
  * into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV forces the
  * former (error if it does not fit), RNN_ALGO_TILED the latter. f32 sums in
  * the kernel's own order: within the rnn_sgemm rounding bound of the
@@ -328,6 +336,23 @@ int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,
                           const float *scales, int64_t n_scales, int64_t group,
                           int64_t out_f, const float *bias, float *y,
                           unsigned flags, void *stream);
+
+/* rnn_qt_linear_forward with caller-provided scratch for the bf16 MFMA
+ * GEMV's split-K partial sums and counters: `workspace` (16-byte aligned) of
+ * at least rnn_qt_linear_workspace_size(in_f, out_f) bytes, ZEROED before its
+ * first use (every call leaves it reusable), or NULL to let the call
+ * allocate stream-ordered scratch as rnn_qt_linear_forward does. A layer
+ * that holds one workspace keeps allocation out of its forward (and out of
+ * captured graphs). The workspace is written by the call's kernels: calls
+ * that share one must be ordered on one stream. Same reference semantics
+ * (src/quantize.rs:744-754). */
+size_t rnn_qt_linear_workspace_size(int64_t in_f, int64_t out_f);
+int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, int64_t in_f,
+                             const uint8_t *data, int64_t data_bytes,
+                             const float *scales, int64_t n_scales, int64_t group,
+                             int64_t out_f, const float *bias, float *y,
+                             void *workspace, size_t workspace_bytes,
+                             unsigned flags, void *stream);
 
 /* ------------------------------- RotorQuant KV cache + attention (next row) */
 

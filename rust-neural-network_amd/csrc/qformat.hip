@@ -699,6 +699,247 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
     }
 }
 
+// ------------------------------------------------------------ bf16 MFMA GEMV (m up to 16)
+
+// QuantizedLinear::forward for up to 16 rows of x on v_mfma_f32_16x16x32_bf16.
+// Integer codes (INT4 as 16q, INT8) and bf16 weights are exact in bf16, and
+// x = h + m + l splits exactly into three bf16 parts (h = x with the low 16
+// bits cleared, m likewise of x - h, l = x - h - m, which has at most 8
+// significant bits), so each product is exact and the MFMA sums in f32; the
+// sum of a group's products is scaled once by the group's scale. This is the
+// reference's sum of x * (q*s) reassociated, within the same f32 GEMM
+// rounding bound, at 16x the f32 MFMA's rate per MFMA (three of them per
+// product).
+//
+// Each workgroup splits the x it reads in registers. At m = 16, 4 bytes of x
+// per element against half a byte per INT4 weight mean that a CU taking
+// whole rows of W over all of K would read 2.9x as many x bytes as weight
+// bytes (4096 x 11008) and split every element of x. So K is also split, S
+// ways: workgroup (range r, part s) takes the row range r (of R balanced
+// ranges, up to TPW 16-row tiles) over the s-th K part, with 8 waves each
+// taking CPW chunks (4*EP elements) of it (all loads of a one-chunk wave
+// issued up front). Per chunk a lane (q, i) loads, for each tile, the 16-byte
+// piece of its row i at k = c*4EP + q*EP (the EP codes of MFMA steps j = 0..
+// EP/8-1, 8 each) and x[i][the same EP elements] (rows past m read zero
+// through the buffer descriptor), splits x into the A fragments of the
+// chunk's steps, which serve every tile. A chunk's 4*EP elements lie in one
+// group (the host admits groups that are multiples of 4*EP, or whole rows):
+// the chunk's MFMAs sum into a fresh accumulator, which is scaled and added
+// to the tile's total. The 8 waves' totals are summed through LDS; with
+// S > 1 each workgroup stores its partial tile in the workspace and counts
+// itself in, and the last of a range's S workgroups sums the S partials in
+// part order (deterministic) and writes y, then resets the counter to zero.
+// No workgroup waits for another.
+constexpr int kSplitParts = 3;
+
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+    // high halves of two floats -> packed bf16 (lo in bits 0-15)
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// x = h + m + l exactly: h and m are x and x - h with the low 16 bits
+// cleared, l = x - h - m has at most 8 significant bits. Infinities and NaN
+// stay whole in h.
+__device__ __forceinline__ void split3(float x, float &h, float &m, float &l) {
+    h = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
+    const float r = __builtin_isfinite(x) ? x - h : 0.0f;
+    m = __uint_as_float(__float_as_uint(r) & 0xFFFF0000u);
+    l = r - m;
+}
+
+constexpr int kBf16Waves = 8, kBf16MaxParts = 8;
+
+// (waves_per_eu: the launch has one workgroup of 8 waves per CU, so the
+// register budget is that of 2 waves per SIMD; without it the compiler
+// trades the up-front loads for a higher occupancy that is never used.)
+template <int KIND, int TPW, bool ONE, bool SCALED, bool BIAS>
+__global__ __launch_bounds__(kBf16Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void qt_gemv_bf16_kernel(
+    const float *__restrict__ x, int mrows, int64_t K, const uint8_t *__restrict__ data,
+    const float *__restrict__ scales, int64_t ns, uint32_t cpg, uint32_t kg, uint32_t rpg,
+    int64_t N, int S, uint32_t cpw, float *__restrict__ wpart, uint32_t *__restrict__ counters,
+    const float *__restrict__ bias, float *__restrict__ y) {
+    constexpr int EP = Fmt<KIND>::EP;  // elements per 16-byte piece
+    constexpr int JS = EP / 8;         // MFMA steps per chunk
+    constexpr int NW = kBf16Waves;
+    typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+    __shared__ float part[NW][TPW][16][17];
+    __shared__ uint32_t last;
+    // (the wave index through readfirstlane: uniform to the compiler, so the
+    // chunk offsets are scalar and the buffer loads take them as soffset)
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
+    const int i = lane % 16, q = lane / 16;
+    const uint32_t R = gridDim.x / S, rg = blockIdx.x / S, sp = blockIdx.x % S;
+    // (32-bit: the launch keeps N * R < 2^32 and 64 rows < 2^31 bytes)
+    const uint32_t r0 = rg * (uint32_t)N / R;
+    const int nrows = (int)((rg + 1) * (uint32_t)N / R - r0);
+    const uint32_t rowbytes = (uint32_t)(K * 16 / EP);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(data + (int64_t)r0 * rowbytes), 0, (int)(nrows * rowbytes), 0x00020000);
+    // x: rows past mrows read zero (the launch keeps 16 K floats < 2^31 bytes)
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(x), 0, (int)(mrows * K * 4), 0x00020000);
+    const uint32_t xoff = (uint32_t)((i * K + q * EP) * 4);
+    const uint32_t c0 = (sp * NW + wid) * cpw;  // this wave's first chunk
+    // per tile: the lane's byte offset within the range (row 16t + i, piece
+    // q of a chunk) and its row's first scale index
+    uint32_t voff[TPW];
+    int64_t gbase[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        voff[t] = (16 * t + i) * rowbytes + 16 * q;
+        const int64_t n = r0 + std::min(16 * t + i, nrows - 1);
+        gbase[t] = !SCALED ? 0 : (kg ? n * (int64_t)kg : (int64_t)((uint32_t)n / rpg));
+        if (SCALED) gbase[t] = std::min<int64_t>(gbase[t], ns - 1);
+    }
+    struct Chunk {
+        f4v xf[EP / 4];  // x[i][c*4EP + q*EP ..+ EP)
+        v4i w[TPW];
+        float sc[TPW];
+    };
+    auto load = [&](Chunk &ch, uint32_t c) {
+#pragma unroll
+        for (int u = 0; u < EP / 4; ++u)
+            ch.xf[u] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  xr, xoff + 16 * u, c * (4 * EP * 4), 0));
+        // chunk c starts 64 bytes per chunk into every row (4 pieces); the
+        // group of a chunk is uniform (groups hold whole chunks or rows)
+        const uint32_t grp = kg ? c / cpg : 0u;
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            ch.w[t] = __builtin_bit_cast(
+                v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, voff[t], c * 64u, 2 /* nt */));
+            if (SCALED) {
+                const int64_t gi = gbase[t] + grp;  // (a row's groups are in range)
+                ch.sc[t] = scales[gi];
+            }
+        }
+    };
+    f4v tot[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) tot[t] = f4v{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const Chunk &ch) {
+        // the chunk's A fragments: step j takes elements 8j .. 8j+7
+        v4i a[JS][kSplitParts];
+#pragma unroll
+        for (int j = 0; j < JS; ++j)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const f4v &v4 = ch.xf[2 * j + d / 2];
+                float h0, m0, l0, h1, m1, l1;
+                split3(v4[2 * (d % 2)], h0, m0, l0);
+                split3(v4[2 * (d % 2) + 1], h1, m1, l1);
+                a[j][0][d] = (int)bf16_pair(h0, h1);
+                a[j][1][d] = (int)bf16_pair(m0, m1);
+                a[j][2][d] = (int)bf16_pair(l0, l1);
+            }
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            float v[EP];
+            if (KIND != KIND_BF16) decode_piece<KIND>(ch.w[t], v, nullptr);
+            f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < JS; ++j) {
+                v4i b;
+                if (KIND == KIND_BF16) {
+                    b = ch.w[t];  // already 8 bf16
+                } else {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) b[d] = (int)bf16_pair(v[8 * j + 2 * d], v[8 * j + 2 * d + 1]);
+                }
+#pragma unroll
+                for (int p = 0; p < kSplitParts; ++p)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a[j][p]),
+                                                                 __builtin_bit_cast(bf8, b), acc, 0, 0, 0);
+            }
+            if (SCALED) {
+                const float s = KIND == KIND_I4 ? ch.sc[t] * 0.0625f : ch.sc[t];
+                tot[t] = tot[t] + acc * s;
+            } else {
+                tot[t] = tot[t] + acc;
+            }
+        }
+    };
+    if constexpr (ONE) {  // one chunk per wave: every load up front
+        Chunk A;
+        load(A, c0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(A);
+    } else {  // one chunk in flight ahead of the one being computed
+        Chunk A, B;
+        load(A, c0);
+        for (uint32_t c = 0; c < cpw; c += 2) {
+            load(B, c0 + std::min(c + 1, cpw - 1));
+            compute(A);
+            load(A, c0 + std::min(c + 2, cpw - 1));
+            if (c + 1 < cpw) compute(B);
+        }
+    }
+    // lane holds D[m = 4q + r][n = i] of each tile
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[wid][t][4 * q + r][i] = tot[t][r];
+    __syncthreads();
+    // outputs of this workgroup: (tile t, row m, column n), m < mrows
+    if (S == 1) {
+        for (int u = threadIdx.x; u < TPW * 256; u += NW * 64) {
+            const int t = u / 256, m = (u / 16) % 16, n = u % 16;
+            if (m >= mrows || 16 * t + n >= nrows) continue;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) sum += part[w][t][m][n];
+            const int64_t col = r0 + 16 * t + n;
+            if (BIAS) sum = sum + bias[col];
+            y[(int64_t)m * N + col] = sum;
+        }
+        return;
+    }
+    // S > 1: this part's sums into the workspace, [S][16][N]
+    for (int u = threadIdx.x; u < TPW * 256; u += NW * 64) {
+        const int t = u / 256, m = (u / 16) % 16, n = u % 16;
+        if (m >= mrows || 16 * t + n >= nrows) continue;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += part[w][t][m][n];
+        __hip_atomic_store(&wpart[((int64_t)sp * 16 + m) * N + r0 + 16 * t + n], sum,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // The partials are device-scope atomic stores, which write through this
+    // XCD's L2 to the device's coherence point; once this workgroup's stores
+    // have completed (vmcnt 0), it counts itself in. The last workgroup
+    // reads the partials with device-scope atomic loads, from that point.
+    // (A release/acquire fence pair would write back and invalidate the
+    // whole L2 once per workgroup: 6x slower for the whole GEMV.)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(&counters[rg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)S - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int u = threadIdx.x; u < TPW * 256; u += NW * 64) {
+        const int t = u / 256, m = (u / 16) % 16, n = u % 16;
+        if (m >= mrows || 16 * t + n >= nrows) continue;
+        const int64_t col = r0 + 16 * t + n;
+        // all S loads in flight, then summed in part order
+        float pv[kBf16MaxParts];
+#pragma unroll
+        for (int sq = 0; sq < kBf16MaxParts; ++sq)
+            pv[sq] = sq < S ? __hip_atomic_load(&wpart[((int64_t)sq * 16 + m) * N + col],
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : 0.0f;
+        float sum = pv[0];
+#pragma unroll
+        for (int sq = 1; sq < kBf16MaxParts; ++sq)
+            if (sq < S) sum += pv[sq];
+        if (BIAS) sum = sum + bias[col];
+        y[(int64_t)m * N + col] = sum;
+    }
+    if (threadIdx.x == 0)  // ready for the next call
+        __hip_atomic_store(&counters[rg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __global__ void qt_bias_kernel(float *__restrict__ y, int64_t m, int64_t n,
                                const float *__restrict__ bias) {
     const int64_t total = m * n;
@@ -882,6 +1123,112 @@ static void launch_mfma_kind(int kind, const float *x, int mrows, int64_t K, con
     }
 }
 
+// Shape of the bf16 GEMV launch: S K parts, R row ranges, TPW tiles per
+// range, CPW chunks per wave.
+struct Bf16Plan {
+    int S, R, TPW;
+    uint32_t cpw;
+};
+constexpr int kBf16MaxTilesOne = 12, kBf16MaxTiles = 4;
+
+// The largest S (up to 8 for m > 8, else 1) that gives every wave whole
+// chunks and keeps the tiles per range within the register budget; S = 0 if
+// none does. (Splitting K trades the x bytes and x splitting per CU against
+// the partial sums' round trip through memory: measured at 4096 x 11008
+// INT4, m = 16: 18.0 us with S = 4, 19.3 with S = 1; m = 8: 16.8 against 15.5.)
+static Bf16Plan bf16_plan(int64_t M, int64_t K, int64_t N, int ep) {
+    const int64_t nch = K / (4 * ep), cus = device_cu_count();
+    for (int S = M > 8 ? kBf16MaxParts : 1; S >= 1; S /= 2) {
+        if (nch % (S * kBf16Waves) != 0) continue;
+        const uint32_t cpw = (uint32_t)(nch / (S * kBf16Waves));
+        const int tmax = cpw == 1 ? kBf16MaxTilesOne : kBf16MaxTiles;
+        const int64_t R = std::max<int64_t>(std::min<int64_t>(ceil_div(N, 16), std::max<int64_t>(1, cus / S)),
+                                            ceil_div(N, 16 * tmax));
+        const int64_t tpw = ceil_div(ceil_div(N, R), 16);
+        if (tpw > tmax || N * R >= (int64_t(1) << 32) || R * S > 0x7fffffffLL) continue;
+        return {S, (int)R, (int)tpw, cpw};
+    }
+    return {0, 0, 0, 0};
+}
+
+// Workspace (split K): one counter per range, then the parts' sums
+// [S][16][N] -- bounded for any device.
+static size_t bf16_workspace(int64_t N) {
+    return 4 * (size_t)ceil_div(N, 16) + 256 + (size_t)kBf16MaxParts * 16 * N * 4;
+}
+static size_t bf16_counter_bytes(int64_t N) { return 4 * (size_t)ceil_div(N, 16) + 256; }
+
+template <int KIND, int TPW, bool ONE, bool SCALED>
+static void launch_bf16_t(const float *xs, int mrows, int64_t K, const uint8_t *data,
+                          const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
+                          float *y, const Bf16Plan &pl, float *wpart, uint32_t *cnt, hipStream_t st) {
+    constexpr int EP = Fmt<KIND>::EP;
+    const uint32_t kg = !SCALED ? 0u : (K % g == 0 ? (uint32_t)(K / g) : 0u);
+    const uint32_t rpg = !SCALED ? 1u : (kg ? 1u : (uint32_t)(g / K));
+    const uint32_t cpg = kg ? (uint32_t)(g / (4 * EP)) : 1u;  // chunks per group
+    const unsigned grid = (unsigned)(pl.R * pl.S);
+    if (bias)
+        qt_gemv_bf16_kernel<KIND, TPW, ONE, SCALED, true><<<grid, kBf16Waves * 64, 0, st>>>(
+            xs, mrows, K, data, scales, ns, cpg, kg, rpg, N, pl.S, pl.cpw, wpart, cnt, bias, y);
+    else
+        qt_gemv_bf16_kernel<KIND, TPW, ONE, SCALED, false><<<grid, kBf16Waves * 64, 0, st>>>(
+            xs, mrows, K, data, scales, ns, cpg, kg, rpg, N, pl.S, pl.cpw, wpart, cnt, bias, y);
+}
+
+template <int KIND, bool SCALED>
+static void launch_bf16_tpw(const float *xs, int mrows, int64_t K, const uint8_t *data,
+                            const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
+                            float *y, const Bf16Plan &pl, float *wp, uint32_t *cnt, hipStream_t st) {
+#define RNN_BF16_T(T, O) launch_bf16_t<KIND, T, O, SCALED>(xs, mrows, K, data, scales, ns, g, N, bias, y, pl, wp, cnt, st)
+    if (pl.cpw != 1) {
+        switch (pl.TPW) {
+        case 1: RNN_BF16_T(1, false); break;
+        case 2: RNN_BF16_T(2, false); break;
+        case 3: RNN_BF16_T(3, false); break;
+        default: RNN_BF16_T(4, false); break;
+        }
+        return;
+    }
+    switch (pl.TPW) {
+    case 1: RNN_BF16_T(1, true); break;
+    case 2: RNN_BF16_T(2, true); break;
+    case 3: RNN_BF16_T(3, true); break;
+    case 4: RNN_BF16_T(4, true); break;
+    case 5: RNN_BF16_T(5, true); break;
+    case 6: RNN_BF16_T(6, true); break;
+    case 7: RNN_BF16_T(7, true); break;
+    case 8: RNN_BF16_T(8, true); break;
+    case 9: RNN_BF16_T(9, true); break;
+    case 10: RNN_BF16_T(10, true); break;
+    case 11: RNN_BF16_T(11, true); break;
+    default: RNN_BF16_T(12, true); break;
+    }
+#undef RNN_BF16_T
+}
+
+template <int KIND, bool SCALED>
+static int launch_bf16(const float *x, int mrows, int64_t K, const uint8_t *data,
+                       const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
+                       float *y, void *workspace, hipStream_t st, const char *name) {
+    constexpr int EP = Fmt<KIND>::EP;
+    const Bf16Plan pl = bf16_plan(mrows, K, N, EP);
+    void *ws = workspace;
+    if (!ws && pl.S > 1) {
+        // stream-ordered scratch, its counters zeroed (a caller's workspace
+        // starts zeroed and every call leaves its counters at zero)
+        RNN_TRY(check_hip(hipMallocAsync(&ws, bf16_workspace(N), st), name));
+        qt_zero_kernel<<<grid_for(pl.R, 256), 256, 0, st>>>(static_cast<uint32_t *>(ws), pl.R);
+    }
+    uint8_t *base = static_cast<uint8_t *>(ws);
+    uint32_t *cnt = reinterpret_cast<uint32_t *>(base);
+    float *wpart = base ? reinterpret_cast<float *>(base + bf16_counter_bytes(N)) : nullptr;
+    launch_bf16_tpw<KIND, SCALED>(x, mrows, K, data, scales, ns, g, N, bias, y, pl, wpart, cnt, st);
+    const int rc = check_launch(name);
+    if (workspace || !ws) return rc;
+    const int rf = check_hip(hipFreeAsync(ws, st), name);
+    return rc != RNN_OK ? rc : rf;
+}
+
 static int piece_elems(int kind) { return kind4(kind) ? 32 : (kind == KIND_I8 ? 16 : 8); }
 
 // The fused path takes every format: K a multiple of 32, 16-byte aligned x
@@ -900,17 +1247,27 @@ static int gemv_kind(int format) {
     }
 }
 
-extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,
-                                     const uint8_t *data, int64_t data_bytes, const float *scales,
-                                     int64_t n_scales, int64_t group, int64_t out_f,
-                                     const float *bias, float *y, unsigned flags, void *stream) {
+extern "C" size_t rnn_qt_linear_workspace_size(int64_t in_f, int64_t out_f) {
+    return in_f > 0 && out_f > 0 ? bf16_workspace(out_f) : 0;
+}
+
+extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, int64_t in_f,
+                                        const uint8_t *data, int64_t data_bytes,
+                                        const float *scales, int64_t n_scales, int64_t group,
+                                        int64_t out_f, const float *bias, float *y,
+                                        void *workspace, size_t workspace_bytes, unsigned flags,
+                                        void *stream) {
     RNN_ENTRY();
     const char *name = "rnn_qt_linear_forward";
+    RNN_REQUIRE(!workspace || (workspace_bytes >= rnn_qt_linear_workspace_size(in_f, out_f) &&
+                               ((uintptr_t)workspace % 16) == 0),
+                "%s: workspace of %zu bytes (or misaligned), %zu needed", name, workspace_bytes,
+                rnn_qt_linear_workspace_size(in_f, out_f));
     RNN_REQUIRE(m >= 0 && in_f >= 0 && out_f >= 0, "%s: negative size", name);
     RNN_TRY(check_tensor(name, format, data, data_bytes, scales, n_scales, group, out_f * in_f));
     const unsigned algo = flags & RNN_ALGO_MASK;
     RNN_REQUIRE(algo == RNN_ALGO_AUTO || algo == RNN_ALGO_GEMV || algo == RNN_ALGO_TILED ||
-                    algo == RNN_ALGO_GEMV_MFMA,
+                    algo == RNN_ALGO_GEMV_MFMA || algo == RNN_ALGO_GEMV_BF16,
                 "%s: bad algo 0x%x", name, algo);
     if (m == 0 || out_f == 0) return RNN_OK;
     RNN_REQUIRE(y != nullptr && (in_f == 0 || x != nullptr), "%s: null pointer", name);
@@ -931,6 +1288,31 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
     // the MFMA GEMV takes all m <= 16 rows at once; its 4 waves split K in
     // whole chunks of 4 pieces
     const bool fits_mfma = fits && m <= 16 && in_f % (kMfmaWaves * 4 * piece_elems(kind)) == 0;
+    // the bf16 MFMA GEMV: integer codes and bf16 weights, whole chunks of
+    // 4 pieces per group
+    const int ep = kind >= 0 ? piece_elems(kind) : 32;
+    const bool fits_bf16 =
+        fits && m <= 16 && (kind == KIND_I4 || kind == KIND_I8 || kind == KIND_BF16) &&
+        in_f % (kBf16Waves * 4 * ep) == 0 &&
+        (!scaled || (group % (4 * ep) == 0 && in_f % group == 0) || group % in_f == 0) &&
+        bf16_plan(m, in_f, out_f, ep).S > 0 && 64 * in_f * 16 / ep < (int64_t(1) << 31) &&
+        16 * in_f * 4 < (int64_t(1) << 31);
+    if (algo == RNN_ALGO_GEMV_BF16 || (algo == RNN_ALGO_AUTO && m >= 5 && fits_bf16)) {
+        RNN_REQUIRE(fits_bf16, "%s: the bf16 MFMA GEMV needs INT4/Q4/INT8/Q8/BF16 weights, m <= 16, "
+                    "in_f a multiple of %d, a group that is a multiple of %d dividing in_f (or a "
+                    "multiple of in_f), and 16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
+        switch (kind) {
+        case KIND_I4:
+            return launch_bf16<KIND_I4, true>(x, (int)m, in_f, data, scales, n_scales, group, out_f,
+                                              bias, y, workspace, st, name);
+        case KIND_I8:
+            return launch_bf16<KIND_I8, true>(x, (int)m, in_f, data, scales, n_scales, group, out_f,
+                                              bias, y, workspace, st, name);
+        default:
+            return launch_bf16<KIND_BF16, false>(x, (int)m, in_f, data, scales, n_scales, 1, out_f,
+                                                 bias, y, workspace, st, name);
+        }
+    }
     if (algo == RNN_ALGO_GEMV_MFMA || (algo == RNN_ALGO_AUTO && m >= 5 && fits_mfma)) {
         RNN_REQUIRE(fits_mfma, "%s: the MFMA GEMV needs m <= 16, the fused GEMV's conditions and "
                     "in_f a multiple of %d", name, kMfmaWaves * 4 * (kind >= 0 ? piece_elems(kind) : 32));
@@ -991,4 +1373,12 @@ extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int6
     }
     const int rf = check_hip(hipFreeAsync(w, st), name);
     return rc != RNN_OK ? rc : rf;
+}
+
+extern "C" int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,
+                                     const uint8_t *data, int64_t data_bytes, const float *scales,
+                                     int64_t n_scales, int64_t group, int64_t out_f,
+                                     const float *bias, float *y, unsigned flags, void *stream) {
+    return rnn_qt_linear_forward_ws(format, x, m, in_f, data, data_bytes, scales, n_scales, group,
+                                    out_f, bias, y, nullptr, 0, flags, stream);
 }

@@ -444,6 +444,7 @@ class QuantizedLinear(Module):
     def __init__(self, weight, bias, in_features, out_features):
         self.weight, self.bias = weight, bias
         self.in_features, self.out_features = in_features, out_features
+        self._workspace = None  # the bf16 MFMA GEMV's split x, made on first use
 
     @classmethod
     def from_linear(cls, weight, bias, fmt, group_size):
@@ -452,10 +453,18 @@ class QuantizedLinear(Module):
                    weight.shape[0])
 
     def forward(self, x):
-        """QuantizedLinear::forward (src/quantize.rs:744-754)."""
+        """QuantizedLinear::forward (src/quantize.rs:744-754). The layer keeps
+        one workspace for the GEMV, so a forward allocates nothing but its
+        output (forwards of one layer are ordered on the current stream)."""
+        import torch
         w = self.weight
+        if self._workspace is None:
+            self._workspace = torch.zeros(H.qt_linear_workspace_size(self.in_features,
+                                                                     self.out_features),
+                                          dtype=torch.uint8, device=w.data.device)
         return H.qt_linear_forward(w.format, x.reshape(-1, self.in_features).contiguous(),
-                                   w.data, w.scales, w.group_size, self.out_features, self.bias)
+                                   w.data, w.scales, w.group_size, self.out_features, self.bias,
+                                   workspace=self._workspace)
 
     def parameters(self):
         """The bias (the quantized weight is frozen, not an f32 tensor)."""

@@ -27,6 +27,7 @@ ALGO_TILED = 0x10
 ALGO_GEMV = 0x20
 ALGO_TILED_DMA = 0x30
 ALGO_GEMV_MFMA = 0x40
+ALGO_GEMV_BF16 = 0x50
 FLAG_TERNARY_MFMA_LAYOUT = 0x100
 
 TERNARY_ROWS = 0
@@ -78,6 +79,9 @@ SIGNATURES = {
     "rnn_qt_dequantize": ([_INT, _P, _I64, _P, _I64, _I64, _I64, _P, _P], _INT),
     "rnn_qt_linear_forward": ([_INT, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P,
                                _UINT, _P], _INT),
+    "rnn_qt_linear_workspace_size": ([_I64, _I64], ctypes.c_size_t),
+    "rnn_qt_linear_forward_ws": ([_INT, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P,
+                                  _P, ctypes.c_size_t, _UINT, _P], _INT),
     "rnn_rotorquant_kv_page_elems": ([_I64, _I64, _I64, _P, _P], _INT),
     "rnn_rotorquant_kv_pack": ([_P, _P, _I64, _I64, _I64, _INT, _INT, _P, _P, _P], _INT),
     "rnn_rotorquant_kv_attention": ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64,
@@ -566,18 +570,28 @@ def qt_dequantize(fmt, data, scales, group, n, stream=None):
     return out
 
 
+def qt_linear_workspace_size(in_f, out_f) -> int:
+    return int(load().rnn_qt_linear_workspace_size(in_f, out_f))
+
+
 def qt_linear_forward(fmt, x, data, scales, group, out_f, bias=None, algo=ALGO_AUTO, y=None,
-                      stream=None):
-    """QuantizedLinear::forward (src/quantize.rs:744-754): x [m, in] -> y [m, out]."""
+                      stream=None, workspace=None):
+    """QuantizedLinear::forward (src/quantize.rs:744-754): x [m, in] -> y [m, out].
+    `workspace`: a zeroed device byte tensor of at least
+    qt_linear_workspace_size(in, out) bytes for the bf16 MFMA GEMV's scratch
+    (else the call allocates); calls leave it reusable."""
     import torch
     _dev(x, torch.float32, "x"), _dev(data, torch.uint8, "data")
     _dev(scales, torch.float32, "scales"), _dev(bias, torch.float32, "bias")
+    _dev(workspace, torch.uint8, "workspace")
     m, in_f = _dims(x, 2, "x")
     _need(bias, out_f, "bias")
     y = _out(y, torch.float32, m * out_f, "y") if y is not None else _empty((m, out_f), torch.float32, x)
-    _check(load().rnn_qt_linear_forward(fmt, _ptr(x), m, in_f, _ptr(data), data.numel(),
-                                        _ptr(scales), scales.numel(), group, out_f, _ptr(bias),
-                                        _ptr(y), algo, _stream(stream)))
+    ws_bytes = 0 if workspace is None else workspace.numel()
+    _check(load().rnn_qt_linear_forward_ws(fmt, _ptr(x), m, in_f, _ptr(data), data.numel(),
+                                           _ptr(scales), scales.numel(), group, out_f, _ptr(bias),
+                                           _ptr(y), _ptr(workspace), ws_bytes, algo,
+                                           _stream(stream)))
     return y
 
 

@@ -141,6 +141,17 @@ def gemm_check(got, x, wdeq, bias):
     assert np.all(err <= lim), f"max err {err.max():.3g}, worst excess {(err - lim).max():.3g}"
 
 
+def bf16_gemv_fits(fmt, m, k, g):
+    """The bf16 MFMA GEMV's conditions: integer codes or bf16 weights, whole
+    chunks of 4 pieces for each of 8 waves, groups of whole chunks."""
+    if fmt not in (O.QF_INT4, O.QF_GGUF_Q4, O.QF_GGUF_Q4K, O.QF_INT8, O.QF_GGUF_Q8, O.QF_BF16):
+        return False
+    ep = 32 if O.QF_BITS[fmt] == 4 else (16 if O.QF_BITS[fmt] == 8 else 8)
+    grouped = fmt != O.QF_BF16
+    return (m <= 16 and k % (32 * ep) == 0 and
+            (not grouped or (g % (4 * ep) == 0 and k % g == 0) or g % k == 0))
+
+
 @pytest.mark.parametrize("fmt", GEMV_FMTS, ids=[O.QF_NAMES[f] for f in GEMV_FMTS])
 @pytest.mark.parametrize("m,k,n,gs", [(1, 4096, 1000, 128), (3, 2048, 257, 32), (4, 64, 9, 64),
                                       (8, 4096, 512, 32), (16, 2080, 130, 32), (2, 6144, 40, 0),
@@ -161,11 +172,80 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
         bd = None if bias is None else to_dev(bias, dev)
         ep = 32 if O.QF_BITS[fmt] == 4 else (16 if O.QF_BITS[fmt] == 8 else 8)
         algos = [hip.ALGO_GEMV, hip.ALGO_TILED] + ([hip.ALGO_GEMV_MFMA] if k % (16 * ep) == 0 else [])
+        if bf16_gemv_fits(fmt, m, k, g):
+            algos.append(hip.ALGO_GEMV_BF16)
         for algo in algos:
             y = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd, algo=algo))
             gemm_check(y, x, wdeq, bias)
         auto = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd))
         gemm_check(auto, x, wdeq, bias)
+
+
+@pytest.mark.parametrize("fmt,gs", [(O.QF_INT4, 128), (O.QF_INT4, 0), (O.QF_INT8, 64),
+                                    (O.QF_INT8, 4096), (O.QF_BF16, 0), (O.QF_INT4, 512)],
+                         ids=["INT4-g128", "INT4-tensor", "INT8-g64", "INT8-rows", "BF16", "INT4-g512"])
+@pytest.mark.parametrize("m,k,n", [(5, 4096, 4096), (16, 4096, 5000), (9, 2048, 11008),
+                                   (16, 4096, 16000), (12, 1024, 20000), (7, 4096, 30),
+                                   (16, 2048, 1)])
+def test_linear_forward_bf16_gemv(dev, hip, fmt, gs, m, k, n):
+    """The bf16 MFMA GEMV (x split into three bf16 parts, codes exact in
+    bf16, one scale per group sum, K split over 1-8 workgroups): 1-12 row
+    tiles per range, one or several chunks per wave, row ranges that are not
+    multiples of 16, fewer rows than CUs, rows of x past m; with and without
+    bias, forced, with the caller's workspace (bit-identical, and the same
+    counters reused) and as AUTO picks it, within the GEMM rounding bound; x
+    with outlier channels and tiny values."""
+    rng = np.random.default_rng(m * 7 + k + n + gs)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[:, :7] *= 20.0
+    x[0, 7:15] = np.float32(3e-30)
+    b = rng.standard_normal(n).astype(np.float32)
+    d, s, g = O.qt_quantize(fmt, w, gs)
+    assert bf16_gemv_fits(fmt, m, k, g)
+    wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
+    dd, sd, xd = to_dev(d, dev), to_dev(s if s.size else np.zeros(1, np.float32), dev), to_dev(x, dev)
+    import torch
+    ws = torch.zeros(hip.qt_linear_workspace_size(k, n), dtype=torch.uint8, device=dev)
+    for bias in (None, b):
+        bd = None if bias is None else to_dev(bias, dev)
+        y = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd, algo=hip.ALGO_GEMV_BF16))
+        gemm_check(y, x, wdeq, bias)
+        y2 = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd, algo=hip.ALGO_GEMV_BF16,
+                                        workspace=ws))
+        assert np.array_equal(y2, y)        # same kernels, caller's scratch
+    auto = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, to_dev(b, dev)))
+    gemm_check(auto, x, wdeq, b)
+    # the same workspace for a second x: no partial sum of the first call
+    # may survive into the second
+    x2 = (rng.standard_normal((m, k)) * 3.0).astype(np.float32)
+    y3 = host(hip.qt_linear_forward(fmt, to_dev(x2, dev), dd, sd, g, n, algo=hip.ALGO_GEMV_BF16,
+                                    workspace=ws))
+    gemm_check(y3, x2, wdeq, None)
+
+
+def test_linear_forward_bf16_gemv_rejects(dev, hip):
+    """Forced bf16 GEMV outside its conditions: NF4 codes, a group of 32
+    (GGUF Q4_0), m = 17; and a workspace one 16-byte step too small -- an
+    RnnError, no launch."""
+    rng = np.random.default_rng(3)
+    n, k = 64, 512
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    for fmt, gs, m in ((O.QF_NF4, 128, 8), (O.QF_GGUF_Q4, 32, 8), (O.QF_INT4, 128, 17)):
+        d, s, g = O.qt_quantize(fmt, w, gs)
+        x = to_dev(rng.standard_normal((m, k)).astype(np.float32), dev)
+        with pytest.raises(hip.RnnError) as e:
+            hip.qt_linear_forward(fmt, x, to_dev(d, dev), to_dev(s, dev), g, n,
+                                  algo=hip.ALGO_GEMV_BF16)
+        assert e.value.status == hip.RNN_ERR_INVALID_ARG or e.value.status == hip.RNN_ERR_UNSUPPORTED
+    # a workspace below rnn_qt_linear_workspace_size
+    import torch
+    d, s, g = O.qt_quantize(O.QF_INT4, w, 128)
+    small = torch.empty(hip.qt_linear_workspace_size(k, n) - 16, dtype=torch.uint8, device=dev)
+    with pytest.raises(hip.RnnError) as e:
+        hip.qt_linear_forward(O.QF_INT4, to_dev(rng.standard_normal((8, k)).astype(np.float32), dev),
+                              to_dev(d, dev), to_dev(s, dev), g, n, workspace=small)
+    assert e.value.status == hip.RNN_ERR_INVALID_ARG
 
 
 @pytest.mark.parametrize("fmt", [O.QF_NF4, O.QF_NVFP4, O.QF_INT4],
