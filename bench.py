@@ -346,26 +346,35 @@ QT_FORMATS = [("INT4_g128", 3, 128), ("GGUF_Q4_0", 6, 32), ("GGUF_Q8_0", 8, 32),
               ("NF4_g64", 4, 64)]
 
 
-def qt_bf16_path(fmt, k, g):
-    """Whether AUTO takes the bf16 MFMA GEMV for m >= 5 (the conditions of
-    rnn_qt_linear_forward for INT4 / GGUF Q4 / INT8 / GGUF Q8_0 / BF16)."""
+def qt_bf16_path(fmt, m, k, n, g, cus):
+    """Whether AUTO takes the bf16 MFMA GEMV (the conditions of
+    rnn_qt_linear_forward for INT4 / GGUF Q4 / INT8 / GGUF Q8_0 / BF16: m >= 5,
+    or m = 3, 4 with at least two 16-row tiles of W per CU)."""
     kinds = {3: 32, 6: 32, 7: 32, 2: 16, 8: 16, 1: 8}   # format -> elements per 16 bytes
-    if fmt not in kinds:
+    if fmt not in kinds or m < 3:
         return False
     ep = kinds[fmt]
-    return k % (32 * ep) == 0 and (fmt == 1 or (g % (4 * ep) == 0 and k % g == 0) or g % k == 0)
+    fits = k % (32 * ep) == 0 and (fmt == 1 or (g % (4 * ep) == 0 and k % g == 0) or g % k == 0)
+    if not fits:
+        return False
+    if m >= 5:
+        return True
+    r = max(min(-(-n // 16), cus), -(-n // 64))     # ranges of the m <= 8 plan (S = 1)
+    return -(-(-(-n // r)) // 16) >= 2
 
 
 def bench_qt_gemv(H, dev, steps, floor):
     """QuantizedLinear::forward (src/quantize.rs:744-754) at decode shapes:
     the fused GEMV that decodes INT4/GGUF/BF16/NF4 weights in registers (the
-    VALU GEMV for m <= 4, the f32-MFMA GEMV for m >= 5, as AUTO picks). Bytes per
+    VALU GEMV for small m, the bf16- or f32-MFMA GEMV for more rows, as AUTO
+    picks). Bytes per
     launch = weight codes + f32 scales + x (4 m k) + y (4 m n); weights
-    rotate over copies past the MALL as for the W8A8 GEMV. For m >= 5 the
-    binding roof can be the f32 MFMA rate (2*16*k*n flops with rows padded to
-    16), so that fraction is given beside the HBM one."""
+    rotate over copies past the MALL as for the W8A8 GEMV. For the MFMA GEMVs
+    the MFMA rate they run at (flops with rows padded to 16; three bf16
+    products per MAC for the bf16 kernel) is given beside the HBM fraction."""
     import torch
     out = {}
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     for name, fmt, gs in QT_FORMATS:
         for (m, k, n) in QT_SHAPES:
             if (name in ("BF16", "NF4_g64") and (m, n) != (1, 11008)) or \
@@ -391,7 +400,7 @@ def bench_qt_gemv(H, dev, steps, floor):
                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
                    "weight_copies": copies, "launches_timed": 5 * n_launch,
                    "timing": "HIP graph replay, events / launches"}
-            if m >= 5 and qt_bf16_path(fmt, k, g):
+            if qt_bf16_path(fmt, m, k, n, g, cus):
                 # three bf16 MFMAs per product (x split in three parts)
                 tf = 3 * 2.0 * 16 * k * n / (ms * 1e-3) / 1e12
                 ent["kernel"] = "bf16 MFMA GEMV (split x, caller workspace)"

@@ -1297,7 +1297,12 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
         (!scaled || (group % (4 * ep) == 0 && in_f % group == 0) || group % in_f == 0) &&
         bf16_plan(m, in_f, out_f, ep).S > 0 && 64 * in_f * 16 / ep < (int64_t(1) << 31) &&
         16 * in_f * 4 < (int64_t(1) << 31);
-    if (algo == RNN_ALGO_GEMV_BF16 || (algo == RNN_ALGO_AUTO && m >= 5 && fits_bf16)) {
+    // AUTO takes it for m >= 5, and for m = 3, 4 when every CU gets at least
+    // two row tiles (measured, INT4 g128 x 4096: m = 4 at N = 11008 14.0 us
+    // against 16.3 for the VALU GEMV; at N = 4096 8.6 against 7.4)
+    const bool bf16_auto =
+        fits_bf16 && (m >= 5 || (m >= 3 && bf16_plan(m, in_f, out_f, ep).TPW >= 2));
+    if (algo == RNN_ALGO_GEMV_BF16 || (algo == RNN_ALGO_AUTO && bf16_auto)) {
         RNN_REQUIRE(fits_bf16, "%s: the bf16 MFMA GEMV needs INT4/Q4/INT8/Q8/BF16 weights, m <= 16, "
                     "in_f a multiple of %d, a group that is a multiple of %d dividing in_f (or a "
                     "multiple of in_f), and 16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
