@@ -216,7 +216,10 @@ int rnn_rotor_rotation_matrices(const float *rotors, int64_t n, float *rot9,
  * (RotorQuant::rotors, src/quant.rs:127). bits in [2,8] (qmax = 2^(bits-1)-1).
  * y [rows,dim] receives the reconstruction (may be NULL when codes is set);
  * codes [rows,padded_dim] int8 and scales [rows,padded_dim/3] are optional.
- * A group with max|rv| < 1e-12 is left untouched (:189-191): codes 0, scale 0. */
+ * A group with max|rv| < 1e-12 is left untouched (:189-191): codes 0, scale 0.
+ * Any dim (the reference takes any): up to 2688 the rotation matrices sit in
+ * LDS, beyond that each group's matrix is rebuilt from its rotor in
+ * registers (same expressions, same bits). */
 int rnn_rotorquant_quantize(const float *x, int64_t rows, int64_t dim, int bits,
                             const float *rotors, float *y, int8_t *codes,
                             float *scales, void *stream);

@@ -15,7 +15,8 @@
 namespace rnn {
 
 constexpr int kRqThreads = 256;
-constexpr int kRqMaxGroups = 896;  // dim <= 2688: 42 KiB of rotation matrices in LDS
+constexpr int kRqMaxGroups = 896;  // dim <= 2688: 42 KiB of rotation matrices in LDS (larger
+                                   // dims rebuild them per item)
 
 __global__ void rotation_matrices_kernel(const float *__restrict__ rotors, int64_t n,
                                          float *__restrict__ rot9) {
@@ -90,19 +91,23 @@ __device__ __forceinline__ bool rq_group(const float *R, float qmax, float y_qma
 // indexed by f itself. The rotation matrices sit in LDS at a 48-byte stride
 // (three conflict-free 16-byte reads per group); nothing else is staged.
 // IDX is the element-offset type: uint32_t when rows * padded < 2^32 (item
-// split by a magic multiply), int64_t otherwise.
+// split by a magic multiply), int64_t otherwise. LDSROT = false (dims past
+// the LDS table, 3 * kRqMaxGroups): each item rebuilds its group's matrix from
+// the rotor (the same expressions, so the same bits; the rotors stay in L2).
 constexpr int kRqU = 4;
 constexpr int kRotStride = 12;  // floats per rotation matrix in LDS (9 used)
 
-template <typename IDX>
+template <typename IDX, bool LDSROT = true>
 __global__ __launch_bounds__(kRqThreads) void rotorquant_kernel(
     const float *__restrict__ x, int64_t rows, int dim, int ng, float qmax, float y_qmax,
     uint32_t ng_magic, const float *__restrict__ rotors, float *__restrict__ y,
     int8_t *__restrict__ codes, float *__restrict__ scales) {
     extern __shared__ __attribute__((aligned(16))) float rot[];  // ng * kRotStride floats
-    for (int g = threadIdx.x; g < ng; g += kRqThreads)
-        rotation_matrix(rotors + 4 * g, rot + kRotStride * g);
-    __syncthreads();
+    if (LDSROT) {
+        for (int g = threadIdx.x; g < ng; g += kRqThreads)
+            rotation_matrix(rotors + 4 * g, rot + kRotStride * g);
+        __syncthreads();
+    }
     const IDX padded = (IDX)ng * 3;
     const IDX total = (IDX)rows * (IDX)ng;
     const IDX stride = (IDX)gridDim.x * kRqThreads;
@@ -138,9 +143,13 @@ __global__ __launch_bounds__(kRqThreads) void rotorquant_kernel(
             if (!live[u]) continue;
             const int g = grp[u], e = 3 * g;
             float R[12];
-            *reinterpret_cast<float4 *>(R + 0) = *reinterpret_cast<const float4 *>(rot + kRotStride * g);
-            *reinterpret_cast<float4 *>(R + 4) = *reinterpret_cast<const float4 *>(rot + kRotStride * g + 4);
-            *reinterpret_cast<float4 *>(R + 8) = *reinterpret_cast<const float4 *>(rot + kRotStride * g + 8);
+            if (LDSROT) {
+                *reinterpret_cast<float4 *>(R + 0) = *reinterpret_cast<const float4 *>(rot + kRotStride * g);
+                *reinterpret_cast<float4 *>(R + 4) = *reinterpret_cast<const float4 *>(rot + kRotStride * g + 4);
+                *reinterpret_cast<float4 *>(R + 8) = *reinterpret_cast<const float4 *>(rot + kRotStride * g + 8);
+            } else {
+                rotation_matrix(rotors + 4 * g, R);
+            }
             float scale = 0.0f, q[3] = {0.0f, 0.0f, 0.0f};
             rq_group(R, qmax, y_qmax, v[u][0], v[u][1], v[u][2], scale, q);
             if (codes) {
@@ -256,20 +265,26 @@ __global__ __launch_bounds__(kRqThreads) void rotorquant_tile_kernel(
     }
 }
 
-// Reconstruction from codes: one thread per (row, group).
+// Reconstruction from codes: one thread per (row, group); LDSROT as in
+// rotorquant_kernel.
+template <bool LDSROT = true>
 __global__ __launch_bounds__(kRqThreads) void rotorquant_dequant_kernel(
     const int8_t *__restrict__ codes, const float *__restrict__ scales, int64_t rows, int dim,
     int ng, const float *__restrict__ rotors, float *__restrict__ y) {
     extern __shared__ float rot[];  // ng * 9 floats (dynamic)
-    for (int g = threadIdx.x; g < ng; g += kRqThreads) rotation_matrix(rotors + 4 * g, rot + 9 * g);
-    __syncthreads();
+    if (LDSROT) {
+        for (int g = threadIdx.x; g < ng; g += kRqThreads) rotation_matrix(rotors + 4 * g, rot + 9 * g);
+        __syncthreads();
+    }
     const int padded = 3 * ng;
     const int64_t work = rows * ng;
     for (int64_t f = blockIdx.x * (int64_t)kRqThreads + threadIdx.x; f < work;
          f += (int64_t)gridDim.x * kRqThreads) {
         const int64_t row = f / ng;
         const int g = (int)(f - row * ng);
-        const float *R = rot + 9 * g;
+        float Rg[9];
+        if (!LDSROT) rotation_matrix(rotors + 4 * g, Rg);
+        const float *R = LDSROT ? rot + 9 * g : Rg;
         const float s = scales[f];
         const int8_t *c = codes + row * padded + 3 * g;
         const float rv0 = (float)c[0] * s, rv1 = (float)c[1] * s, rv2 = (float)c[2] * s;
@@ -305,9 +320,7 @@ extern "C" int rnn_rotorquant_quantize(const float *x, int64_t rows, int64_t dim
     RNN_REQUIRE(bits >= 2, "%s: RotorQuant needs at least 2 bits", name);
     RNN_REQUIRE(bits <= (codes ? 8 : 32), "%s: bits %d out of range", name, bits);
     const int64_t ng = (dim + 2) / 3;
-    if (ng > kRqMaxGroups)
-        return set_error(RNN_ERR_UNSUPPORTED, "%s: dim %lld > %d unsupported", name,
-                         (long long)dim, 3 * kRqMaxGroups);
+    RNN_REQUIRE(ng <= 0x7fffffff / 3, "%s: dim %lld too large", name, (long long)dim);
     if (rows == 0) return RNN_OK;
     RNN_REQUIRE(x && rotors, "%s: null input", name);
     RNN_REQUIRE(y || codes || scales, "%s: no output requested", name);
@@ -338,6 +351,15 @@ extern "C" int rnn_rotorquant_quantize(const float *x, int64_t rows, int64_t dim
     // needs, and the per-block rotation-matrix setup amortised over many items.
     const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(total, kRqThreads * kRqU),
                                                       8 * device_cu_count());
+    if (ng > kRqMaxGroups) {  // matrices rebuilt per item, no LDS table
+        if (narrow)
+            rotorquant_kernel<uint32_t, false><<<grid, kRqThreads, 0, st>>>(
+                x, rows, (int)dim, (int)ng, qmax, y_qmax, magic, rotors, y, codes, scales);
+        else
+            rotorquant_kernel<int64_t, false><<<grid, kRqThreads, 0, st>>>(
+                x, rows, (int)dim, (int)ng, qmax, y_qmax, magic, rotors, y, codes, scales);
+        return check_launch(name);
+    }
     const size_t smem = (size_t)ng * kRotStride * sizeof(float);
     if (narrow)
         rotorquant_kernel<uint32_t><<<grid, kRqThreads, smem, st>>>(
@@ -355,15 +377,19 @@ extern "C" int rnn_rotorquant_dequantize(const int8_t *codes, const float *scale
     const char *name = "rnn_rotorquant_dequantize";
     RNN_REQUIRE(rows >= 0 && dim > 0, "%s: bad size", name);
     const int64_t ng = (dim + 2) / 3;
-    if (ng > kRqMaxGroups)
-        return set_error(RNN_ERR_UNSUPPORTED, "%s: dim %lld unsupported", name, (long long)dim);
+    RNN_REQUIRE(ng <= 0x7fffffff / 3, "%s: dim %lld too large", name, (long long)dim);
     if (rows == 0) return RNN_OK;
     RNN_REQUIRE(codes && scales && rotors && y, "%s: null pointer", name);
+    RNN_REQUIRE(rows <= INT64_MAX / ng, "%s: too many rows", name);
     const int64_t work = rows * ng;
     const unsigned grid =
         (unsigned)std::min<int64_t>(ceil_div(work, kRqThreads), 8 * device_cu_count());
-    rotorquant_dequant_kernel<<<grid, kRqThreads, (size_t)ng * 9 * sizeof(float),
-                                as_stream(stream)>>>(codes, scales, rows,
-                                                                          (int)dim, (int)ng, rotors, y);
+    if (ng > kRqMaxGroups)  // matrices rebuilt per item, no LDS table
+        rotorquant_dequant_kernel<false><<<grid, kRqThreads, 0, as_stream(stream)>>>(
+            codes, scales, rows, (int)dim, (int)ng, rotors, y);
+    else
+        rotorquant_dequant_kernel<true><<<grid, kRqThreads, (size_t)ng * 9 * sizeof(float),
+                                          as_stream(stream)>>>(codes, scales, rows, (int)dim,
+                                                               (int)ng, rotors, y);
     return check_launch(name);
 }

@@ -106,8 +106,12 @@ def test_rotorquant_argument_rules(lib):
             H.RNN_ERR_INVALID_ARG, "out of range")
     _status(lib.rnn_rotorquant_quantize(FAKE, 1, 0, 4, FAKE, FAKE, None, None, None),
             H.RNN_ERR_INVALID_ARG, "dim")
-    _status(lib.rnn_rotorquant_quantize(FAKE, 1, 4000, 4, FAKE, FAKE, None, None, None),
-            H.RNN_ERR_UNSUPPORTED, "unsupported")
+    # any dim (past 2688 the kernels rebuild the rotation matrices per item);
+    # a dim whose group count overflows the kernels' index type is refused
+    _status(lib.rnn_rotorquant_quantize(FAKE, 1, 10**10, 4, FAKE, FAKE, None, None, None),
+            H.RNN_ERR_INVALID_ARG, "too large")
+    _status(lib.rnn_rotorquant_dequantize(FAKE, FAKE, 1, 10**10, FAKE, FAKE, None),
+            H.RNN_ERR_INVALID_ARG, "too large")
     _status(lib.rnn_ternary_quantize(FAKE, 2, 2, 7, FAKE, FAKE, None), H.RNN_ERR_INVALID_ARG,
             "bad mode")
 

@@ -23,7 +23,8 @@ def test_rotation_matrices_parity(dev, hip):
 @pytest.mark.parametrize("rows,dim,bits", [(1, 12, 4), (2, 10, 3), (5, 6, 4), (333, 128, 4),
                                            (64, 129, 8), (7, 1, 2), (50, 2, 5), (3, 130, 4),
                                            (4100, 128, 4), (9, 2688, 4), (37, 64, 4),
-                                           (19, 256, 4), (8, 256, 8), (1, 64, 2)])
+                                           (19, 256, 4), (8, 256, 8), (1, 64, 2),
+                                           (5, 3001, 4), (2, 6000, 8)])
 def test_rotorquant_parity(dev, hip, rows, dim, bits):
     x = W.activations(rows, dim, seed=rows + dim)
     x[0, : min(dim, 3)] = 0.0              # an all-zero group (skipped, src/quant.rs:189-191)
