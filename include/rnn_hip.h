@@ -393,7 +393,9 @@ int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, int64_t bh,
  * (rnn_rotorquant_dequantize) of K and V, without forming them: scores are
  * s_g ((R_g q_g) . c_g) summed over groups and V is accumulated in the
  * rotated domain. k_* is a RNN_RQ_PAGE_K page, v_* a RNN_RQ_PAGE_V page.
- * out [bh, nq, dim]; dim <= 192; scale multiplies q.k as in the reference.
+ * out [bh, nq, dim]; any dim whose rotated query (16 bytes per group) fits
+ * the workgroup's LDS beside 13 KB of accumulators (dim <= ~27,000 on
+ * gfx950); scale multiplies q.k as in the reference.
  * f32 sums in the kernel's own order: within a floating-point bound of the
  * reference, not bit for bit. Pages 16-byte aligned. */
 int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t nq,

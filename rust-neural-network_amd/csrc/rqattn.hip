@@ -36,6 +36,8 @@
 #include "common.hpp"
 #include "rotor.hpp"
 
+#include <atomic>
+
 namespace rnn {
 
 constexpr int kTile = 64;
@@ -268,6 +270,155 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
     }
 }
 
+// Head dims past 192 (more than 64 groups). The same online softmax; the
+// scores loop over the K page's 8-group blocks with the rotated query in LDS
+// (16 bytes per group), and V takes the workgroup's range of at most
+// kWideRange groups 64 at a time, a lane per group, each wave's accumulators
+// kept in LDS between tiles. grid: (BH * nq, ceil(ng / kWideRange)); every
+// workgroup of a query scores all groups and accumulates its own range.
+constexpr int kWideRange = 256;
+
+__global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
+    const float *__restrict__ q, const uint16_t *__restrict__ kc, const float *__restrict__ ks,
+    const uint16_t *__restrict__ vc, const float *__restrict__ vs, const float *__restrict__ krot,
+    const float *__restrict__ vrot, int64_t nq, int64_t S, int64_t dim, int64_t ng, int64_t T,
+    float scale, float *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
+    __shared__ __attribute__((aligned(16))) float pb[kAttnWaves][64];
+    __shared__ float mrg[kAttnWaves][2];
+    const int64_t ng4 = (ng + 3) / 4, ng8 = (ng + 7) / 8;
+    float *qs = dyn;               // rotated query: 4 floats per group, 8 * ng8 groups, zero past ng
+    float *acc = dyn + 32 * ng8;   // [kAttnWaves][3 * kWideRange]
+    const int wid = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int64_t bh = blockIdx.x / nq, qi = blockIdx.x % nq;
+    const int64_t g0 = (int64_t)blockIdx.y * kWideRange;
+    const int nr = (int)(ng - g0 < kWideRange ? ng - g0 : kWideRange);  // groups of this range
+    const float *qrow = q + (bh * nq + qi) * dim;
+    for (int64_t g = threadIdx.x; g < 8 * ng8; g += kAttnWaves * 64) {
+        f4v qv = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (g < ng) {
+            float R[9];
+            rotation_matrix(krot + 4 * g, R);
+            float x[3];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) x[c] = 3 * g + c < dim ? qrow[3 * g + c] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) qv[i] = R[3 * i] * x[0] + R[3 * i + 1] * x[1] + R[3 * i + 2] * x[2];
+        }
+        *reinterpret_cast<f4v *>(&qs[4 * g]) = qv;
+    }
+    for (int i = threadIdx.x; i < kAttnWaves * 3 * kWideRange; i += kAttnWaves * 64) acc[i] = 0.0f;
+    __syncthreads();
+    float *aw = acc + wid * 3 * kWideRange;
+    float m = -INFINITY, l = 0.0f;
+    for (int64_t t = wid; t < T; t += kAttnWaves) {
+        const int64_t tile = bh * T + t;
+        // lane = position: score = scale * sum_g s_g (q'_g . c_g), 8 groups a block
+        const uint16_t *pcb = kc + (tile * ng8 * 64 + lane) * 8;
+        const float *psb = ks + (tile * ng4 * 64 + lane) * 4;
+        float sc = 0.0f;
+        for (int64_t b = 0; b < ng8; ++b) {
+            const v4i c = *reinterpret_cast<const v4i *>(pcb + b * 64 * 8);
+            const bool two = 2 * b + 1 < ng4;  // the block's second 4 scales exist
+            const f4v s0 = *reinterpret_cast<const f4v *>(psb + 2 * b * 64 * 4);
+            const f4v s1 = *reinterpret_cast<const f4v *>(psb + (two ? 2 * b + 1 : 2 * b) * 64 * 4);
+#pragma unroll
+            for (int gg = 0; gg < 8; ++gg) {
+                const f4v qv = *reinterpret_cast<const f4v *>(&qs[4 * (8 * b + gg)]);
+                const uint32_t word = (uint32_t)c[gg / 2];
+                const uint32_t w = (gg & 1) ? (word >> 16) : word;
+                float d = qv[0] * rq_code(w, 0);
+                d = __builtin_fmaf(qv[1], rq_code(w, 1), d);
+                d = __builtin_fmaf(qv[2], rq_code(w, 2), d);
+                const float sg = 8 * b + gg < ng ? (gg < 4 ? s0[gg] : s1[gg - 4]) : 0.0f;
+                sc = __builtin_fmaf(sg, d, sc);
+            }
+        }
+        sc *= scale;
+        if (t * kTile + lane >= S) sc = -INFINITY;
+        const float mt = wave_max_f(sc);
+        const float mn = fmaxf(m, mt);
+        const float corr = expf(m - mn);  // 0 on the first tile (m = -inf)
+        const float p = expf(sc - mn);    // 0 for masked positions
+        l = l * corr + p;
+        m = mn;
+        pb[wid][lane] = p;
+        __builtin_amdgcn_wave_barrier();  // one wave's LDS operations complete in order
+        // lane = group of the range: acc_g = acc_g * corr + sum_j p_j s_jg c_jg
+        for (int c0 = 0; c0 < nr; c0 += 64) {
+            const int gl = c0 + lane;
+            if (gl < nr) {
+                RqTileV V;
+                rq_load_v(V, vc, vs, tile, ng, (int)(g0 + gl));
+                float a0 = aw[3 * gl] * corr, a1 = aw[3 * gl + 1] * corr, a2 = aw[3 * gl + 2] * corr;
+#pragma unroll
+                for (int q4 = 0; q4 < 16; ++q4) {
+                    const f4v p4 = *reinterpret_cast<const f4v *>(&pb[wid][4 * q4]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t word = (uint32_t)V.c[q4 / 2][2 * (q4 & 1) + r / 2];
+                        const uint32_t w = (r & 1) ? (word >> 16) : (word & 0xFFFFu);
+                        const float ws = p4[r] * V.s[q4][r];
+                        a0 = __builtin_fmaf(ws, rq_code(w, 0), a0);
+                        a1 = __builtin_fmaf(ws, rq_code(w, 1), a1);
+                        a2 = __builtin_fmaf(ws, rq_code(w, 2), a2);
+                    }
+                }
+                aw[3 * gl] = a0, aw[3 * gl + 1] = a1, aw[3 * gl + 2] = a2;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    // merge the waves: M = max m_w, L = sum l_w e^(m_w - M), A = sum a_w e^(m_w - M)
+    l = wave_sum_f(l);
+    if (lane == 0) mrg[wid][0] = m, mrg[wid][1] = l;
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, mrg[w][0]);
+    float f[kAttnWaves], L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+        const float mw = mrg[w][0];
+        f[w] = (M == -INFINITY || mw == -INFINITY) ? 0.0f : expf(mw - M);
+        L = L + f[w] * mrg[w][1];
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
+    float *orow = out + (bh * nq + qi) * dim;
+    for (int gl = threadIdx.x; gl < nr; gl += kAttnWaves * 64) {
+        float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            A0 = A0 + f[w] * acc[w * 3 * kWideRange + 3 * gl];
+            A1 = A1 + f[w] * acc[w * 3 * kWideRange + 3 * gl + 1];
+            A2 = A2 + f[w] * acc[w * 3 * kWideRange + 3 * gl + 2];
+        }
+        const int64_t g = g0 + gl;
+        float R[9];
+        rotation_matrix(vrot + 4 * g, R);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const float o = (R[c] * A0 + R[3 + c] * A1 + R[6 + c] * A2) * inv;  // R^T A, then * inv
+            if (3 * g + c < dim) orow[3 * g + c] = o;
+        }
+    }
+}
+
+// Largest LDS a workgroup may use on the current device (cached per device).
+static int device_max_lds() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+            n <= 0)
+            n = 65536;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 }  // namespace rnn
 
 using namespace rnn;
@@ -311,8 +462,14 @@ extern "C" int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t n
     RNN_ENTRY();
     const char *name = "rnn_rotorquant_kv_attention";
     RNN_REQUIRE(bh >= 0 && nq >= 0 && seq >= 0 && dim > 0, "%s: bad size", name);
-    RNN_REQUIRE(dim <= 192, "%s: head dim %lld > 192 (at most 64 groups per wave)", name,
-                (long long)dim);
+    const int64_t ngw = ceil_div(dim, 3);
+    // the wide kernel's LDS: the rotated query (16 bytes per group, 8-group
+    // blocks), the accumulators, and the static probabilities and merge rows
+    const int64_t wide_lds = (32 * ceil_div(ngw, 8) + kAttnWaves * 3 * kWideRange) * 4;
+    const int64_t wide_static = kAttnWaves * (64 + 2) * 4;
+    RNN_REQUIRE(ngw <= 64 || wide_lds + wide_static <= device_max_lds(),
+                "%s: head dim %lld needs %lld bytes of LDS (the device has %d)", name,
+                (long long)dim, (long long)(wide_lds + wide_static), device_max_lds());
     if (bh == 0 || nq == 0) return RNN_OK;
     RNN_REQUIRE(q && out && k_rotors && v_rotors, "%s: null pointer", name);
     RNN_REQUIRE(seq == 0 || (k_codes && k_scales && v_codes && v_scales), "%s: null page", name);
@@ -323,7 +480,17 @@ extern "C" int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t n
     const int64_t ng = ceil_div(dim, 3), T = ceil_div(seq, kTile);
     const unsigned grid = (unsigned)(bh * nq);
     hipStream_t st = as_stream(stream);
-    if (ng <= 44)
+    if (ng > 64) {
+        if (wide_lds > 65536)
+            RNN_REQUIRE(hipFuncSetAttribute((const void *)rq_kv_attn_wide_kernel,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)wide_lds) == hipSuccess,
+                        "%s: %lld bytes of dynamic LDS refused", name, (long long)wide_lds);
+        rq_kv_attn_wide_kernel<<<dim3(grid, (unsigned)ceil_div(ng, kWideRange)), kAttnWaves * 64,
+                                 (size_t)wide_lds, st>>>(q, k_codes, k_scales, v_codes, v_scales,
+                                                         k_rotors, v_rotors, nq, seq, dim, ng, T,
+                                                         scale, out);
+    } else if (ng <= 44)
         rq_kv_attn_kernel<11, 6><<<grid, kAttnWaves * 64, 0, st>>>(
             q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, scale,
             out);

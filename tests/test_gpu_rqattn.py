@@ -52,7 +52,13 @@ def make_cache(hip, dev, x, rot, bits, bh, seq, kind):
 @pytest.mark.parametrize("bh,nq,seq,dim,bits", [(2, 1, 300, 128, 4), (3, 2, 64, 128, 4),
                                                 (1, 1, 1, 128, 4), (4, 1, 129, 96, 3),
                                                 (2, 3, 200, 130, 4), (1, 1, 4096, 128, 4),
-                                                (2, 1, 70, 5, 2), (1, 4, 257, 192, 4)])
+                                                (2, 1, 70, 5, 2), (1, 4, 257, 192, 4),
+                                                # past 64 groups: the wide kernel, one range
+                                                (2, 1, 300, 193, 4), (3, 2, 130, 256, 3),
+                                                (1, 1, 4096, 256, 4), (1, 3, 64, 576, 4),
+                                                # several 256-group ranges, and past 64 KB of LDS
+                                                (2, 1, 200, 800, 4), (1, 2, 70, 4096, 2),
+                                                (1, 1, 100, 12000, 4)])
 def test_kv_attention_parity(dev, hip, bh, nq, seq, dim, bits):
     rng = np.random.default_rng(bh * 1000 + seq + dim)
     ng = (dim + 2) // 3
@@ -95,9 +101,11 @@ def test_kv_attention_empty_cache_and_errors(dev, hip):
     rot = to_dev(W.rotors(43, seed=1), dev)
     out = hip.rotorquant_kv_attention(q, (z16, z32), (z16, z32), rot, rot, 0, 1.0)
     assert torch.equal(out, torch.zeros_like(out))          # row_sum 0 -> inv 0 (src/tensor.rs:657)
-    with pytest.raises(hip.RnnError):                       # head dim above 192
-        hip.rotorquant_kv_attention(torch.ones((1, 1, 195), device=dev), (z16, z32), (z16, z32),
-                                    rot, rot, 0, 1.0)
+    big = 10 ** 6                                           # more LDS than a workgroup has
+    rbig = torch.zeros(4 * ((big + 2) // 3), device=dev)
+    with pytest.raises(hip.RnnError, match="LDS"):
+        hip.rotorquant_kv_attention(torch.ones((1, 1, big), device=dev), (z16, z32), (z16, z32),
+                                    rbig, rbig, 0, 1.0)
     codes = torch.zeros((4, 129), dtype=torch.int8, device=dev)
     with pytest.raises(hip.RnnError):                       # page kind must be K or V
         hip.rotorquant_kv_pack(codes, torch.zeros((4, 43), device=dev), 1, 4, 128, 4, 2)
