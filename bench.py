@@ -576,9 +576,11 @@ def bench_rq_attention(H, W, dev, steps):
     K and V, [8, 32, 4096, 128], 4-bit, as pages): one query per (batch,
     head). Algorithmic bytes per position = 6 per group (a 4-bit code triple in
     a u16 and an f32 scale) for K and for V; the K page pads codes to 8 groups
-    and scales to 4, so the bytes it reads are given beside. Beside it, torch's
-    f32 scaled_dot_product_attention over the reconstructed K and V (what a
-    cache without the codes would read), timed the same way, for context."""
+    and scales to 4, so the bytes it reads are given beside. Timed by graph
+    replay, and again at batch 1 (the sequence split). Beside it, torch's f32
+    scaled_dot_product_attention over the reconstructed K and V (what a cache
+    without the codes would read), timed by events around back-to-back calls
+    (each takes far longer than its host call), for context."""
     import torch
     c = W.ROTORQUANT
     b, h, seq, dim, bits = c["batch"], c["heads"], c["seq"], c["head_dim"], c["bits"]
@@ -597,12 +599,21 @@ def bench_rq_attention(H, W, dev, steps):
     q = gen_f32((bh, 1, dim), 13, dev)
     out = torch.empty_like(q)
     scale = 1.0 / dim ** 0.5
-
-    def step():
-        H.rotorquant_kv_attention(q, pages[0], pages[1], rots[0], rots[1], seq, scale, out=out)
-
-    settle(step, 0.1)
-    ms = timed(step, max(steps // 2, 20), 10)
+    ws = torch.empty(max(1, H.rotorquant_kv_attention_workspace_size(bh, 1, seq, dim)),
+                     dtype=torch.uint8, device=dev)
+    ms = graph_timed(lambda i: H.rotorquant_kv_attention(q, pages[0], pages[1], rots[0], rots[1],
+                                                         seq, scale, out=out, workspace=ws), 20)
+    # batch 1 (the first h sequences of the same pages): too few queries to
+    # fill the device, so each sequence is split over several workgroups
+    b1 = h
+    nc1, ns1 = H.rotorquant_kv_page_elems(b1, seq, dim)
+    p1 = [(pg[0][:nc1], pg[1][:ns1]) for pg in pages]
+    q1, out1 = q[:b1], out[:b1]
+    ws1 = torch.empty(max(1, H.rotorquant_kv_attention_workspace_size(b1, 1, seq, dim)),
+                      dtype=torch.uint8, device=dev)
+    ms1 = graph_timed(lambda i: H.rotorquant_kv_attention(q1, p1[0], p1[1], rots[0], rots[1], seq,
+                                                          scale, out=out1, workspace=ws1), 20)
+    nbytes1 = 2 * b1 * seq * 6 * ng + 2 * q1.numel() * 4
     npos = bh * seq
     nbytes = 2 * npos * 6 * ng + 2 * q.numel() * 4
     npos_t = bh * -(-seq // 64) * 64
@@ -618,6 +629,9 @@ def bench_rq_attention(H, W, dev, steps):
     return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
             "bytes": nbytes, "bytes_read_with_padding": read,
             "kernel": "rq_kv_attn_kernel (scores and V in the rotated domain)",
+            "batch1": {"us": round(ms1 * 1e3, 2), "bytes": nbytes1,
+                       "frac_hbm": round(nbytes1 / (ms1 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                       "note": "32 queries: sequence split over workgroups + merge kernel"},
             "f32_kv_sdpa_us": round(ms_f32 * 1e3, 2),
             "f32_kv_bytes": 2 * bh * seq * dim * 4,
             "shape": {"batch": b, "heads": h, "seq": seq, "head_dim": dim, "bits": bits, "nq": 1}}

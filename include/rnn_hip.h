@@ -397,13 +397,35 @@ int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, int64_t bh,
  * the workgroup's LDS beside 13 KB of accumulators (dim <= ~27,000 on
  * gfx950); scale multiplies q.k as in the reference.
  * f32 sums in the kernel's own order: within a floating-point bound of the
- * reference, not bit for bit. Pages 16-byte aligned. */
+ * reference, not bit for bit. Pages 16-byte aligned. When the queries alone
+ * do not fill the device, each query's sequence is split over several
+ * workgroups whose softmax states a second kernel merges; their scratch is
+ * stream-ordered device memory here, or the caller's workspace with
+ * rnn_rotorquant_kv_attention_ws. */
 int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t nq,
                                 const uint16_t *k_codes, const float *k_scales,
                                 const uint16_t *v_codes, const float *v_scales,
                                 const float *k_rotors, const float *v_rotors,
                                 int64_t seq, int64_t dim, float scale, float *out,
                                 void *stream);
+
+/* Bytes of workspace rnn_rotorquant_kv_attention_ws needs for this shape on
+ * the current device (0: the call does not split, no workspace needed).
+ * No counterpart in the reference: the sequence split is this library's. */
+size_t rnn_rotorquant_kv_attention_workspace_size(int64_t bh, int64_t nq, int64_t seq,
+                                                  int64_t dim);
+
+/* rnn_rotorquant_kv_attention (src/tensor.rs:618-672) with the split states
+ * in a caller's workspace of workspace_bytes (at least
+ * rnn_rotorquant_kv_attention_workspace_size; any contents; calls sharing a
+ * workspace must be ordered on one stream). workspace NULL: as
+ * rnn_rotorquant_kv_attention. */
+int rnn_rotorquant_kv_attention_ws(const float *q, int64_t bh, int64_t nq,
+                                   const uint16_t *k_codes, const float *k_scales,
+                                   const uint16_t *v_codes, const float *v_scales,
+                                   const float *k_rotors, const float *v_rotors,
+                                   int64_t seq, int64_t dim, float scale, float *out,
+                                   void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -140,18 +140,31 @@ __device__ __forceinline__ void rq_load_k(RqTileK<NG4, NG8> &t, const uint16_t *
     for (int a = 0; a < NG4; ++a)
         t.s[a] = *reinterpret_cast<const f4v *>(ps + ((tile * ng4 + (a < ng4 ? a : ng4 - 1)) * 64 + lane) * 4);
 #pragma unroll
-    for (int b = 0; b < NG8; ++b)
-        t.c[b] = *reinterpret_cast<const v4i *>(pc + ((tile * ng8 + (b < ng8 ? b : ng8 - 1)) * 64 + lane) * 8);
+    for (int b = 0; b < NG8; ++b) {
+        const uint16_t *p = pc + ((tile * ng8 + (b < ng8 ? b : ng8 - 1)) * 64 + lane) * 8;
+        if (b == NG8 - 1 && 4 * NG4 <= 8 * b + 4) {
+            // only the block's first 4 groups are scored: an 8-byte load, so
+            // that no register of the tile is dead (the compiler would reuse
+            // it and wait for every outstanding load before the write)
+            const u2v h = *reinterpret_cast<const u2v *>(p);
+            t.c[b] = v4i{(int)h.x, (int)h.y, 0, 0};
+        } else {
+            t.c[b] = *reinterpret_cast<const v4i *>(p);
+        }
+    }
 }
 
 
-// grid: BH * nq workgroups of kAttnWaves waves; ng <= 4 * NG4 <= 8 * NG8 <= 64.
+// grid: (BH * nq, splits) workgroups of kAttnWaves waves; ng <= 4 * NG4 <= 8
+// * NG8 <= 64. Split y takes tiles [y * tps, min(T, (y + 1) * tps)); with
+// part != null it writes its unnormalised state (max, sum, rotated
+// accumulators) there for rq_kv_attn_merge_kernel instead of the output.
 template <int NG4, int NG8>
 __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const float *__restrict__ ks,
     const uint16_t *__restrict__ vc, const float *__restrict__ vs, const float *__restrict__ krot,
     const float *__restrict__ vrot, int64_t nq, int64_t S, int64_t dim, int64_t ng, int64_t T,
-    float scale, float *__restrict__ out) {
+    int64_t tps, float scale, float *__restrict__ out, float *__restrict__ part) {
     __shared__ __attribute__((aligned(16))) float qs[4 * 64];  // rotated query, 4 floats per group
     __shared__ __attribute__((aligned(16))) float pb[kAttnWaves][64];
     __shared__ float mrg[kAttnWaves][2 + 3 * 64];
@@ -159,6 +172,19 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
     const int64_t bh = blockIdx.x / nq, qi = blockIdx.x % nq;
     const int g = lane < ng ? lane : (int)ng - 1;  // group lanes past ng mirror the last one
     const bool gact = lane < ng;
+
+    const int64_t seq = bh * T;
+    // this split's tiles [tb, te); the waves take them round-robin. The first
+    // tile's loads are issued before the query is rotated.
+    const int64_t tb = blockIdx.y * tps, te = tb + tps < T ? tb + tps : T;
+    const int64_t nt = wid < te - tb ? (te - tb - wid + kAttnWaves - 1) / kAttnWaves : 0;
+    const int64_t last = tb + wid + (nt - 1) * kAttnWaves;
+    RqTileK<NG4, NG8> K;
+    RqTileV V;
+    if (nt > 0) {
+        rq_load_k<NG4, NG8>(K, kc, ks, seq + tb + wid, ng, lane);
+        rq_load_v(V, vc, vs, seq + tb + wid, ng, g);
+    }
 
     // rotated query q'_g = R_g q_g (zero past dim), published in LDS
     if (wid == 0) {
@@ -179,19 +205,13 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
         qv[3] = 0.0f;
         *reinterpret_cast<f4v *>(&qs[4 * lane]) = qv;
     }
-    __syncthreads();
+    // a barrier over LDS only: the tile loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     float m = -INFINITY, l = 0.0f, a0 = 0.0f, a1 = 0.0f, a2 = 0.0f;
-    const int64_t seq = bh * T;
-    const int64_t nt = wid < T ? (T - wid + kAttnWaves - 1) / kAttnWaves : 0;
-    const int64_t last = wid + (nt - 1) * kAttnWaves;
-    RqTileK<NG4, NG8> K;
-    RqTileV V;
-    if (nt > 0) {
-        rq_load_k<NG4, NG8>(K, kc, ks, seq + wid, ng, lane);
-        rq_load_v(V, vc, vs, seq + wid, ng, g);
-    }
     for (int64_t i = 0; i < nt; ++i) {
-        const int64_t t = wid + i * kAttnWaves;
+        const int64_t t = tb + wid + i * kAttnWaves;
         // the next tile, or this one again at the end (an L2 hit): the loads
         // stay unconditional so that the compiler's waits stay exact
         const int64_t tn = t + kAttnWaves <= last ? t + kAttnWaves : t;
@@ -258,6 +278,12 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
             A2 = A2 + f * mrg[w][4 + 3 * lane];
         }
     }
+    if (part) {  // this split's state, merged by rq_kv_attn_merge_kernel
+        float *pp = part + ((bh * nq + qi) * gridDim.y + blockIdx.y) * (2 + 3 * ng);
+        if (lane == 0) pp[0] = M, pp[1] = L;
+        if (gact) pp[2 + 3 * g] = A0, pp[3 + 3 * g] = A1, pp[4 + 3 * g] = A2;
+        return;
+    }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
     if (!gact) return;
     float R[9];
@@ -274,15 +300,17 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
 // scores loop over the K page's 8-group blocks with the rotated query in LDS
 // (16 bytes per group), and V takes the workgroup's range of at most
 // kWideRange groups 64 at a time, a lane per group, each wave's accumulators
-// kept in LDS between tiles. grid: (BH * nq, ceil(ng / kWideRange)); every
-// workgroup of a query scores all groups and accumulates its own range.
+// kept in LDS between tiles. grid: (BH * nq, ceil(ng / kWideRange), splits);
+// every workgroup of a query scores all groups and accumulates its own range
+// over its split's tiles (as rq_kv_attn_kernel, part != null: the split's
+// state, the first range writing the max and sum).
 constexpr int kWideRange = 256;
 
 __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const float *__restrict__ ks,
     const uint16_t *__restrict__ vc, const float *__restrict__ vs, const float *__restrict__ krot,
     const float *__restrict__ vrot, int64_t nq, int64_t S, int64_t dim, int64_t ng, int64_t T,
-    float scale, float *__restrict__ out) {
+    int64_t tps, float scale, float *__restrict__ out, float *__restrict__ part) {
     extern __shared__ __attribute__((aligned(16))) float dyn[];
     __shared__ __attribute__((aligned(16))) float pb[kAttnWaves][64];
     __shared__ float mrg[kAttnWaves][2];
@@ -311,7 +339,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
     __syncthreads();
     float *aw = acc + wid * 3 * kWideRange;
     float m = -INFINITY, l = 0.0f;
-    for (int64_t t = wid; t < T; t += kAttnWaves) {
+    const int64_t tb = blockIdx.z * tps, te = tb + tps < T ? tb + tps : T;
+    for (int64_t t = tb + wid; t < te; t += kAttnWaves) {
         const int64_t tile = bh * T + t;
         // lane = position: score = scale * sum_g s_g (q'_g . c_g), 8 groups a block
         const uint16_t *pcb = kc + (tile * ng8 * 64 + lane) * 8;
@@ -385,6 +414,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
     float *orow = out + (bh * nq + qi) * dim;
+    float *pp = part ? part + ((bh * nq + qi) * gridDim.z + blockIdx.z) * (2 + 3 * ng) : nullptr;
+    if (pp && blockIdx.y == 0 && threadIdx.x == 0) pp[0] = M, pp[1] = L;
     for (int gl = threadIdx.x; gl < nr; gl += kAttnWaves * 64) {
         float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
 #pragma unroll
@@ -394,6 +425,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
             A2 = A2 + f[w] * acc[w * 3 * kWideRange + 3 * gl + 2];
         }
         const int64_t g = g0 + gl;
+        if (pp) {
+            pp[2 + 3 * g] = A0, pp[3 + 3 * g] = A1, pp[4 + 3 * g] = A2;
+            continue;
+        }
         float R[9];
         rotation_matrix(vrot + 4 * g, R);
 #pragma unroll
@@ -402,6 +437,75 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
             if (3 * g + c < dim) orow[3 * g + c] = o;
         }
     }
+}
+
+// Sequence splits: at most kMaxSplits, each of at least kAttnWaves tiles.
+constexpr int kMaxSplits = 64;
+
+// Merges the splits of one query (a workgroup per query): M = max m_s,
+// L = sum l_s e^(m_s - M), A = sum a_s e^(m_s - M) in split order, then
+// out = R^T A / L as the attention kernels do.
+__global__ __launch_bounds__(256) void rq_kv_attn_merge_kernel(const float *__restrict__ part,
+                                                               int ns, const float *__restrict__ vrot,
+                                                               int64_t dim, int64_t ng,
+                                                               float *__restrict__ out) {
+    __shared__ float fs[kMaxSplits];
+    __shared__ float linv;
+    const int64_t stride = 2 + 3 * ng;
+    const float *pp = part + (int64_t)blockIdx.x * ns * stride;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, pp[s * stride]);
+    if (threadIdx.x < ns) {
+        const float mw = pp[threadIdx.x * stride];
+        fs[threadIdx.x] = (M == -INFINITY || mw == -INFINITY) ? 0.0f : expf(mw - M);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float L = 0.0f;
+        for (int s = 0; s < ns; ++s) L = L + fs[s] * pp[s * stride + 1];
+        linv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
+    }
+    __syncthreads();
+    const float inv = linv;
+    float *orow = out + (int64_t)blockIdx.x * dim;
+    for (int64_t g = threadIdx.x; g < ng; g += 256) {
+        float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
+        for (int s = 0; s < ns; ++s) {
+            const float *a = pp + s * stride + 2 + 3 * g;
+            A0 = A0 + fs[s] * a[0];
+            A1 = A1 + fs[s] * a[1];
+            A2 = A2 + fs[s] * a[2];
+        }
+        float R[9];
+        rotation_matrix(vrot + 4 * g, R);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const float o = (R[c] * A0 + R[3 + c] * A1 + R[6 + c] * A2) * inv;
+            if (3 * g + c < dim) orow[3 * g + c] = o;
+        }
+    }
+}
+
+// Splits of each query's tiles: enough workgroups for the given number per
+// CU, at least kAttnWaves tiles per split, one split when the queries alone
+// fill the device. tps = tiles per split.
+constexpr int kNarrowWgsPerCu = 1, kWideWgsPerCu = 2;
+
+static void attn_splits(int64_t wgs, int64_t T, bool wide, int64_t &ns, int64_t &tps) {
+    const int64_t want = (int64_t)(wide ? kWideWgsPerCu : kNarrowWgsPerCu) * device_cu_count();
+    ns = 1;
+    if (wgs < want && T >= 2 * kAttnWaves)
+        ns = std::min<int64_t>({ceil_div(want, wgs), T / kAttnWaves, kMaxSplits});
+    tps = ceil_div(T, ns);
+    ns = T > 0 ? ceil_div(T, tps) : 1;  // no empty split
+}
+
+static size_t attn_workspace_bytes(int64_t bh, int64_t nq, int64_t seq, int64_t dim) {
+    const int64_t ng = ceil_div(dim, 3), T = ceil_div(seq, kTile);
+    const int64_t wgs = bh * nq * (ng > 64 ? ceil_div(ng, kWideRange) : 1);
+    int64_t ns, tps;
+    attn_splits(wgs, T, ng > 64, ns, tps);
+    return ns > 1 ? (size_t)(bh * nq * ns * (2 + 3 * ng)) * sizeof(float) : 0;
 }
 
 // Largest LDS a workgroup may use on the current device (cached per device).
@@ -453,12 +557,19 @@ extern "C" int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, 
     return check_launch(name);
 }
 
-extern "C" int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t nq,
-                                           const uint16_t *k_codes, const float *k_scales,
-                                           const uint16_t *v_codes, const float *v_scales,
-                                           const float *k_rotors, const float *v_rotors,
-                                           int64_t seq, int64_t dim, float scale, float *out,
-                                           void *stream) {
+extern "C" size_t rnn_rotorquant_kv_attention_workspace_size(int64_t bh, int64_t nq, int64_t seq,
+                                                             int64_t dim) {
+    if (bh <= 0 || nq <= 0 || seq <= 0 || dim <= 0) return 0;
+    return attn_workspace_bytes(bh, nq, seq, dim);
+}
+
+extern "C" int rnn_rotorquant_kv_attention_ws(const float *q, int64_t bh, int64_t nq,
+                                              const uint16_t *k_codes, const float *k_scales,
+                                              const uint16_t *v_codes, const float *v_scales,
+                                              const float *k_rotors, const float *v_rotors,
+                                              int64_t seq, int64_t dim, float scale, float *out,
+                                              void *workspace, size_t workspace_bytes,
+                                              void *stream) {
     RNN_ENTRY();
     const char *name = "rnn_rotorquant_kv_attention";
     RNN_REQUIRE(bh >= 0 && nq >= 0 && seq >= 0 && dim > 0, "%s: bad size", name);
@@ -479,24 +590,57 @@ extern "C" int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t n
     RNN_REQUIRE(bh * nq <= 0x7fffffffLL, "%s: too many queries", name);
     const int64_t ng = ceil_div(dim, 3), T = ceil_div(seq, kTile);
     const unsigned grid = (unsigned)(bh * nq);
+    const int64_t nranges = ng > 64 ? ceil_div(ng, kWideRange) : 1;
+    int64_t ns, tps;
+    attn_splits(bh * nq * nranges, T, ng > 64, ns, tps);
     hipStream_t st = as_stream(stream);
+    // ns > 1: the splits' states go to the workspace (or stream-ordered
+    // scratch) and a merge kernel writes out
+    const size_t need = ns > 1 ? (size_t)(bh * nq * ns * (2 + 3 * ng)) * sizeof(float) : 0;
+    RNN_REQUIRE(!workspace || workspace_bytes >= need,
+                "%s: workspace of %zu bytes, %zu needed (rnn_rotorquant_kv_attention_workspace_size)",
+                name, workspace_bytes, need);
+    if (ng > 64 && wide_lds > 65536)
+        RNN_REQUIRE(hipFuncSetAttribute((const void *)rq_kv_attn_wide_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)wide_lds) == hipSuccess,
+                    "%s: %lld bytes of dynamic LDS refused", name, (long long)wide_lds);
+    void *ws = need ? workspace : nullptr;
+    if (need && !ws) RNN_TRY(check_hip(hipMallocAsync(&ws, need, st), name));
+    float *part = static_cast<float *>(ws);
     if (ng > 64) {
-        if (wide_lds > 65536)
-            RNN_REQUIRE(hipFuncSetAttribute((const void *)rq_kv_attn_wide_kernel,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            (int)wide_lds) == hipSuccess,
-                        "%s: %lld bytes of dynamic LDS refused", name, (long long)wide_lds);
-        rq_kv_attn_wide_kernel<<<dim3(grid, (unsigned)ceil_div(ng, kWideRange)), kAttnWaves * 64,
+        rq_kv_attn_wide_kernel<<<dim3(grid, (unsigned)nranges, (unsigned)ns), kAttnWaves * 64,
                                  (size_t)wide_lds, st>>>(q, k_codes, k_scales, v_codes, v_scales,
                                                          k_rotors, v_rotors, nq, seq, dim, ng, T,
-                                                         scale, out);
-    } else if (ng <= 44)
-        rq_kv_attn_kernel<11, 6><<<grid, kAttnWaves * 64, 0, st>>>(
-            q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, scale,
-            out);
-    else
-        rq_kv_attn_kernel<16, 8><<<grid, kAttnWaves * 64, 0, st>>>(
-            q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, scale,
-            out);
-    return check_launch(name);
+                                                         tps, scale, out, part);
+    } else if (ng <= 44) {
+        rq_kv_attn_kernel<11, 6><<<dim3(grid, (unsigned)ns), kAttnWaves * 64, 0, st>>>(
+            q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, tps,
+            scale, out, part);
+    } else {
+        rq_kv_attn_kernel<16, 8><<<dim3(grid, (unsigned)ns), kAttnWaves * 64, 0, st>>>(
+            q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, tps,
+            scale, out, part);
+    }
+    int rc = check_launch(name);
+    if (rc == RNN_OK && ns > 1) {
+        rq_kv_attn_merge_kernel<<<grid, 256, 0, st>>>(part, (int)ns, v_rotors, dim, ng, out);
+        rc = check_launch(name);
+    }
+    if (ws && ws != workspace) {
+        const int rf = check_hip(hipFreeAsync(ws, st), name);
+        if (rc == RNN_OK) rc = rf;
+    }
+    return rc;
+}
+
+extern "C" int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t nq,
+                                           const uint16_t *k_codes, const float *k_scales,
+                                           const uint16_t *v_codes, const float *v_scales,
+                                           const float *k_rotors, const float *v_rotors,
+                                           int64_t seq, int64_t dim, float scale, float *out,
+                                           void *stream) {
+    return rnn_rotorquant_kv_attention_ws(q, bh, nq, k_codes, k_scales, v_codes, v_scales,
+                                          k_rotors, v_rotors, seq, dim, scale, out, nullptr, 0,
+                                          stream);
 }

@@ -80,6 +80,9 @@ SIGNATURES = {
     "rnn_qt_linear_forward": ([_INT, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P,
                                _UINT, _P], _INT),
     "rnn_qt_linear_workspace_size": ([_I64, _I64], ctypes.c_size_t),
+    "rnn_rotorquant_kv_attention_workspace_size": ([_I64, _I64, _I64, _I64], ctypes.c_size_t),
+    "rnn_rotorquant_kv_attention_ws": ([_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                        ctypes.c_float, _P, _P, ctypes.c_size_t, _P], _INT),
     "rnn_qt_linear_forward_ws": ([_INT, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P,
                                   _P, ctypes.c_size_t, _UINT, _P], _INT),
     "rnn_rotorquant_kv_page_elems": ([_I64, _I64, _I64, _P, _P], _INT),
@@ -625,11 +628,18 @@ def rotorquant_kv_pack(codes, scales, bh, seq, dim, bits, kind, stream=None):
     return pc, ps
 
 
+def rotorquant_kv_attention_workspace_size(bh, nq, seq, dim) -> int:
+    return int(load().rnn_rotorquant_kv_attention_workspace_size(bh, nq, seq, dim))
+
+
 def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, out=None,
-                            stream=None):
+                            stream=None, workspace=None):
     """Tensor::flash_attention (src/tensor.rs:618-672) of q [bh, nq, dim] over
     a K page (RQ_PAGE_K) and a V page (RQ_PAGE_V) of rotorquant_kv_pack.
-    Returns out [bh, nq, dim]."""
+    Returns out [bh, nq, dim]. `workspace`: a device byte tensor of at least
+    rotorquant_kv_attention_workspace_size(bh, nq, seq, dim) bytes for the
+    sequence split's states; on the current stream one is taken from torch's
+    allocator when none is given, on another stream the call allocates."""
     import torch
     _dev(q, torch.float32, "q")
     for t, nm in ((k_page[0], "k codes"), (v_page[0], "v codes")):
@@ -637,6 +647,7 @@ def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, o
     for t, nm in ((k_page[1], "k scales"), (v_page[1], "v scales"), (k_rotors, "k rotors"),
                   (v_rotors, "v rotors")):
         _dev(t, torch.float32, nm)
+    _dev(workspace, torch.uint8, "workspace")
     bh, nq, dim = _dims(q, 3, "q")
     nc, ns = rotorquant_kv_page_elems(bh, seq, dim)
     for t, n_, nm in ((k_page[0], nc, "k codes"), (v_page[0], nc, "v codes"),
@@ -646,8 +657,13 @@ def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, o
     _need(k_rotors, 4 * ng, "k rotors", at_least=True), _need(v_rotors, 4 * ng, "v rotors", at_least=True)
     out = (_out(out, torch.float32, bh * nq * dim, "out") if out is not None
            else _empty((bh, nq, dim), torch.float32, q))
-    _check(load().rnn_rotorquant_kv_attention(_ptr(q), bh, nq, _ptr(k_page[0]), _ptr(k_page[1]),
-                                              _ptr(v_page[0]), _ptr(v_page[1]), _ptr(k_rotors),
-                                              _ptr(v_rotors), seq, dim, float(scale), _ptr(out),
-                                              _stream(stream)))
+    if workspace is None and stream is None:
+        wsb = rotorquant_kv_attention_workspace_size(bh, nq, seq, dim)
+        if wsb:
+            workspace = torch.empty(wsb, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel()
+    _check(load().rnn_rotorquant_kv_attention_ws(_ptr(q), bh, nq, _ptr(k_page[0]), _ptr(k_page[1]),
+                                                 _ptr(v_page[0]), _ptr(v_page[1]), _ptr(k_rotors),
+                                                 _ptr(v_rotors), seq, dim, float(scale), _ptr(out),
+                                                 _ptr(workspace), ws_bytes, _stream(stream)))
     return out

@@ -58,7 +58,11 @@ def make_cache(hip, dev, x, rot, bits, bh, seq, kind):
                                                 (1, 1, 4096, 256, 4), (1, 3, 64, 576, 4),
                                                 # several 256-group ranges, and past 64 KB of LDS
                                                 (2, 1, 200, 800, 4), (1, 2, 70, 4096, 2),
-                                                (1, 1, 100, 12000, 4)])
+                                                (1, 1, 100, 12000, 4),
+                                                # few queries: the sequence split over workgroups
+                                                (1, 1, 1000, 128, 4), (3, 1, 2000, 64, 3),
+                                                (1, 2, 4096, 256, 4), (1, 1, 600, 800, 4),
+                                                (1, 1, 513, 150, 2)])
 def test_kv_attention_parity(dev, hip, bh, nq, seq, dim, bits):
     rng = np.random.default_rng(bh * 1000 + seq + dim)
     ng = (dim + 2) // 3
@@ -112,3 +116,37 @@ def test_kv_attention_empty_cache_and_errors(dev, hip):
     with pytest.raises(hip.RnnError):                       # 8-bit codes do not fit the page
         hip.rotorquant_kv_pack(codes, torch.zeros((4, 43), device=dev), 1, 4, 128, 8,
                                hip.RQ_PAGE_K)
+
+
+def test_kv_attention_split_workspace_and_alloc(dev, hip):
+    """The sequence split (one query, 4096 positions): a caller's workspace,
+    torch's (the wrapper's default) and the library's own stream-ordered
+    scratch (the plain entry point, called through ctypes) give the same
+    bits; a workspace below the size the library asks for is refused."""
+    import ctypes
+    import torch
+    bh, nq, seq, dim = 2, 1, 4096, 128
+    ng = (dim + 2) // 3
+    kp, _ = make_cache(hip, dev, W.activations(bh * seq, dim, seed=21), W.rotors(ng, seed=22), 4,
+                       bh, seq, hip.RQ_PAGE_K)
+    vp, _ = make_cache(hip, dev, W.activations(bh * seq, dim, seed=23), W.rotors(ng, seed=24), 4,
+                       bh, seq, hip.RQ_PAGE_V)
+    krot, vrot = to_dev(W.rotors(ng, seed=22), dev), to_dev(W.rotors(ng, seed=24), dev)
+    q = torch.randn((bh, nq, dim), device=dev)
+    need = hip.rotorquant_kv_attention_workspace_size(bh, nq, seq, dim)
+    assert need > 0                                          # 2 queries do not fill the device
+    ws = torch.full((need,), 0xAB, dtype=torch.uint8, device=dev)   # any contents
+    a = hip.rotorquant_kv_attention(q, kp, vp, krot, vrot, seq, 0.125, workspace=ws)
+    b = hip.rotorquant_kv_attention(q, kp, vp, krot, vrot, seq, 0.125)
+    c = torch.empty_like(a)
+    P = ctypes.c_void_p
+    rc = hip.load().rnn_rotorquant_kv_attention(
+        P(q.data_ptr()), bh, nq, P(kp[0].data_ptr()), P(kp[1].data_ptr()), P(vp[0].data_ptr()),
+        P(vp[1].data_ptr()), P(krot.data_ptr()), P(vrot.data_ptr()), seq, dim, 0.125,
+        P(c.data_ptr()), P(torch.cuda.current_stream().cuda_stream))
+    assert rc == hip.RNN_OK, hip.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(a, c)
+    with pytest.raises(hip.RnnError, match="workspace"):
+        hip.rotorquant_kv_attention(q, kp, vp, krot, vrot, seq, 0.125, workspace=ws[: need - 4])
+    assert hip.rotorquant_kv_attention_workspace_size(1024, 1, seq, dim) == 0  # queries fill it
