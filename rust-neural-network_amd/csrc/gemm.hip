@@ -114,14 +114,21 @@ __device__ __forceinline__ v4i ternary_word_to_i8x16(uint32_t w) {
 // one per byte, and one byte permute maps each code through a 4-entry table
 // (00 -> 0, 01 -> +1, 10 -> -1, 11 -> 0, src/ternary.rs:9-14, :63-75) held in
 // a constant: bytes {0x00, 0x01, 0xFF, 0x00}. Selector values 0-3 pick those
-// bytes, so 16 codes decode in 11 VALU operations with no LDS table.
+// bytes, so 16 codes decode with no LDS table.
+// The codes at bits 2-3 of a byte are used in place, as selectors 0, 4, 8,
+// 12: v_perm_b32 gives src1 byte 0 for 0, src0 byte 0 for 4, the sign of
+// src1 byte 1 replicated for 8, and 0x00 for 12; with src0 = 0x01 and src1
+// byte 1 = 0x80 that is the same table. So a word takes one shift, four
+// masks and four permutes (9 VALU operations).
 constexpr uint32_t kTerPermTable = 0x00FF0100u;
+constexpr uint32_t kTerPermHi0 = 0x00000001u, kTerPermHi1 = 0x00008000u;
 __device__ __forceinline__ v4i ternary_perm_decode(uint32_t w) {
     v4i r;
+    const uint32_t w4 = w >> 4;
     r.x = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, w & 0x03030303u);
-    r.y = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, (w >> 2) & 0x03030303u);
-    r.z = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, (w >> 4) & 0x03030303u);
-    r.w = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, (w >> 6) & 0x03030303u);
+    r.y = (int)__builtin_amdgcn_perm(kTerPermHi0, kTerPermHi1, w & 0x0C0C0C0Cu);
+    r.z = (int)__builtin_amdgcn_perm(kTerPermTable, kTerPermTable, w4 & 0x03030303u);
+    r.w = (int)__builtin_amdgcn_perm(kTerPermHi0, kTerPermHi1, w4 & 0x0C0C0C0Cu);
     return r;
 }
 

@@ -440,42 +440,63 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
 }
 
 // Sequence splits: at most kMaxSplits, each of at least kAttnWaves tiles.
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 16;
 
 // Merges the splits of one query (a workgroup per query): M = max m_s,
 // L = sum l_s e^(m_s - M), A = sum a_s e^(m_s - M) in split order, then
-// out = R^T A / L as the attention kernels do.
+// out = R^T A / L as the attention kernels do. Every load of a thread's first
+// group (the splits' max and sum, and its accumulators in every split) is
+// issued before the one barrier, so the kernel waits on memory once.
 __global__ __launch_bounds__(256) void rq_kv_attn_merge_kernel(const float *__restrict__ part,
                                                                int ns, const float *__restrict__ vrot,
                                                                int64_t dim, int64_t ng,
                                                                float *__restrict__ out) {
-    __shared__ float fs[kMaxSplits];
-    __shared__ float linv;
+    __shared__ float ml[2][kMaxSplits];
     const int64_t stride = 2 + 3 * ng;
     const float *pp = part + (int64_t)blockIdx.x * ns * stride;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, pp[s * stride]);
-    if (threadIdx.x < ns) {
-        const float mw = pp[threadIdx.x * stride];
-        fs[threadIdx.x] = (M == -INFINITY || mw == -INFINITY) ? 0.0f : expf(mw - M);
+    const int tid = threadIdx.x;
+    if (tid < kMaxSplits) {  // (splits past ns are read clamped and not used)
+        const int sc = tid < ns ? tid : ns - 1;
+        ml[0][tid] = pp[sc * stride];
+        ml[1][tid] = pp[sc * stride + 1];
     }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float L = 0.0f;
-        for (int s = 0; s < ns; ++s) L = L + fs[s] * pp[s * stride + 1];
-        linv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
-    }
-    __syncthreads();
-    const float inv = linv;
-    float *orow = out + (int64_t)blockIdx.x * dim;
-    for (int64_t g = threadIdx.x; g < ng; g += 256) {
-        float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
-        for (int s = 0; s < ns; ++s) {
-            const float *a = pp + s * stride + 2 + 3 * g;
-            A0 = A0 + fs[s] * a[0];
-            A1 = A1 + fs[s] * a[1];
-            A2 = A2 + fs[s] * a[2];
+    float a[kMaxSplits][3];
+    auto load_acc = [&](int64_t g) {
+        const int64_t gc = g < ng ? g : ng - 1;
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s) {
+            const float *p = pp + (s < ns ? s : ns - 1) * stride + 2 + 3 * gc;
+            a[s][0] = p[0], a[s][1] = p[1], a[s][2] = p[2];
         }
+    };
+    load_acc(tid);
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s)
+        if (s < ns) M = fmaxf(M, ml[0][s]);
+    float f[kMaxSplits], L = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+        f[s] = 0.0f;
+        if (s < ns) {
+            const float mw = ml[0][s];
+            f[s] = (M == -INFINITY || mw == -INFINITY) ? 0.0f : expf(mw - M);
+            L = L + f[s] * ml[1][s];
+        }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
+    float *orow = out + (int64_t)blockIdx.x * dim;
+    for (int64_t g = tid; g < ng; g += 256) {
+        if (g != tid) load_acc(g);
+        float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s)
+            if (s < ns) {
+                A0 = A0 + f[s] * a[s][0];
+                A1 = A1 + f[s] * a[s][1];
+                A2 = A2 + f[s] * a[s][2];
+            }
         float R[9];
         rotation_matrix(vrot + 4 * g, R);
 #pragma unroll
