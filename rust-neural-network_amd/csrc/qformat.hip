@@ -1131,14 +1131,17 @@ struct Bf16Plan {
 };
 constexpr int kBf16MaxTilesOne = 12, kBf16MaxTiles = 4;
 
-// The largest S (up to 8 for m > 8, else 1) that gives every wave whole
-// chunks and keeps the tiles per range within the register budget; S = 0 if
-// none does. (Splitting K trades the x bytes and x splitting per CU against
-// the partial sums' round trip through memory: measured at 4096 x 11008
-// INT4, m = 16: 18.0 us with S = 4, 19.3 with S = 1; m = 8: 16.8 against 15.5.)
+// The largest S (up to 8 for m > 8 with 4-bit codes, else 1) that gives
+// every wave whole chunks and keeps the tiles per range within the register
+// budget; S = 0 if none does. (Splitting K trades the x bytes and x splitting
+// per CU against the partial sums' round trip through memory. Measured at
+// 4096 x 11008: INT4, m = 16: 18.0 us with S = 4, 19.3 with S = 1; m = 8:
+// 16.8 against 15.5. With 2 or 4 weight bytes per 4 codes' worth of x the
+// weights dominate and S = 1 wins: INT8 m = 16 24.4 against 33.4 us (S = 8),
+// BF16 m = 16 28.4 against 43.7.)
 static Bf16Plan bf16_plan(int64_t M, int64_t K, int64_t N, int ep) {
     const int64_t nch = K / (4 * ep), cus = device_cu_count();
-    for (int S = M > 8 ? kBf16MaxParts : 1; S >= 1; S /= 2) {
+    for (int S = M > 8 && ep >= 32 ? kBf16MaxParts : 1; S >= 1; S /= 2) {
         if (nch % (S * kBf16Waves) != 0) continue;
         const uint32_t cpw = (uint32_t)(nch / (S * kBf16Waves));
         const int tmax = cpw == 1 ? kBf16MaxTilesOne : kBf16MaxTiles;
