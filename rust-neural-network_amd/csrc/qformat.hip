@@ -762,8 +762,18 @@ void qt_gemv_bf16_kernel(
     constexpr int EP = Fmt<KIND>::EP;  // elements per 16-byte piece
     constexpr int JS = EP / 8;         // MFMA steps per chunk
     constexpr int NW = kBf16Waves;
+    // Several chunks per wave (!ONE): x is loaded in whole-row runs (a load
+    // instruction reads 1 KiB of consecutive bytes: 64/EP rows of the chunk)
+    // and regrouped into the fragment layout through the wave's LDS slice.
+    // The fragment layout itself (each lane reads 4 EP consecutive bytes of
+    // its row, so one instruction touches 64 different lines 16 bytes at a
+    // time) measured 19.3 against 15.2 us at m = 16 over all of K.
+    constexpr bool STAGE = !ONE;
+    constexpr int XP = 4 * EP + 4;     // floats per staged row (16-byte pad: no bank conflicts)
+    constexpr int XRPL = 64 / EP;      // rows per whole-row load instruction
     typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
     __shared__ float part[NW][TPW][16][17];
+    __shared__ __attribute__((aligned(16))) float xs[STAGE ? NW * 16 * XP : 4];
     __shared__ uint32_t last;
     // (the wave index through readfirstlane: uniform to the compiler, so the
     // chunk offsets are scalar and the buffer loads take them as soffset)
@@ -779,7 +789,10 @@ void qt_gemv_bf16_kernel(
     // x: rows past mrows read zero (the launch keeps 16 K floats < 2^31 bytes)
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(x), 0, (int)(mrows * K * 4), 0x00020000);
-    const uint32_t xoff = (uint32_t)((i * K + q * EP) * 4);
+    // (the row is always in the per-lane offset, which the descriptor's
+    // range check covers: rows past mrows read zero)
+    const uint32_t xoff = STAGE ? (uint32_t)(((lane / EP) * K + (lane % EP) * 4) * 4)
+                                : (uint32_t)((i * K + q * EP) * 4);
     const uint32_t c0 = (sp * NW + wid) * cpw;  // this wave's first chunk
     // per tile: the lane's byte offset within the range (row 16t + i, piece
     // q of a chunk) and its row's first scale index
@@ -793,15 +806,18 @@ void qt_gemv_bf16_kernel(
         if (SCALED) gbase[t] = std::min<int64_t>(gbase[t], ns - 1);
     }
     struct Chunk {
-        f4v xf[EP / 4];  // x[i][c*4EP + q*EP ..+ EP)
+        f4v xf[EP / 4];  // x[i][c*4EP + q*EP ..+ EP), or (staged) whole-row runs
         v4i w[TPW];
         float sc[TPW];
     };
     auto load = [&](Chunk &ch, uint32_t c) {
 #pragma unroll
         for (int u = 0; u < EP / 4; ++u)
-            ch.xf[u] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  xr, xoff + 16 * u, c * (4 * EP * 4), 0));
+            ch.xf[u] = __builtin_bit_cast(
+                f4v, STAGE ? __builtin_amdgcn_raw_buffer_load_b128(
+                                 xr, xoff + (uint32_t)(u * XRPL * K * 4), c * (4 * EP * 4), 0)
+                           : __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 16 * u,
+                                                                   c * (4 * EP * 4), 0));
         // chunk c starts 64 bytes per chunk into every row (4 pieces); the
         // group of a chunk is uniform (groups hold whole chunks or rows)
         const uint32_t grp = kg ? c / cpg : 0u;
@@ -819,13 +835,29 @@ void qt_gemv_bf16_kernel(
 #pragma unroll
     for (int t = 0; t < TPW; ++t) tot[t] = f4v{0.f, 0.f, 0.f, 0.f};
     auto compute = [&](const Chunk &ch) {
+        // (staged: the whole-row runs into the wave's LDS slice, then the
+        // lane's fragment, x[i][q EP .. q EP + EP), back; one wave's LDS
+        // operations complete in order)
+        f4v xfr[EP / 4];
+        if constexpr (STAGE) {
+            float *xw = xs + wid * 16 * XP;
+#pragma unroll
+            for (int u = 0; u < EP / 4; ++u)
+                *reinterpret_cast<f4v *>(xw + (u * XRPL + lane / EP) * XP + (lane % EP) * 4) = ch.xf[u];
+#pragma unroll
+            for (int u = 0; u < EP / 4; ++u)
+                xfr[u] = *reinterpret_cast<const f4v *>(xw + i * XP + q * EP + 4 * u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < EP / 4; ++u) xfr[u] = ch.xf[u];
+        }
         // the chunk's A fragments: step j takes elements 8j .. 8j+7
         v4i a[JS][kSplitParts];
 #pragma unroll
         for (int j = 0; j < JS; ++j)
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                const f4v &v4 = ch.xf[2 * j + d / 2];
+                const f4v &v4 = xfr[2 * j + d / 2];
                 float h0, m0, l0, h1, m1, l1;
                 split3(v4[2 * (d % 2)], h0, m0, l0);
                 split3(v4[2 * (d % 2) + 1], h1, m1, l1);
@@ -1131,17 +1163,25 @@ struct Bf16Plan {
 };
 constexpr int kBf16MaxTilesOne = 12, kBf16MaxTiles = 4;
 
-// The largest S (up to 8 for m > 8 with 4-bit codes, else 1) that gives
-// every wave whole chunks and keeps the tiles per range within the register
-// budget; S = 0 if none does. (Splitting K trades the x bytes and x splitting
-// per CU against the partial sums' round trip through memory. Measured at
-// 4096 x 11008: INT4, m = 16: 18.0 us with S = 4, 19.3 with S = 1; m = 8:
-// 16.8 against 15.5. With 2 or 4 weight bytes per 4 codes' worth of x the
-// weights dominate and S = 1 wins: INT8 m = 16 24.4 against 33.4 us (S = 8),
-// BF16 m = 16 28.4 against 43.7.)
+// The K split S (1, 2, 4 or 8) with the lowest estimated time among those
+// that give every wave whole chunks and keep the tiles per range within the
+// register budget; S = 0 if none does. The estimate, per workgroup, from
+// rates measured on this kernel (MI355X, m = 8 and 16, K = 4096 to 14336,
+// INT4 and INT8): 5.75 us + x bytes at 77 GB/s (rows past m are not
+// fetched) + weight bytes at 13 GB/s + 4.5 us for the partial sums' round
+// trip when S > 1, times the rounds of workgroups over the CUs. Splitting K
+// cuts the x bytes every CU reads (all of its K range, for 16 rows) at the
+// cost of that round trip. Measured (us, S = 1 against the split chosen
+// before by size alone): INT4 m = 16 4096 x 11008 15.9 against 18.1 (S = 4),
+// 8192 x 8192 22.5 against 33.3 (S = 8, 344 workgroups); 14336 x 4096 26.4
+// against 23.5 (S = 2, which the estimate keeps); INT8 m = 16 4096 x 11008
+// 22.7 against 33.8 (S = 8).
 static Bf16Plan bf16_plan(int64_t M, int64_t K, int64_t N, int ep) {
     const int64_t nch = K / (4 * ep), cus = device_cu_count();
-    for (int S = M > 8 && ep >= 32 ? kBf16MaxParts : 1; S >= 1; S /= 2) {
+    const double wbytes = 16.0 / ep;  // weight bytes per element
+    Bf16Plan best = {0, 0, 0, 0};
+    double best_us = 0.0;
+    for (int S = kBf16MaxParts; S >= 1; S /= 2) {
         if (nch % (S * kBf16Waves) != 0) continue;
         const uint32_t cpw = (uint32_t)(nch / (S * kBf16Waves));
         const int tmax = cpw == 1 ? kBf16MaxTilesOne : kBf16MaxTiles;
@@ -1149,9 +1189,14 @@ static Bf16Plan bf16_plan(int64_t M, int64_t K, int64_t N, int ep) {
                                             ceil_div(N, 16 * tmax));
         const int64_t tpw = ceil_div(ceil_div(N, R), 16);
         if (tpw > tmax || N * R >= (int64_t(1) << 32) || R * S > 0x7fffffffLL) continue;
-        return {S, (int)R, (int)tpw, cpw};
+        const double kpart = (double)K / S;
+        const double x_bytes = 4.0 * std::min<int64_t>(M, 16) * kpart;
+        const double w_bytes = (double)ceil_div(N, R) * kpart * wbytes;
+        const double us = (5.75 + x_bytes / 77e3 + w_bytes / 13e3 + (S > 1 ? 4.5 : 0.0)) *
+                          (double)ceil_div(R * S, cus);
+        if (best.S == 0 || us < best_us) best = {S, (int)R, (int)tpw, cpw}, best_us = us;
     }
-    return {0, 0, 0, 0};
+    return best;
 }
 
 // Workspace (split K): one counter per range, then the parts' sums
