@@ -445,8 +445,8 @@ constexpr int kMaxSplits = 16;
 // Merges the splits of one query (a workgroup per query): M = max m_s,
 // L = sum l_s e^(m_s - M), A = sum a_s e^(m_s - M) in split order, then
 // out = R^T A / L as the attention kernels do. Every load of a thread's first
-// group (the splits' max and sum, and its accumulators in every split) is
-// issued before the one barrier, so the kernel waits on memory once.
+// group (the splits' max and sum, its accumulators in every split and its V
+// rotor) is issued before the one barrier, so the kernel waits on memory once.
 __global__ __launch_bounds__(256) void rq_kv_attn_merge_kernel(const float *__restrict__ part,
                                                                int ns, const float *__restrict__ vrot,
                                                                int64_t dim, int64_t ng,
@@ -455,21 +455,23 @@ __global__ __launch_bounds__(256) void rq_kv_attn_merge_kernel(const float *__re
     const int64_t stride = 2 + 3 * ng;
     const float *pp = part + (int64_t)blockIdx.x * ns * stride;
     const int tid = threadIdx.x;
-    if (tid < kMaxSplits) {  // (splits past ns are read clamped and not used)
-        const int sc = tid < ns ? tid : ns - 1;
-        ml[0][tid] = pp[sc * stride];
-        ml[1][tid] = pp[sc * stride + 1];
-    }
-    float a[kMaxSplits][3];
-    auto load_acc = [&](int64_t g) {
+    float a[kMaxSplits][3], rq[4];
+    auto load_group = [&](int64_t g) {
         const int64_t gc = g < ng ? g : ng - 1;
 #pragma unroll
         for (int s = 0; s < kMaxSplits; ++s) {
             const float *p = pp + (s < ns ? s : ns - 1) * stride + 2 + 3 * gc;
             a[s][0] = p[0], a[s][1] = p[1], a[s][2] = p[2];
         }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) rq[c] = vrot[4 * gc + c];
     };
-    load_acc(tid);
+    load_group(tid);
+    if (tid < kMaxSplits) {  // (after the group's loads; splits past ns: clamped, not used)
+        const int sc = tid < ns ? tid : ns - 1;
+        ml[0][tid] = pp[sc * stride];
+        ml[1][tid] = pp[sc * stride + 1];
+    }
     __syncthreads();
     float M = -INFINITY;
 #pragma unroll
@@ -488,7 +490,7 @@ __global__ __launch_bounds__(256) void rq_kv_attn_merge_kernel(const float *__re
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
     float *orow = out + (int64_t)blockIdx.x * dim;
     for (int64_t g = tid; g < ng; g += 256) {
-        if (g != tid) load_acc(g);
+        if (g != tid) load_group(g);
         float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
 #pragma unroll
         for (int s = 0; s < kMaxSplits; ++s)
@@ -498,7 +500,7 @@ __global__ __launch_bounds__(256) void rq_kv_attn_merge_kernel(const float *__re
                 A2 = A2 + f[s] * a[s][2];
             }
         float R[9];
-        rotation_matrix(vrot + 4 * g, R);
+        rotation_matrix(rq, R);
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const float o = (R[c] * A0 + R[3 + c] * A1 + R[6 + c] * A2) * inv;
