@@ -599,7 +599,7 @@ def bench_rq_attention(H, W, dev, steps):
     q = gen_f32((bh, 1, dim), 13, dev)
     out = torch.empty_like(q)
     scale = 1.0 / dim ** 0.5
-    ws = torch.empty(max(1, H.rotorquant_kv_attention_workspace_size(bh, 1, seq, dim)),
+    ws = torch.zeros(max(1, H.rotorquant_kv_attention_workspace_size(bh, 1, seq, dim)),
                      dtype=torch.uint8, device=dev)
     ms = graph_timed(lambda i: H.rotorquant_kv_attention(q, pages[0], pages[1], rots[0], rots[1],
                                                          seq, scale, out=out, workspace=ws), 20)
@@ -609,7 +609,7 @@ def bench_rq_attention(H, W, dev, steps):
     nc1, ns1 = H.rotorquant_kv_page_elems(b1, seq, dim)
     p1 = [(pg[0][:nc1], pg[1][:ns1]) for pg in pages]
     q1, out1 = q[:b1], out[:b1]
-    ws1 = torch.empty(max(1, H.rotorquant_kv_attention_workspace_size(b1, 1, seq, dim)),
+    ws1 = torch.zeros(max(1, H.rotorquant_kv_attention_workspace_size(b1, 1, seq, dim)),
                       dtype=torch.uint8, device=dev)
     ms1 = graph_timed(lambda i: H.rotorquant_kv_attention(q1, p1[0], p1[1], rots[0], rots[1], seq,
                                                           scale, out=out1, workspace=ws1), 20)
@@ -631,7 +631,7 @@ def bench_rq_attention(H, W, dev, steps):
             "kernel": "rq_kv_attn_kernel (scores and V in the rotated domain)",
             "batch1": {"us": round(ms1 * 1e3, 2), "bytes": nbytes1,
                        "frac_hbm": round(nbytes1 / (ms1 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                       "note": "32 queries: sequence split over workgroups + merge kernel"},
+                       "note": "32 queries: sequence split over workgroups, merged by the last split"},
             "f32_kv_sdpa_us": round(ms_f32 * 1e3, 2),
             "f32_kv_bytes": 2 * bh * seq * dim * 4,
             "shape": {"batch": b, "heads": h, "seq": seq, "head_dim": dim, "bits": bits, "nq": 1}}

@@ -399,7 +399,7 @@ int rnn_rotorquant_kv_pack(const int8_t *codes, const float *scales, int64_t bh,
  * f32 sums in the kernel's own order: within a floating-point bound of the
  * reference, not bit for bit. Pages 16-byte aligned. When the queries alone
  * do not fill the device, each query's sequence is split over several
- * workgroups whose softmax states a second kernel merges; their scratch is
+ * workgroups whose softmax states the last of them merges; their scratch is
  * stream-ordered device memory here, or the caller's workspace with
  * rnn_rotorquant_kv_attention_ws. */
 int rnn_rotorquant_kv_attention(const float *q, int64_t bh, int64_t nq,
@@ -417,9 +417,10 @@ size_t rnn_rotorquant_kv_attention_workspace_size(int64_t bh, int64_t nq, int64_
 
 /* rnn_rotorquant_kv_attention (src/tensor.rs:618-672) with the split states
  * in a caller's workspace of workspace_bytes (at least
- * rnn_rotorquant_kv_attention_workspace_size; any contents; calls sharing a
- * workspace must be ordered on one stream). workspace NULL: as
- * rnn_rotorquant_kv_attention. */
+ * rnn_rotorquant_kv_attention_workspace_size). The workspace holds counts:
+ * zero it once before its first use; every call leaves them at zero, so it
+ * is reused as is. Calls sharing a workspace must be ordered on one stream.
+ * workspace NULL: as rnn_rotorquant_kv_attention. */
 int rnn_rotorquant_kv_attention_ws(const float *q, int64_t bh, int64_t nq,
                                    const uint16_t *k_codes, const float *k_scales,
                                    const uint16_t *v_codes, const float *v_scales,

@@ -42,6 +42,8 @@ namespace rnn {
 
 constexpr int kTile = 64;
 constexpr int kAttnWaves = 4;
+// Sequence splits: at most kMaxSplits, each of at least kAttnWaves tiles.
+constexpr int kMaxSplits = 16;
 
 enum { RQ_PAGE_K = 0, RQ_PAGE_V = 1 };
 
@@ -156,15 +158,23 @@ __device__ __forceinline__ void rq_load_k(RqTileK<NG4, NG8> &t, const uint16_t *
 
 
 // grid: (BH * nq, splits) workgroups of kAttnWaves waves; ng <= 4 * NG4 <= 8
-// * NG8 <= 64. Split y takes tiles [y * tps, min(T, (y + 1) * tps)); with
-// part != null it writes its unnormalised state (max, sum, rotated
-// accumulators) there for rq_kv_attn_merge_kernel instead of the output.
+// * NG8 <= 64. Split y takes tiles [y * tps, min(T, (y + 1) * tps)). With
+// several splits (part != null) each writes its unnormalised state (max,
+// sum, rotated accumulators) to part and counts itself in at cnt[query];
+// the last of a query's splits merges the states in split order (M = max
+// m_s, L = sum l_s e^(m_s - M), A = sum a_s e^(m_s - M)), writes the output
+// and resets the count.
+// The states are device-scope atomic stores, written through the XCD's L2
+// to the device's coherence point and complete (vmcnt 0) before the count;
+// the last split reads them with device-scope atomic loads. No workgroup
+// waits for another.
 template <int NG4, int NG8>
 __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const float *__restrict__ ks,
     const uint16_t *__restrict__ vc, const float *__restrict__ vs, const float *__restrict__ krot,
     const float *__restrict__ vrot, int64_t nq, int64_t S, int64_t dim, int64_t ng, int64_t T,
-    int64_t tps, float scale, float *__restrict__ out, float *__restrict__ part) {
+    int64_t tps, float scale, float *__restrict__ out, float *__restrict__ part,
+    uint32_t *__restrict__ cnt) {
     __shared__ __attribute__((aligned(16))) float qs[4 * 64];  // rotated query, 4 floats per group
     __shared__ __attribute__((aligned(16))) float pb[kAttnWaves][64];
     __shared__ float mrg[kAttnWaves][2 + 3 * 64];
@@ -278,11 +288,52 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_kernel(
             A2 = A2 + f * mrg[w][4 + 3 * lane];
         }
     }
-    if (part) {  // this split's state, merged by rq_kv_attn_merge_kernel
-        float *pp = part + ((bh * nq + qi) * gridDim.y + blockIdx.y) * (2 + 3 * ng);
-        if (lane == 0) pp[0] = M, pp[1] = L;
-        if (gact) pp[2 + 3 * g] = A0, pp[3 + 3 * g] = A1, pp[4 + 3 * g] = A2;
-        return;
+    if (part) {
+        const int64_t qrow = bh * nq + qi, stride = 2 + 3 * ng;
+        const int ns = (int)gridDim.y;
+        float *pp = part + (qrow * ns + blockIdx.y) * stride;
+        if (lane == 0) {
+            __hip_atomic_store(pp, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (gact) {
+            __hip_atomic_store(pp + 2 + 3 * g, A0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 3 + 3 * g, A1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 4 + 3 * g, A2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        uint32_t old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(&cnt[qrow], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__shfl(old, 0, 64) != (uint32_t)ns - 1) return;
+        // the last split: every state's loads in flight, then merged in split order
+        float mv[kMaxSplits], lv[kMaxSplits], av[kMaxSplits][3];
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s) {
+            const float *ps = part + (qrow * ns + (s < ns ? s : ns - 1)) * stride;
+            mv[s] = __hip_atomic_load(ps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lv[s] = __hip_atomic_load(ps + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                av[s][c] = __hip_atomic_load(ps + 2 + 3 * g + c, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane == 0)  // ready for the next call
+            __hip_atomic_store(&cnt[qrow], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s)
+            if (s < ns) M = fmaxf(M, mv[s]);
+        L = 0.0f, A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s)
+            if (s < ns) {
+                const float f = (M == -INFINITY || mv[s] == -INFINITY) ? 0.0f : expf(mv[s] - M);
+                L = L + f * lv[s];
+                A0 = A0 + f * av[s][0];
+                A1 = A1 + f * av[s][1];
+                A2 = A2 + f * av[s][2];
+            }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
     if (!gact) return;
@@ -310,10 +361,13 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
     const float *__restrict__ q, const uint16_t *__restrict__ kc, const float *__restrict__ ks,
     const uint16_t *__restrict__ vc, const float *__restrict__ vs, const float *__restrict__ krot,
     const float *__restrict__ vrot, int64_t nq, int64_t S, int64_t dim, int64_t ng, int64_t T,
-    int64_t tps, float scale, float *__restrict__ out, float *__restrict__ part) {
+    int64_t tps, float scale, float *__restrict__ out, float *__restrict__ part,
+    uint32_t *__restrict__ cnt) {
     extern __shared__ __attribute__((aligned(16))) float dyn[];
     __shared__ __attribute__((aligned(16))) float pb[kAttnWaves][64];
     __shared__ float mrg[kAttnWaves][2];
+    __shared__ float sml[2][kMaxSplits];
+    __shared__ uint32_t last;
     const int64_t ng4 = (ng + 3) / 4, ng8 = (ng + 7) / 8;
     float *qs = dyn;               // rotated query: 4 floats per group, 8 * ng8 groups, zero past ng
     float *acc = dyn + 32 * ng8;   // [kAttnWaves][3 * kWideRange]
@@ -414,8 +468,86 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
     float *orow = out + (bh * nq + qi) * dim;
-    float *pp = part ? part + ((bh * nq + qi) * gridDim.z + blockIdx.z) * (2 + 3 * ng) : nullptr;
-    if (pp && blockIdx.y == 0 && threadIdx.x == 0) pp[0] = M, pp[1] = L;
+    if (part) {
+        // this split's state (every range writes the same max and sum: the
+        // scores are computed alike), counted in per (query, range); the
+        // last split of the range merges them, as in rq_kv_attn_kernel
+        const int64_t qrow = bh * nq + qi, stride = 2 + 3 * ng;
+        const int ns = (int)gridDim.z;
+        float *pp = part + (qrow * ns + blockIdx.z) * stride;
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(pp, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        for (int gl = threadIdx.x; gl < nr; gl += kAttnWaves * 64) {
+            float A[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < kAttnWaves; ++w)
+#pragma unroll
+                for (int c = 0; c < 3; ++c) A[c] = A[c] + f[w] * acc[w * 3 * kWideRange + 3 * gl + c];
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                __hip_atomic_store(pp + 2 + 3 * (g0 + gl) + c, A[c], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        uint32_t *cq = cnt + qrow * gridDim.y + blockIdx.y;
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(cq, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)ns - 1;
+        __syncthreads();
+        if (!last) return;
+        if (threadIdx.x < kMaxSplits) {
+            const float *ps = part + (qrow * ns + (threadIdx.x < ns ? threadIdx.x : ns - 1)) * stride;
+            sml[0][threadIdx.x] = __hip_atomic_load(ps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sml[1][threadIdx.x] = __hip_atomic_load(ps + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (threadIdx.x == 0)  // ready for the next call
+            __hip_atomic_store(cq, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        float Ms = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s)
+            if (s < ns) Ms = fmaxf(Ms, sml[0][s]);
+        float fs[kMaxSplits], Ls = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kMaxSplits; ++s) {
+            fs[s] = 0.0f;
+            if (s < ns) {
+                fs[s] = (Ms == -INFINITY || sml[0][s] == -INFINITY) ? 0.0f : expf(sml[0][s] - Ms);
+                Ls = Ls + fs[s] * sml[1][s];
+            }
+        }
+        const float invs = Ls > 0.0f ? 1.0f / Ls : 0.0f;  // src/tensor.rs:657
+        for (int gl = threadIdx.x; gl < nr; gl += kAttnWaves * 64) {
+            const int64_t g = g0 + gl;
+            float av[kMaxSplits][3];
+#pragma unroll
+            for (int s = 0; s < kMaxSplits; ++s)
+#pragma unroll
+                for (int c = 0; c < 3; ++c)
+                    av[s][c] = __hip_atomic_load(part + (qrow * ns + (s < ns ? s : ns - 1)) * stride +
+                                                     2 + 3 * g + c,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
+#pragma unroll
+            for (int s = 0; s < kMaxSplits; ++s)
+                if (s < ns) {
+                    A0 = A0 + fs[s] * av[s][0];
+                    A1 = A1 + fs[s] * av[s][1];
+                    A2 = A2 + fs[s] * av[s][2];
+                }
+            float R[9];
+            rotation_matrix(vrot + 4 * g, R);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const float o = (R[c] * A0 + R[3 + c] * A1 + R[6 + c] * A2) * invs;
+                if (3 * g + c < dim) orow[3 * g + c] = o;
+            }
+        }
+        return;
+    }
     for (int gl = threadIdx.x; gl < nr; gl += kAttnWaves * 64) {
         float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
 #pragma unroll
@@ -425,10 +557,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
             A2 = A2 + f[w] * acc[w * 3 * kWideRange + 3 * gl + 2];
         }
         const int64_t g = g0 + gl;
-        if (pp) {
-            pp[2 + 3 * g] = A0, pp[3 + 3 * g] = A1, pp[4 + 3 * g] = A2;
-            continue;
-        }
         float R[9];
         rotation_matrix(vrot + 4 * g, R);
 #pragma unroll
@@ -439,75 +567,6 @@ __global__ __launch_bounds__(kAttnWaves * 64) void rq_kv_attn_wide_kernel(
     }
 }
 
-// Sequence splits: at most kMaxSplits, each of at least kAttnWaves tiles.
-constexpr int kMaxSplits = 16;
-
-// Merges the splits of one query (a workgroup per query): M = max m_s,
-// L = sum l_s e^(m_s - M), A = sum a_s e^(m_s - M) in split order, then
-// out = R^T A / L as the attention kernels do. Every load of a thread's first
-// group (the splits' max and sum, its accumulators in every split and its V
-// rotor) is issued before the one barrier, so the kernel waits on memory once.
-__global__ __launch_bounds__(256) void rq_kv_attn_merge_kernel(const float *__restrict__ part,
-                                                               int ns, const float *__restrict__ vrot,
-                                                               int64_t dim, int64_t ng,
-                                                               float *__restrict__ out) {
-    __shared__ float ml[2][kMaxSplits];
-    const int64_t stride = 2 + 3 * ng;
-    const float *pp = part + (int64_t)blockIdx.x * ns * stride;
-    const int tid = threadIdx.x;
-    float a[kMaxSplits][3], rq[4];
-    auto load_group = [&](int64_t g) {
-        const int64_t gc = g < ng ? g : ng - 1;
-#pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s) {
-            const float *p = pp + (s < ns ? s : ns - 1) * stride + 2 + 3 * gc;
-            a[s][0] = p[0], a[s][1] = p[1], a[s][2] = p[2];
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) rq[c] = vrot[4 * gc + c];
-    };
-    load_group(tid);
-    if (tid < kMaxSplits) {  // (after the group's loads; splits past ns: clamped, not used)
-        const int sc = tid < ns ? tid : ns - 1;
-        ml[0][tid] = pp[sc * stride];
-        ml[1][tid] = pp[sc * stride + 1];
-    }
-    __syncthreads();
-    float M = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s)
-        if (s < ns) M = fmaxf(M, ml[0][s]);
-    float f[kMaxSplits], L = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) {
-        f[s] = 0.0f;
-        if (s < ns) {
-            const float mw = ml[0][s];
-            f[s] = (M == -INFINITY || mw == -INFINITY) ? 0.0f : expf(mw - M);
-            L = L + f[s] * ml[1][s];
-        }
-    }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;  // src/tensor.rs:657
-    float *orow = out + (int64_t)blockIdx.x * dim;
-    for (int64_t g = tid; g < ng; g += 256) {
-        if (g != tid) load_group(g);
-        float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f;
-#pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s)
-            if (s < ns) {
-                A0 = A0 + f[s] * a[s][0];
-                A1 = A1 + f[s] * a[s][1];
-                A2 = A2 + f[s] * a[s][2];
-            }
-        float R[9];
-        rotation_matrix(rq, R);
-#pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            const float o = (R[c] * A0 + R[3 + c] * A1 + R[6 + c] * A2) * inv;
-            if (3 * g + c < dim) orow[3 * g + c] = o;
-        }
-    }
-}
 
 // Splits of each query's tiles: enough workgroups for the given number per
 // CU, at least kAttnWaves tiles per split, one split when the queries alone
@@ -523,12 +582,30 @@ static void attn_splits(int64_t wgs, int64_t T, bool wide, int64_t &ns, int64_t 
     ns = T > 0 ? ceil_div(T, tps) : 1;  // no empty split
 }
 
+// Split workspace: a count per query and range (the first bytes, rounded up
+// to 256), then the splits' states [query][split][2 + 3 ng].
+static size_t attn_count_bytes(int64_t queries) {
+    return (size_t)ceil_div(4 * queries, 256) * 256;
+}
+static size_t attn_split_bytes(int64_t queries, int64_t ns, int64_t ng) {
+    const int64_t ranges = ng > 64 ? ceil_div(ng, kWideRange) : 1;  // a count per range
+    return ns > 1 ? attn_count_bytes(queries * ranges) +
+                        (size_t)(queries * ns * (2 + 3 * ng)) * sizeof(float)
+                  : 0;
+}
+
 static size_t attn_workspace_bytes(int64_t bh, int64_t nq, int64_t seq, int64_t dim) {
     const int64_t ng = ceil_div(dim, 3), T = ceil_div(seq, kTile);
     const int64_t wgs = bh * nq * (ng > 64 ? ceil_div(ng, kWideRange) : 1);
     int64_t ns, tps;
     attn_splits(wgs, T, ng > 64, ns, tps);
-    return ns > 1 ? (size_t)(bh * nq * ns * (2 + 3 * ng)) * sizeof(float) : 0;
+    return attn_split_bytes(bh * nq, ns, ng);
+}
+
+__global__ void rq_zero_kernel(uint32_t *__restrict__ p, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
 }
 
 // Largest LDS a workgroup may use on the current device (cached per device).
@@ -618,8 +695,9 @@ extern "C" int rnn_rotorquant_kv_attention_ws(const float *q, int64_t bh, int64_
     attn_splits(bh * nq * nranges, T, ng > 64, ns, tps);
     hipStream_t st = as_stream(stream);
     // ns > 1: the splits' states go to the workspace (or stream-ordered
-    // scratch) and a merge kernel writes out
-    const size_t need = ns > 1 ? (size_t)(bh * nq * ns * (2 + 3 * ng)) * sizeof(float) : 0;
+    // scratch, its counts zeroed); the last split of each query (and range)
+    // merges them
+    const size_t need = attn_split_bytes(bh * nq, ns, ng);
     RNN_REQUIRE(!workspace || workspace_bytes >= need,
                 "%s: workspace of %zu bytes, %zu needed (rnn_rotorquant_kv_attention_workspace_size)",
                 name, workspace_bytes, need);
@@ -629,27 +707,30 @@ extern "C" int rnn_rotorquant_kv_attention_ws(const float *q, int64_t bh, int64_
                                         (int)wide_lds) == hipSuccess,
                     "%s: %lld bytes of dynamic LDS refused", name, (long long)wide_lds);
     void *ws = need ? workspace : nullptr;
-    if (need && !ws) RNN_TRY(check_hip(hipMallocAsync(&ws, need, st), name));
-    float *part = static_cast<float *>(ws);
+    if (need && !ws) {
+        RNN_TRY(check_hip(hipMallocAsync(&ws, need, st), name));
+        rq_zero_kernel<<<(unsigned)std::min<int64_t>(ceil_div(bh * nq * nranges, 256), 1024), 256,
+                         0, st>>>(static_cast<uint32_t *>(ws), bh * nq * nranges);
+    }
+    uint32_t *cnt = static_cast<uint32_t *>(ws);
+    float *part = ws ? reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                                 attn_count_bytes(bh * nq * nranges))
+                     : nullptr;
     if (ng > 64) {
         rq_kv_attn_wide_kernel<<<dim3(grid, (unsigned)nranges, (unsigned)ns), kAttnWaves * 64,
                                  (size_t)wide_lds, st>>>(q, k_codes, k_scales, v_codes, v_scales,
                                                          k_rotors, v_rotors, nq, seq, dim, ng, T,
-                                                         tps, scale, out, part);
+                                                         tps, scale, out, part, cnt);
     } else if (ng <= 44) {
         rq_kv_attn_kernel<11, 6><<<dim3(grid, (unsigned)ns), kAttnWaves * 64, 0, st>>>(
             q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, tps,
-            scale, out, part);
+            scale, out, part, cnt);
     } else {
         rq_kv_attn_kernel<16, 8><<<dim3(grid, (unsigned)ns), kAttnWaves * 64, 0, st>>>(
             q, k_codes, k_scales, v_codes, v_scales, k_rotors, v_rotors, nq, seq, dim, ng, T, tps,
-            scale, out, part);
+            scale, out, part, cnt);
     }
     int rc = check_launch(name);
-    if (rc == RNN_OK && ns > 1) {
-        rq_kv_attn_merge_kernel<<<grid, 256, 0, st>>>(part, (int)ns, v_rotors, dim, ng, out);
-        rc = check_launch(name);
-    }
     if (ws && ws != workspace) {
         const int rf = check_hip(hipFreeAsync(ws, st), name);
         if (rc == RNN_OK) rc = rf;

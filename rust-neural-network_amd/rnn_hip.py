@@ -632,14 +632,30 @@ def rotorquant_kv_attention_workspace_size(bh, nq, seq, dim) -> int:
     return int(load().rnn_rotorquant_kv_attention_workspace_size(bh, nq, seq, dim))
 
 
+# Zeroed attention workspaces kept per (device, stream): every call leaves
+# the counts at zero, so one is reused by the calls ordered on its stream.
+_attn_ws = {}
+
+
+def _attn_workspace(dev, nbytes):
+    import torch
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _attn_ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        _attn_ws[key] = ws
+    return ws
+
+
 def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, out=None,
                             stream=None, workspace=None):
     """Tensor::flash_attention (src/tensor.rs:618-672) of q [bh, nq, dim] over
     a K page (RQ_PAGE_K) and a V page (RQ_PAGE_V) of rotorquant_kv_pack.
-    Returns out [bh, nq, dim]. `workspace`: a device byte tensor of at least
-    rotorquant_kv_attention_workspace_size(bh, nq, seq, dim) bytes for the
-    sequence split's states; on the current stream one is taken from torch's
-    allocator when none is given, on another stream the call allocates."""
+    Returns out [bh, nq, dim]. `workspace`: a zeroed device byte tensor of at
+    least rotorquant_kv_attention_workspace_size(bh, nq, seq, dim) bytes for
+    the sequence split's states (calls leave it reusable); on the current
+    stream a cached one is used when none is given, on another stream the
+    call allocates."""
     import torch
     _dev(q, torch.float32, "q")
     for t, nm in ((k_page[0], "k codes"), (v_page[0], "v codes")):
@@ -660,7 +676,7 @@ def rotorquant_kv_attention(q, k_page, v_page, k_rotors, v_rotors, seq, scale, o
     if workspace is None and stream is None:
         wsb = rotorquant_kv_attention_workspace_size(bh, nq, seq, dim)
         if wsb:
-            workspace = torch.empty(wsb, dtype=torch.uint8, device=q.device)
+            workspace = _attn_workspace(q.device, wsb)
     ws_bytes = 0 if workspace is None else workspace.numel()
     _check(load().rnn_rotorquant_kv_attention_ws(_ptr(q), bh, nq, _ptr(k_page[0]), _ptr(k_page[1]),
                                                  _ptr(v_page[0]), _ptr(v_page[1]), _ptr(k_rotors),

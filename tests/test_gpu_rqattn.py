@@ -119,10 +119,11 @@ def test_kv_attention_empty_cache_and_errors(dev, hip):
 
 
 def test_kv_attention_split_workspace_and_alloc(dev, hip):
-    """The sequence split (one query, 4096 positions): a caller's workspace,
-    torch's (the wrapper's default) and the library's own stream-ordered
-    scratch (the plain entry point, called through ctypes) give the same
-    bits; a workspace below the size the library asks for is refused."""
+    """The sequence split (two queries, 4096 positions): a caller's zeroed
+    workspace (twice in a row: the calls leave its counts at zero), the
+    wrapper's cached one and the library's own stream-ordered scratch (the
+    plain entry point, called through ctypes) give the same bits; a
+    workspace below the size the library asks for is refused."""
     import ctypes
     import torch
     bh, nq, seq, dim = 2, 1, 4096, 128
@@ -135,9 +136,15 @@ def test_kv_attention_split_workspace_and_alloc(dev, hip):
     q = torch.randn((bh, nq, dim), device=dev)
     need = hip.rotorquant_kv_attention_workspace_size(bh, nq, seq, dim)
     assert need > 0                                          # 2 queries do not fill the device
-    ws = torch.full((need,), 0xAB, dtype=torch.uint8, device=dev)   # any contents
+    ws = torch.zeros((need,), dtype=torch.uint8, device=dev)
     a = hip.rotorquant_kv_attention(q, kp, vp, krot, vrot, seq, 0.125, workspace=ws)
+    a2 = hip.rotorquant_kv_attention(q, kp, vp, krot, vrot, seq, 0.125, workspace=ws)
     b = hip.rotorquant_kv_attention(q, kp, vp, krot, vrot, seq, 0.125)
+    assert torch.equal(a, a2)
+    q2 = torch.randn((bh, nq, dim), device=dev)               # another query, same workspace
+    e = hip.rotorquant_kv_attention(q2, kp, vp, krot, vrot, seq, 0.125, workspace=ws)
+    f = hip.rotorquant_kv_attention(q2, kp, vp, krot, vrot, seq, 0.125)
+    assert torch.equal(e, f) and not torch.equal(a, e)
     c = torch.empty_like(a)
     P = ctypes.c_void_p
     rc = hip.load().rnn_rotorquant_kv_attention(
