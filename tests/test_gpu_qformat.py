@@ -186,11 +186,14 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
                          ids=["INT4-g128", "INT4-tensor", "INT8-g64", "INT8-rows", "BF16", "INT4-g512"])
 @pytest.mark.parametrize("m,k,n", [(5, 4096, 4096), (16, 4096, 5000), (9, 2048, 11008),
                                    (16, 4096, 16000), (12, 1024, 20000), (7, 4096, 30),
-                                   (16, 2048, 1)])
+                                   (16, 2048, 1),
+                                   # long K, few rows: K split 8 ways, one and two chunks per wave
+                                   (16, 8192, 300), (16, 16384, 64)])
 def test_linear_forward_bf16_gemv(dev, hip, fmt, gs, m, k, n):
     """The bf16 MFMA GEMV (x split into three bf16 parts, codes exact in
-    bf16, one scale per group sum, K split over 1-8 workgroups): 1-12 row
-    tiles per range, one or several chunks per wave, row ranges that are not
+    bf16, one scale per group sum, K split over 1-8 workgroups as the
+    plan's estimate picks): 1-12 row tiles per range, one or several chunks
+    per wave (x staged through LDS), row ranges that are not
     multiples of 16, fewer rows than CUs, rows of x past m; with and without
     bias, forced, with the caller's workspace (bit-identical, and the same
     counters reused) and as AUTO picks it, within the GEMM rounding bound; x
