@@ -738,11 +738,13 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
 }
 
 // x = h + m + l exactly: h and m are x and x - h with the low 16 bits
-// cleared, l = x - h - m has at most 8 significant bits. Infinities and NaN
-// stay whole in h.
+// cleared, l = x - h - m has at most 8 significant bits. Infinities stay
+// whole in h (r = 0 when h == x); a NaN whose payload sits only in the low
+// 16 bits becomes an infinity in h, but then r = x - h is NaN, so the sum
+// stays NaN as the reference's product does.
 __device__ __forceinline__ void split3(float x, float &h, float &m, float &l) {
     h = __uint_as_float(__float_as_uint(x) & 0xFFFF0000u);
-    const float r = __builtin_isfinite(x) ? x - h : 0.0f;
+    const float r = h == x ? 0.0f : x - h;
     m = __uint_as_float(__float_as_uint(r) & 0xFFFF0000u);
     l = r - m;
 }

@@ -227,6 +227,42 @@ def test_linear_forward_bf16_gemv(dev, hip, fmt, gs, m, k, n):
     gemm_check(y3, x2, wdeq, None)
 
 
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
+def test_linear_forward_nonfinite_x(dev, hip, m):
+    """Inf, -Inf and NaN in x (a canonical NaN and one whose payload sits
+    only in the low 16 bits, which the bf16 split must not turn into an
+    infinity): every fused path gives the reference's non-finite pattern --
+    inf * w is +-inf, inf * 0 and inf - inf are NaN, whatever the summation
+    order -- and its finite outputs stay within the GEMM bound."""
+    rng = np.random.default_rng(m + 40)
+    n, k = 48, 4096
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[5, :] = 0.0                                            # inf * 0 -> NaN in column 5
+    d, s, g = O.qt_quantize(O.QF_INT4, w, 128)
+    wdeq = O.qt_dequantize(O.QF_INT4, d, s, g, n * k).reshape(n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    low_nan = np.array([0x7F800001], dtype=np.uint32).view(np.float32)[0]
+    x[0, 10] = np.inf
+    if m > 1:
+        x[1, 20], x[1, 30] = np.inf, -np.inf                 # +inf - inf -> NaN
+    if m > 2:
+        x[2, 40] = np.nan
+    if m > 3:
+        x[3, 50] = low_nan
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = O.qt_linear_forward(O.QF_INT4, x, d, s, g, n, None)
+    fin = np.isfinite(x).all(axis=1)
+    algos = [hip.ALGO_GEMV, hip.ALGO_GEMV_MFMA] + ([hip.ALGO_GEMV_BF16] if m >= 3 else [])
+    for algo in algos:
+        y = host(hip.qt_linear_forward(O.QF_INT4, to_dev(x, dev), to_dev(d, dev), to_dev(s, dev),
+                                       g, n, algo=algo))
+        assert np.array_equal(np.isnan(y), np.isnan(ref)), algo
+        assert np.array_equal(np.isposinf(y), np.isposinf(ref)), algo
+        assert np.array_equal(np.isneginf(y), np.isneginf(ref)), algo
+        if fin.any():
+            gemm_check(y[fin], x[fin], wdeq, None)
+
+
 def test_linear_forward_bf16_gemv_rejects(dev, hip):
     """Forced bf16 GEMV outside its conditions: NF4 codes, a group of 32
     (GGUF Q4_0), m = 17; and a workspace one 16-byte step too small -- an
