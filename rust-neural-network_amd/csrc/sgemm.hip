@@ -2,8 +2,9 @@
 // (src/blas.rs:712-734, contract at :89-190): C = alpha*op(A)*op(B) + beta*C,
 // row-major storage with leading dimensions, op = identity or transpose.
 //
-// Fast path: v_mfma_f32_16x16x4f32 on 128x128 block tiles of 4 waves (64x64
-// each), K staged 32 floats at a time through double-buffered LDS:
+// Fast path (K % 32 == 0): sgemm_mfma2_kernel, below. Otherwise
+// sgemm_mfma_kernel: v_mfma_f32_16x16x4f32 on 128x128 block tiles of 4 waves
+// (64x64 each), K staged 32 floats at a time through double-buffered LDS:
 //  * K-contiguous operands (A as stored, B transposed) are kept as 128-byte
 //    LDS rows (32 floats) whose 16-byte chunks are XOR-swizzled by
 //    (row >> 1) & 7. A lane reads one 16-byte chunk = 4 consecutive k and
@@ -175,6 +176,197 @@ __global__ __launch_bounds__(256) void sgemm_mfma_kernel(const float *__restrict
         }
 }
 
+// K % 32 == 0: the same tiles and MFMAs with both operands in one LDS layout,
+// [kq][row][4] (kq = the 4-k quad within the 32-k stage), every fragment one
+// ds_read_b128. Physical row = row ^ kq ^ ((row >> 4) & 3): 16 lanes reading
+// a fragment (one kq, rows base..base+15), or storing a transposed K-major
+// quad (one kq, rows 4t + j for 16 consecutive t), touch 16 different 16-byte
+// bank groups.
+// K-contiguous operands are loaded a row's 128 bytes per 8 lanes and written
+// as they come; K-major ones are loaded 512 bytes of a k-row per 32 lanes,
+// 4 k-rows per thread, and transposed in registers (4 quads of one row).
+// Loads go through buffer descriptors whose range ends at the operand's last
+// element, so no branch guards them: rows past M or N read other rows' data
+// or zeros, and only reach outputs that are not stored. Each super-step's
+// fragments are read while the previous super-step's MFMAs run.
+__device__ __forceinline__ int sg2_row(int row, int kq) { return row ^ kq ^ ((row >> 4) & 3); }
+
+template <bool KMAJ>
+struct SgOp2 {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t off[4];  // per-thread byte offsets within the stage (from the stage base)
+    f4 reg[4];
+    // row-major loads (K-contiguous): f = tid + 256 i -> row f / 8, kq f % 8;
+    // K-major: kq = tid / 32, row quad tid % 32, k row 4 kq + i
+    __device__ __forceinline__ void init(int64_t ld, int tid) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (KMAJ) {
+                off[i] = (uint32_t)(((4 * (tid >> 5) + i) * ld + 4 * (tid & 31)) * 4);
+            } else {
+                const int f = tid + 256 * i;
+                off[i] = (uint32_t)(((f >> 3) * ld + 4 * (f & 7)) * 4);
+            }
+        }
+    }
+    // the stage's buffer: K-contiguous from the block's first row (the k0
+    // advance is the scalar offset), K-major from k row k0
+    __device__ __forceinline__ void load(uint32_t soff) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            reg[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[i], soff, 0));
+    }
+    __device__ __forceinline__ void store(float *lds, int tid) const {
+        if (KMAJ) {
+            const int kq = tid >> 5, r = 4 * (tid & 31);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f4 v = {reg[0][j], reg[1][j], reg[2][j], reg[3][j]};
+                *reinterpret_cast<f4 *>(lds + (kq * kSgBM + sg2_row(r + j, kq)) * 4) = v;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int f = tid + 256 * i, row = f >> 3, kq = f & 7;
+                *reinterpret_cast<f4 *>(lds + (kq * kSgBM + sg2_row(row, kq)) * 4) = reg[i];
+            }
+        }
+    }
+    __device__ __forceinline__ static f4 frag(const float *lds, int row, int q, int ss) {
+        const int kq = 4 * ss + q;
+        return *reinterpret_cast<const f4 *>(lds + (kq * kSgBM + sg2_row(row, kq)) * 4);
+    }
+};
+
+constexpr int kSg2Tile = kSgBM * kSgBK;  // 4096 floats per operand and stage
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void sgemm_mfma2_kernel(const float *__restrict__ A, int64_t lda,
+                                                          const float *__restrict__ B, int64_t ldb,
+                                                          float *__restrict__ C, int64_t ldc,
+                                                          int64_t M, int64_t N, int64_t K,
+                                                          float alpha, float beta, int tiles_m) {
+    constexpr bool AK = TA, BK = !TB;  // K-major storage of op(A) / op(B)
+    __shared__ __attribute__((aligned(16))) float smem[2 * 2 * kSg2Tile];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid & 1, wn = wid >> 1;
+    const int fr = lane & 15, q = lane >> 4;
+    const int tm = (int)blockIdx.x % tiles_m, tn = (int)blockIdx.x / tiles_m;
+    const int64_t m0 = (int64_t)tm * kSgBM, n0 = (int64_t)tn * kSgBN;
+
+    SgOp2<AK> a;
+    SgOp2<BK> b;
+    a.init(lda, tid);
+    b.init(ldb, tid);
+    // K-contiguous: base = row r0, range to the operand's last element (at
+    // most 128 rows); K-major: base = (k0, r0) per stage, range to the last
+    // element, at most the stage's 32 k rows
+    auto rsrc_rows = [&](const float *p, int64_t ld, int64_t rows, int64_t r0) {
+        const int64_t last = std::min<int64_t>(rows - 1 - r0, kSgBM - 1) * ld + K;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p + r0 * ld), 0, (int)(last * 4),
+                                                 0x00020000);
+    };
+    auto rsrc_kmaj = [&](const float *p, int64_t ld, int64_t rows, int64_t r0, int64_t k0) {
+        const int64_t last = std::min<int64_t>((K - 1 - k0) * ld + rows - r0, (int64_t)kSgBK * ld);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p + k0 * ld + r0), 0,
+                                                 (int)(last * 4), 0x00020000);
+    };
+    auto load_stage = [&](int64_t k0) {
+        if (AK) {
+            a.rsrc = rsrc_kmaj(A, lda, M, m0, k0);
+            a.load(0);
+        } else {
+            a.load((uint32_t)(k0 * 4));
+        }
+        if (BK) {
+            b.rsrc = rsrc_kmaj(B, ldb, N, n0, k0);
+            b.load(0);
+        } else {
+            b.load((uint32_t)(k0 * 4));
+        }
+    };
+    if (!AK) a.rsrc = rsrc_rows(A, lda, M, m0);
+    if (!BK) b.rsrc = rsrc_rows(B, ldb, N, n0);
+
+    f4 acc[4][4];  // [n tile][m tile]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    const int nst = (int)(K / kSgBK);
+    load_stage(0);
+    a.store(smem, tid);
+    b.store(smem + kSg2Tile, tid);
+    __syncthreads();
+    f4 fa[2][4], fb[2][4];
+    auto read_frags = [&](const float *buf, int ss, f4 (&xa)[4], f4 (&xb)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa[j] = SgOp2<AK>::frag(buf, wm * 64 + 16 * j + fr, q, ss);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xb[i] = SgOp2<BK>::frag(buf + kSg2Tile, wn * 64 + 16 * i + fr, q, ss);
+    };
+    auto mfmas = [&](const f4 (&xa)[4], const f4 (&xb)[4]) {
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[i][k4], xa[j][k4], acc[i][j], 0, 0, 0);
+    };
+    read_frags(smem, 0, fa[0], fb[0]);
+    for (int s = 0; s < nst; ++s) {
+        const float *cur = smem + (s & 1) * 2 * kSg2Tile;
+        float *nxt = smem + ((s + 1) & 1) * 2 * kSg2Tile;
+        if (s + 1 < nst) load_stage((int64_t)(s + 1) * kSgBK);  // in flight during the MFMAs
+        read_frags(cur, 1, fa[1], fb[1]);                          // super-step 1's fragments
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa[0], fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        // the next stage into the other buffer (last read before the previous
+        // barrier); after this barrier its first super-step's fragments are
+        // read while this stage's second super-step runs
+        if (s + 1 < nst) {
+            a.store(nxt, tid);
+            b.store(nxt + kSg2Tile, tid);
+        }
+        __syncthreads();
+        if (s + 1 < nst) read_frags(nxt, 0, fa[0], fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa[1], fb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // lane: m = tile row + fr, n = tile column + 4*q + e (e = 0..3)
+    const bool vec_c = (ldc & 3) == 0 && (((uintptr_t)C) & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t m = m0 + wm * 64 + 16 * j + fr;
+            const int64_t n = n0 + wn * 64 + 16 * i + 4 * q;
+            if (m >= M || n >= N) continue;
+            float *cp = C + m * ldc + n;
+            f4 v = acc[i][j];
+            if (vec_c && n + 3 < N) {
+                f4 o = {alpha * v.x, alpha * v.y, alpha * v.z, alpha * v.w};
+                if (beta != 0.0f) {
+                    const f4 c = *reinterpret_cast<const f4 *>(cp);
+                    o = f4{o.x + beta * c.x, o.y + beta * c.y, o.z + beta * c.z, o.w + beta * c.w};
+                }
+                *reinterpret_cast<f4 *>(cp) = o;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (n + e >= N) break;
+                    const float o = alpha * v[e];
+                    cp[e] = beta != 0.0f ? o + beta * cp[e] : o;
+                }
+            }
+        }
+}
+
 // Any strides: one thread per output, k in order with fused multiply-adds.
 __global__ void sgemm_simple_kernel(int transa, int transb, const float *__restrict__ A, int64_t lda,
                                     const float *__restrict__ B, int64_t ldb, float *__restrict__ C,
@@ -251,6 +443,20 @@ extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k
     const int64_t tm = ceil_div(m, kSgBM), tn = ceil_div(n, kSgBN);
     RNN_REQUIRE(tm * tn <= 0x7fffffffLL && tm < 0x7fffffffLL, "%s: too many tiles", name);
     const unsigned grid = (unsigned)(tm * tn);
+    // K % 32 == 0, and row strides and K below 4M floats (the buffer ranges of
+    // a block or a stage stay under 2 GiB): the single-layout kernel
+    if (k % kSgBK == 0 && k < (int64_t(1) << 22) && lda < (int64_t(1) << 22) &&
+        ldb < (int64_t(1) << 22)) {
+        if (!transa && !transb)
+            sgemm_mfma2_kernel<false, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+        else if (!transa && transb)
+            sgemm_mfma2_kernel<false, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+        else if (transa && !transb)
+            sgemm_mfma2_kernel<true, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+        else
+            sgemm_mfma2_kernel<true, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
+        return check_launch(name);
+    }
     if (!transa && !transb)
         sgemm_mfma_kernel<false, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
     else if (!transa && transb)
