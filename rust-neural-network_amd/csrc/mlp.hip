@@ -70,7 +70,7 @@ __device__ __forceinline__ void mlp_load_tile(const MlpLayer &L, int t, int lane
 __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *__restrict__ x,
                                                                   int64_t M, MlpArgs args,
                                                                   float *__restrict__ y) {
-    __shared__ float xf[kMlpRows][kMlpMaxDim];                            // running activation
+    __shared__ __attribute__((aligned(16))) float xf[kMlpRows][kMlpMaxDim];  // running activation
     __shared__ __attribute__((aligned(16))) int8_t xq[kMlpRows][kMlpMaxDim + 64];  // its codes
     __shared__ float sa[kMlpRows];                                        // row scales
     const int tid = threadIdx.x, wid = tid / 64, lane = tid % 64;
@@ -137,36 +137,37 @@ __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *_
             if (have_nxt) mlp_load_tile<kMlpPrefetchKb>(Ln, wid, lane, nxt);
         }
         // quantize: one wave per row, max over the row (order-independent),
-        // then the codes, zero-padded to whole 64-k blocks. Four elements per
-        // lane per step, so that four independent LDS reads and divisions
-        // are in flight instead of one dependent chain.
+        // then the codes, zero-padded to whole 64-k blocks. A lane takes 4
+        // consecutive elements per step (K % 16 == 0: a quad is wholly inside
+        // or past K): one 16-byte LDS read, 4 codes packed into one 4-byte
+        // write. q = round(x / s) through the reciprocal with the exact
+        // division only next to a half-integer (round_quotient), the same
+        // integer as the IEEE quotient rounded.
         for (int r = wid; r < kMlpRows; r += kMlpWaves) {
             float mx = 0.0f;
-            for (int c0 = 0; c0 < 64 * kb_n; c0 += 256) {
-                float v[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int c = c0 + 64 * u + lane;
-                    v[u] = c < K ? xf[r][c] : 0.0f;
-                }
-#pragma unroll
-                for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fabsf(v[u]));
+            for (int c0 = 4 * lane; c0 < K; c0 += 256) {
+                const float4 v = *reinterpret_cast<const float4 *>(&xf[r][c0]);
+                mx = fmaxf(mx, fabsf(v.x));
+                mx = fmaxf(mx, fabsf(v.y));
+                mx = fmaxf(mx, fabsf(v.z));
+                mx = fmaxf(mx, fabsf(v.w));
             }
             mx = wave_max(mx);
             const float s = mx > 0.0f ? mx / 127.0f : 1.0f;
+            const float inv = __builtin_amdgcn_rcpf(s);
             if (lane == 0) sa[r] = s;
-            for (int c0 = 0; c0 < 64 * kb_n; c0 += 256) {
-                float v[4];
+            for (int c0 = 4 * lane; c0 < 64 * kb_n; c0 += 256) {
+                uint32_t packed = 0u;
+                if (c0 < K) {
+                    const float4 v = *reinterpret_cast<const float4 *>(&xf[r][c0]);
+                    const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int c = c0 + 64 * u + lane;
-                    v[u] = c < K ? xf[r][c] : 0.0f;
+                    for (int u = 0; u < 4; ++u) {
+                        const float qv = clamp_rs(round_quotient(e[u], s, inv), -128.0f, 127.0f);
+                        packed |= (uint32_t)(uint8_t)to_i8_rs(qv) << (8 * u);
+                    }
                 }
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int c = c0 + 64 * u + lane;
-                    if (c < 64 * kb_n) xq[r][c] = c < K ? quant_i8(v[u], s) : (int8_t)0;
-                }
+                *reinterpret_cast<uint32_t *>(&xq[r][c0]) = packed;
             }
         }
         lds_barrier();

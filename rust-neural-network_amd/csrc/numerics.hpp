@@ -30,6 +30,21 @@ __device__ __forceinline__ int8_t quant_i8(float v, float s) {
     return quant_i8_from_ratio(v / s);
 }
 
+// round(rv / scale) with the reference's rounding (IEEE-rounded quotient, then
+// f32::round = half away from zero) from a multiply by inv ~= 1/scale
+// (v_rcp_f32, 1 ulp): t = rv * inv is within 3 * 2^-23 |t| of the rounded
+// quotient, so whenever t is farther than 4e-6 * (1 + |t|) from a
+// half-integer both round to the same integer, and rint(t) is that integer
+// (rint and round differ only at exact halves). Near a half-integer the exact
+// division decides.
+__device__ __forceinline__ float round_quotient(float rv, float scale, float inv) {
+    const float t = rv * inv;
+    const float r = rintf(t);
+    if (__builtin_expect(fabsf(fabsf(t - r) - 0.5f) > __builtin_fmaf(fabsf(t), 4.0e-6f, 4.0e-6f), 1))
+        return r;
+    return roundf(rv / scale);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -118,6 +118,34 @@ def test_w8a8_mlp_one_launch_matches_chain(dev, hip, m, dims, relu):
     np.testing.assert_array_equal(host(model.forward_per_layer(to_dev(x, dev), relu)), h)
 
 
+def test_w8a8_mlp_quantization_edges(dev, hip):
+    """The chain's per-row quantization takes the reciprocal path with the
+    exact division next to half-integers: rows whose quotients are exact
+    halves (max 127 -> scale 1: 0.5, -2.5, 126.5 round away from zero), a
+    row of subnormal magnitude, an all-zero row and a row with an infinity
+    and a NaN must give the oracle chain's bits."""
+    dims = (64, 48, 16)
+    params = []
+    for i, (fi, fo) in enumerate(zip(dims[:-1], dims[1:])):
+        params += [W.weights(fo, fi, seed=260 + i), W.weights(1, fo, seed=270 + i)[0]]
+    x = W.activations(6, dims[0], seed=281)
+    x[0, :] = 0.0
+    x[0, :8] = [127.0, 0.5, -2.5, 126.5, 1.5, -0.5, 63.5, -126.5]
+    x[1, :] *= 1e-39                                          # subnormal scale
+    x[2, :] = 0.0
+    x[3, 5], x[3, 9] = np.inf, 2.0
+    x[4, 7] = np.nan
+    x[5, :] = np.float32(0.5) * np.arange(64, dtype=np.float32) - 16.0   # many halves
+    layers, h = [], x
+    for i in range(len(dims) - 1):
+        wq, sw = O.quant_rows_i8(params[2 * i])
+        layers.append((to_dev(wq, dev), to_dev(sw, dev), to_dev(params[2 * i + 1], dev)))
+        aq, sa = O.quant_rows_i8(h)
+        h, _ = O.w8a8_linear(aq, sa, wq, sw, params[2 * i + 1], i < len(dims) - 2)
+    got = host(hip.w8a8_mlp(to_dev(x, dev), layers))
+    np.testing.assert_array_equal(got, h)
+
+
 def test_w8a8_mlp_unsupported_chains_fall_back(dev, hip):
     w = [W.weights(24, 40, seed=90), W.weights(8, 24, seed=91)]    # 40 % 16 != 0
     qs = [O.quant_rows_i8(a) for a in w]
