@@ -143,6 +143,7 @@ __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *_
         // write. q = round(x / s) through the reciprocal with the exact
         // division only next to a half-integer (round_quotient), the same
         // integer as the IEEE quotient rounded.
+#pragma unroll  // (the wave's two rows: their latency chains overlap)
         for (int r = wid; r < kMlpRows; r += kMlpWaves) {
             float mx = 0.0f;
             for (int c0 = 4 * lane; c0 < K; c0 += 256) {

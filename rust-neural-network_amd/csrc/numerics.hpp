@@ -45,10 +45,12 @@ __device__ __forceinline__ float round_quotient(float rv, float scale, float inv
     return roundf(rv / scale);
 }
 
+// Max over the (whole, active) wave of non-negative, non-NaN floats -- every
+// caller folds |x| with fmaxf, which drops NaN as f32::max does. Such floats
+// order as their bit patterns do as unsigned integers, so the reduction runs
+// on DPP lane moves instead of six LDS permute round trips.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    return __uint_as_float(__reduce_max_sync(~0ull, __float_as_uint(v)));
 }
 
 // Block-wide max of non-negative values; `red` holds BLOCK/64 floats.
