@@ -450,6 +450,8 @@ def bench_mlp(H, W, dev, steps, with_cpu):
            "us_graph_per_layer_launches": round(ms_layers * 1e3, 2),
            "per_layer_bit_identical": same,
            "ops": ops, "launches": 1, "batch": W.MLP_BATCH, "layers": list(W.MLP_LAYERS),
+           "weight_bytes": sum(a * b + 4 * b + 4 * b for a, b in zip(W.MLP_LAYERS[:-1], W.MLP_LAYERS[1:])),
+           "traffic": traffic_for("int8_mlp_784_256_128_10"),
            "kernel": "w8a8_mlp_kernel (rnn_w8a8_mlp: the whole chain in one launch, "
                      "activations in LDS between layers)",
            "timing": "us_graph: HIP graph replay of the whole forward; us_eager: Python calls, "
@@ -628,9 +630,11 @@ def bench_rq_attention(H, W, dev, steps):
     torch.cuda.empty_cache()
     return {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
             "bytes": nbytes, "bytes_read_with_padding": read,
+            "traffic": traffic_for("rotorquant_kv_attention"),
             "kernel": "rq_kv_attn_kernel (scores and V in the rotated domain)",
             "batch1": {"us": round(ms1 * 1e3, 2), "bytes": nbytes1,
                        "frac_hbm": round(nbytes1 / (ms1 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                       "traffic": traffic_for("rotorquant_kv_attention_batch1"),
                        "note": "32 queries: sequence split over workgroups, merged by the last split"},
             "f32_kv_sdpa_us": round(ms_f32 * 1e3, 2),
             "f32_kv_bytes": 2 * bh * seq * dim * 4,
