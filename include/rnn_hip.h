@@ -322,13 +322,14 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
  * for m >= 5 with in_f a multiple of 512 (4-bit), 256 (8-bit) or 128
  * (16-bit) a GEMV on MFMA that takes all m rows at once: for INT4, GGUF Q4,
  * INT8, GGUF Q8_0 and BF16 weights whose groups are multiples of 128 (4-bit),
- * 64 (8-bit) elements dividing in_f (or whole rows), with in_f a multiple of
- * 1024 (4-bit), 512 (8-bit) or 256 (bf16), the bf16 MFMA GEMV (x split
- * exactly into three bf16 parts in registers, codes exact in bf16, each
- * group's sum scaled once, K split over up to 8 workgroups whose partial
- * sums are added in a fixed order in stream-ordered scratch;
- * RNN_ALGO_GEMV_BF16 forces it; AUTO also takes it for m = 3, 4 when every
- * CU gets at least two 16-row tiles of W), else
+ * 64 (8-bit) elements dividing in_f (or whole rows), or are 32 elements
+ * (GGUF Q4_0 / Q8_0 blocks), with in_f a multiple of 1024 (4-bit), 512
+ * (8-bit) or 256 (bf16), the bf16 MFMA GEMV (x split exactly into three bf16
+ * parts in registers, codes exact in bf16, each group's sum scaled once, K
+ * split over up to 8 workgroups whose partial sums are added in a fixed order
+ * in stream-ordered scratch; RNN_ALGO_GEMV_BF16 forces it; AUTO also takes it
+ * for 4-bit codes at m = 3, 4 when every CU gets at least two 16-row tiles of
+ * W), else
  * the f32 MFMA GEMV (RNN_ALGO_GEMV_MFMA forces it); else the VALU GEMV
  * (m <= 4, or per 4 rows); otherwise dequantize
  * into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV forces the

@@ -754,7 +754,16 @@ constexpr int kBf16Waves = 8, kBf16MaxParts = 8;
 // (waves_per_eu: the launch has one workgroup of 8 waves per CU, so the
 // register budget is that of 2 waves per SIMD; without it the compiler
 // trades the up-front loads for a higher occupancy that is never used.)
-template <int KIND, int TPW, bool ONE, bool SCALED, bool BIAS>
+//
+// SC: 0 unscaled (BF16), 1 one scale per chunk (groups of whole chunks or
+// rows), 2 groups of 32 elements inside a chunk (GGUF Q4_0 / Q8_0 blocks):
+// every MFMA step then takes one group. A step sums 8 elements from each of
+// the 4 lane groups q (lanes 16q .. 16q+15), so after the 16-byte loads the
+// lanes trade dwords: int8 pieces swap halves between lane groups q and q+2
+// (elements 8q' .. of group j land in step j), 4-bit pieces (one whole group
+// per lane group) are transposed 4 x 4 across the lane groups; both through
+// the gfx950 lane-swap instructions. x is read in the matching order.
+template <int KIND, int TPW, bool ONE, int SC, bool BIAS>
 __global__ __launch_bounds__(kBf16Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void qt_gemv_bf16_kernel(
     const float *__restrict__ x, int mrows, int64_t K, const uint8_t *__restrict__ data,
@@ -764,6 +773,9 @@ void qt_gemv_bf16_kernel(
     constexpr int EP = Fmt<KIND>::EP;  // elements per 16-byte piece
     constexpr int JS = EP / 8;         // MFMA steps per chunk
     constexpr int NW = kBf16Waves;
+    constexpr bool SCALED = SC != 0, G32 = SC == 2;
+    static_assert(!G32 || KIND == KIND_I4 || KIND == KIND_I8, "32-element groups: 4- or 8-bit codes");
+    constexpr int NSC = G32 ? JS : 1;  // scales per tile and chunk
     // Several chunks per wave (!ONE): x is loaded in whole-row runs (a load
     // instruction reads 1 KiB of consecutive bytes: 64/EP rows of the chunk)
     // and regrouped into the fragment layout through the wave's LDS slice.
@@ -795,6 +807,13 @@ void qt_gemv_bf16_kernel(
     // range check covers: rows past mrows read zero)
     const uint32_t xoff = STAGE ? (uint32_t)(((lane / EP) * K + (lane % EP) * 4) * 4)
                                 : (uint32_t)((i * K + q * EP) * 4);
+    // element offset in the chunk of the lane's x float4 u (steps j = u / 2)
+    auto xfo = [&](int u) -> int {
+        if constexpr (G32)
+            return 32 * (u / 2) + (EP == 16 ? 16 * (q & 1) + 8 * (q >> 1) : 8 * q) + 4 * (u % 2);
+        else
+            return q * EP + 4 * u;
+    };
     const uint32_t c0 = (sp * NW + wid) * cpw;  // this wave's first chunk
     // per tile: the lane's byte offset within the range (row 16t + i, piece
     // q of a chunk) and its row's first scale index
@@ -805,12 +824,13 @@ void qt_gemv_bf16_kernel(
         voff[t] = (16 * t + i) * rowbytes + 16 * q;
         const int64_t n = r0 + std::min(16 * t + i, nrows - 1);
         gbase[t] = !SCALED ? 0 : (kg ? n * (int64_t)kg : (int64_t)((uint32_t)n / rpg));
-        if (SCALED) gbase[t] = std::min<int64_t>(gbase[t], ns - 1);
+        // (G32: the row's first scale, which keeps the chunk's vector load aligned)
+        if (SCALED) gbase[t] = std::min<int64_t>(gbase[t], G32 ? ns - kg : ns - 1);
     }
     struct Chunk {
         f4v xf[EP / 4];  // x[i][c*4EP + q*EP ..+ EP), or (staged) whole-row runs
         v4i w[TPW];
-        float sc[TPW];
+        float sc[TPW][NSC];
     };
     auto load = [&](Chunk &ch, uint32_t c) {
 #pragma unroll
@@ -818,18 +838,27 @@ void qt_gemv_bf16_kernel(
             ch.xf[u] = __builtin_bit_cast(
                 f4v, STAGE ? __builtin_amdgcn_raw_buffer_load_b128(
                                  xr, xoff + (uint32_t)(u * XRPL * K * 4), c * (4 * EP * 4), 0)
-                           : __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 16 * u,
-                                                                   c * (4 * EP * 4), 0));
+                           : __builtin_amdgcn_raw_buffer_load_b128(
+                                 xr, G32 ? (uint32_t)((i * K + xfo(u)) * 4) : xoff + 16 * u,
+                                 c * (4 * EP * 4), 0));
         // chunk c starts 64 bytes per chunk into every row (4 pieces); the
-        // group of a chunk is uniform (groups hold whole chunks or rows)
-        const uint32_t grp = kg ? c / cpg : 0u;
+        // group of a chunk is uniform (groups hold whole chunks or rows), or
+        // (G32) the chunk holds the row's groups JS c .. JS c + JS - 1
+        const uint32_t grp = G32 ? c * JS : (kg ? c / cpg : 0u);
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
             ch.w[t] = __builtin_bit_cast(
                 v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, voff[t], c * 64u, 2 /* nt */));
-            if (SCALED) {
+            if constexpr (G32) {
+                // (a row's scales start at a multiple of kg, itself a multiple
+                // of 16: the JS-float load is aligned)
+                typedef float fjv __attribute__((ext_vector_type(JS)));
+                const fjv sv = *reinterpret_cast<const fjv *>(scales + gbase[t] + grp);
+#pragma unroll
+                for (int j = 0; j < JS; ++j) ch.sc[t][j] = sv[j];
+            } else if (SCALED) {
                 const int64_t gi = gbase[t] + grp;  // (a row's groups are in range)
-                ch.sc[t] = scales[gi];
+                ch.sc[t][0] = scales[gi];
             }
         }
     };
@@ -848,7 +877,7 @@ void qt_gemv_bf16_kernel(
                 *reinterpret_cast<f4v *>(xw + (u * XRPL + lane / EP) * XP + (lane % EP) * 4) = ch.xf[u];
 #pragma unroll
             for (int u = 0; u < EP / 4; ++u)
-                xfr[u] = *reinterpret_cast<const f4v *>(xw + i * XP + q * EP + 4 * u);
+                xfr[u] = *reinterpret_cast<const f4v *>(xw + i * XP + xfo(u));
         } else {
 #pragma unroll
             for (int u = 0; u < EP / 4; ++u) xfr[u] = ch.xf[u];
@@ -870,24 +899,50 @@ void qt_gemv_bf16_kernel(
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
             float v[EP];
-            if (KIND != KIND_BF16) decode_piece<KIND>(ch.w[t], v, nullptr);
+            v4i w = ch.w[t];
+            if constexpr (G32) {
+                // lane group q's dwords to the steps of their groups: swap the
+                // upper 32 lanes of one register with the lower 32 of another
+                // (lane groups 2, 3 <-> 0, 1), then (4-bit) odd rows of 16
+                // lanes of one with even rows of the other
+                const auto s02 = __builtin_amdgcn_permlane32_swap((uint32_t)w[0], (uint32_t)w[2], false, false);
+                const auto s13 = __builtin_amdgcn_permlane32_swap((uint32_t)w[1], (uint32_t)w[3], false, false);
+                w = v4i{(int)s02[0], (int)s13[0], (int)s02[1], (int)s13[1]};
+                if constexpr (EP == 32) {
+                    const auto s01 = __builtin_amdgcn_permlane16_swap((uint32_t)w[0], (uint32_t)w[1], false, false);
+                    const auto s23 = __builtin_amdgcn_permlane16_swap((uint32_t)w[2], (uint32_t)w[3], false, false);
+                    w = v4i{(int)s01[0], (int)s01[1], (int)s23[0], (int)s23[1]};
+                }
+            }
+            if (KIND != KIND_BF16) decode_piece<KIND>(w, v, nullptr);
             f4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < JS; ++j) {
                 v4i b;
                 if (KIND == KIND_BF16) {
-                    b = ch.w[t];  // already 8 bf16
+                    b = w;  // already 8 bf16
                 } else {
 #pragma unroll
                     for (int d = 0; d < 4; ++d) b[d] = (int)bf16_pair(v[8 * j + 2 * d], v[8 * j + 2 * d + 1]);
                 }
+                if constexpr (G32) {  // a step is one group: its own sum and scale
+                    f4v aj = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int p = 0; p < kSplitParts; ++p)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a[j][p]),
-                                                                 __builtin_bit_cast(bf8, b), acc, 0, 0, 0);
+                    for (int p = 0; p < kSplitParts; ++p)
+                        aj = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a[j][p]),
+                                                                    __builtin_bit_cast(bf8, b), aj, 0, 0, 0);
+                    const float s = KIND == KIND_I4 ? ch.sc[t][j] * 0.0625f : ch.sc[t][j];
+                    tot[t] = tot[t] + aj * s;
+                } else {
+#pragma unroll
+                    for (int p = 0; p < kSplitParts; ++p)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a[j][p]),
+                                                                     __builtin_bit_cast(bf8, b), acc, 0, 0, 0);
+                }
             }
-            if (SCALED) {
-                const float s = KIND == KIND_I4 ? ch.sc[t] * 0.0625f : ch.sc[t];
+            if constexpr (G32) {
+            } else if (SCALED) {
+                const float s = KIND == KIND_I4 ? ch.sc[t][0] * 0.0625f : ch.sc[t][0];
                 tot[t] = tot[t] + acc * s;
             } else {
                 tot[t] = tot[t] + acc;
@@ -1208,28 +1263,29 @@ static size_t bf16_workspace(int64_t N) {
 }
 static size_t bf16_counter_bytes(int64_t N) { return 4 * (size_t)ceil_div(N, 16) + 256; }
 
-template <int KIND, int TPW, bool ONE, bool SCALED>
+template <int KIND, int TPW, bool ONE, int SC>
 static void launch_bf16_t(const float *xs, int mrows, int64_t K, const uint8_t *data,
                           const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
                           float *y, const Bf16Plan &pl, float *wpart, uint32_t *cnt, hipStream_t st) {
     constexpr int EP = Fmt<KIND>::EP;
+    constexpr bool SCALED = SC != 0;
     const uint32_t kg = !SCALED ? 0u : (K % g == 0 ? (uint32_t)(K / g) : 0u);
     const uint32_t rpg = !SCALED ? 1u : (kg ? 1u : (uint32_t)(g / K));
-    const uint32_t cpg = kg ? (uint32_t)(g / (4 * EP)) : 1u;  // chunks per group
+    const uint32_t cpg = kg && SC == 1 ? (uint32_t)(g / (4 * EP)) : 1u;  // chunks per group
     const unsigned grid = (unsigned)(pl.R * pl.S);
     if (bias)
-        qt_gemv_bf16_kernel<KIND, TPW, ONE, SCALED, true><<<grid, kBf16Waves * 64, 0, st>>>(
+        qt_gemv_bf16_kernel<KIND, TPW, ONE, SC, true><<<grid, kBf16Waves * 64, 0, st>>>(
             xs, mrows, K, data, scales, ns, cpg, kg, rpg, N, pl.S, pl.cpw, wpart, cnt, bias, y);
     else
-        qt_gemv_bf16_kernel<KIND, TPW, ONE, SCALED, false><<<grid, kBf16Waves * 64, 0, st>>>(
+        qt_gemv_bf16_kernel<KIND, TPW, ONE, SC, false><<<grid, kBf16Waves * 64, 0, st>>>(
             xs, mrows, K, data, scales, ns, cpg, kg, rpg, N, pl.S, pl.cpw, wpart, cnt, bias, y);
 }
 
-template <int KIND, bool SCALED>
+template <int KIND, int SC>
 static void launch_bf16_tpw(const float *xs, int mrows, int64_t K, const uint8_t *data,
                             const float *scales, int64_t ns, int64_t g, int64_t N, const float *bias,
                             float *y, const Bf16Plan &pl, float *wp, uint32_t *cnt, hipStream_t st) {
-#define RNN_BF16_T(T, O) launch_bf16_t<KIND, T, O, SCALED>(xs, mrows, K, data, scales, ns, g, N, bias, y, pl, wp, cnt, st)
+#define RNN_BF16_T(T, O) launch_bf16_t<KIND, T, O, SC>(xs, mrows, K, data, scales, ns, g, N, bias, y, pl, wp, cnt, st)
     if (pl.cpw != 1) {
         switch (pl.TPW) {
         case 1: RNN_BF16_T(1, false); break;
@@ -1272,7 +1328,13 @@ static int launch_bf16(const float *x, int mrows, int64_t K, const uint8_t *data
     uint8_t *base = static_cast<uint8_t *>(ws);
     uint32_t *cnt = reinterpret_cast<uint32_t *>(base);
     float *wpart = base ? reinterpret_cast<float *>(base + bf16_counter_bytes(N)) : nullptr;
-    launch_bf16_tpw<KIND, SCALED>(x, mrows, K, data, scales, ns, g, N, bias, y, pl, wpart, cnt, st);
+    // groups of 32 inside a chunk (GGUF blocks): a scale per MFMA step
+    if (SCALED && 4 * EP > 32 && g == 32)
+        launch_bf16_tpw<KIND, KIND == KIND_BF16 ? 0 : 2>(x, mrows, K, data, scales, ns, g, N, bias, y, pl,
+                                                         wpart, cnt, st);
+    else
+        launch_bf16_tpw<KIND, SCALED ? 1 : 0>(x, mrows, K, data, scales, ns, g, N, bias, y, pl, wpart,
+                                              cnt, st);
     const int rc = check_launch(name);
     if (workspace || !ws) return rc;
     const int rf = check_hip(hipFreeAsync(ws, st), name);
@@ -1344,18 +1406,20 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
     const bool fits_bf16 =
         fits && m <= 16 && (kind == KIND_I4 || kind == KIND_I8 || kind == KIND_BF16) &&
         in_f % (kBf16Waves * 4 * ep) == 0 &&
-        (!scaled || (group % (4 * ep) == 0 && in_f % group == 0) || group % in_f == 0) &&
+        (!scaled || (group % (4 * ep) == 0 && in_f % group == 0) || group % in_f == 0 ||
+         (group == 32 && kind != KIND_BF16)) &&
         bf16_plan(m, in_f, out_f, ep).S > 0 && 64 * in_f * 16 / ep < (int64_t(1) << 31) &&
         16 * in_f * 4 < (int64_t(1) << 31);
-    // AUTO takes it for m >= 5, and for m = 3, 4 when every CU gets at least
-    // two row tiles (measured, INT4 g128 x 4096: m = 4 at N = 11008 14.0 us
-    // against 16.3 for the VALU GEMV; at N = 4096 8.6 against 7.4)
+    // AUTO takes it for m >= 5, and for 4-bit codes at m = 3, 4 when every
+    // CU gets at least two row tiles (measured, 4096 x 11008, m = 4: INT4 g128
+    // 14.0 us against 16.3 for the VALU GEMV, GGUF Q4_0 15.8 against 16.7;
+    // at N = 4096 INT4 8.6 against 7.4; GGUF Q8_0 22.4 against 20.1)
     const bool bf16_auto =
-        fits_bf16 && (m >= 5 || (m >= 3 && bf16_plan(m, in_f, out_f, ep).TPW >= 2));
+        fits_bf16 && (m >= 5 || (m >= 3 && kind == KIND_I4 && bf16_plan(m, in_f, out_f, ep).TPW >= 2));
     if (algo == RNN_ALGO_GEMV_BF16 || (algo == RNN_ALGO_AUTO && bf16_auto)) {
         RNN_REQUIRE(fits_bf16, "%s: the bf16 MFMA GEMV needs INT4/Q4/INT8/Q8/BF16 weights, m <= 16, "
                     "in_f a multiple of %d, a group that is a multiple of %d dividing in_f (or a "
-                    "multiple of in_f), and 16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
+                    "multiple of in_f, or 32 for 4- and 8-bit codes), and 16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
         switch (kind) {
         case KIND_I4:
             return launch_bf16<KIND_I4, true>(x, (int)m, in_f, data, scales, n_scales, group, out_f,

@@ -143,13 +143,14 @@ def gemm_check(got, x, wdeq, bias):
 
 def bf16_gemv_fits(fmt, m, k, g):
     """The bf16 MFMA GEMV's conditions: integer codes or bf16 weights, whole
-    chunks of 4 pieces for each of 8 waves, groups of whole chunks."""
+    chunks of 4 pieces for each of 8 waves, groups of whole chunks, or groups
+    of 32 (one per MFMA step)."""
     if fmt not in (O.QF_INT4, O.QF_GGUF_Q4, O.QF_GGUF_Q4K, O.QF_INT8, O.QF_GGUF_Q8, O.QF_BF16):
         return False
     ep = 32 if O.QF_BITS[fmt] == 4 else (16 if O.QF_BITS[fmt] == 8 else 8)
     grouped = fmt != O.QF_BF16
     return (m <= 16 and k % (32 * ep) == 0 and
-            (not grouped or (g % (4 * ep) == 0 and k % g == 0) or g % k == 0))
+            (not grouped or (g % (4 * ep) == 0 and k % g == 0) or g % k == 0 or g == 32))
 
 
 @pytest.mark.parametrize("fmt", GEMV_FMTS, ids=[O.QF_NAMES[f] for f in GEMV_FMTS])
@@ -182,8 +183,11 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
 
 
 @pytest.mark.parametrize("fmt,gs", [(O.QF_INT4, 128), (O.QF_INT4, 0), (O.QF_INT8, 64),
-                                    (O.QF_INT8, 4096), (O.QF_BF16, 0), (O.QF_INT4, 512)],
-                         ids=["INT4-g128", "INT4-tensor", "INT8-g64", "INT8-rows", "BF16", "INT4-g512"])
+                                    (O.QF_INT8, 4096), (O.QF_BF16, 0), (O.QF_INT4, 512),
+                                    (O.QF_GGUF_Q8, 32), (O.QF_GGUF_Q4, 32), (O.QF_INT8, 32),
+                                    (O.QF_INT4, 32)],
+                         ids=["INT4-g128", "INT4-tensor", "INT8-g64", "INT8-rows", "BF16", "INT4-g512",
+                              "Q8_0", "Q4_0", "INT8-g32", "INT4-g32"])
 @pytest.mark.parametrize("m,k,n", [(5, 4096, 4096), (16, 4096, 5000), (9, 2048, 11008),
                                    (16, 4096, 16000), (12, 1024, 20000), (7, 4096, 30),
                                    (16, 2048, 1),
@@ -191,7 +195,8 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
                                    (16, 8192, 300), (16, 16384, 64)])
 def test_linear_forward_bf16_gemv(dev, hip, fmt, gs, m, k, n):
     """The bf16 MFMA GEMV (x split into three bf16 parts, codes exact in
-    bf16, one scale per group sum, K split over 1-8 workgroups as the
+    bf16, one scale per group sum -- for groups of 32 one per MFMA step, the
+    pieces traded between lane groups --, K split over 1-8 workgroups as the
     plan's estimate picks): 1-12 row tiles per range, one or several chunks
     per wave (x staged through LDS), row ranges that are not
     multiples of 16, fewer rows than CUs, rows of x past m; with and without
@@ -264,9 +269,9 @@ def test_linear_forward_nonfinite_x(dev, hip, m):
 
 
 def test_linear_forward_bf16_gemv_rejects(dev, hip):
-    """Forced bf16 GEMV outside its conditions: NF4 codes, a group of 32
-    (GGUF Q4_0), m = 17; and a workspace one 16-byte step too small -- an
-    RnnError, no launch."""
+    """Forced bf16 GEMV outside its conditions: NF4 codes, GGUF Q4_0 with
+    in_f = 512 (4-bit chunks need in_f % 1024 == 0), m = 17; and a workspace
+    one 16-byte step too small -- an RnnError, no launch."""
     rng = np.random.default_rng(3)
     n, k = 64, 512
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
