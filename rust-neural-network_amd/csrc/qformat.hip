@@ -1408,6 +1408,9 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
         in_f % (kBf16Waves * 4 * ep) == 0 &&
         (!scaled || (group % (4 * ep) == 0 && in_f % group == 0) || group % in_f == 0 ||
          (group == 32 && kind != KIND_BF16)) &&
+        // (a scale for every group: the kernel reads a row's scales from the
+        // row's first without the per-index clamp of a shortened array)
+        (!scaled || n_scales >= ceil_div(out_f * in_f, group)) &&
         bf16_plan(m, in_f, out_f, ep).S > 0 && 64 * in_f * 16 / ep < (int64_t(1) << 31) &&
         16 * in_f * 4 < (int64_t(1) << 31);
     // AUTO takes it for m >= 5, and for 4-bit codes at m = 3, 4 when every
@@ -1419,7 +1422,8 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
     if (algo == RNN_ALGO_GEMV_BF16 || (algo == RNN_ALGO_AUTO && bf16_auto)) {
         RNN_REQUIRE(fits_bf16, "%s: the bf16 MFMA GEMV needs INT4/Q4/INT8/Q8/BF16 weights, m <= 16, "
                     "in_f a multiple of %d, a group that is a multiple of %d dividing in_f (or a "
-                    "multiple of in_f, or 32 for 4- and 8-bit codes), and 16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
+                    "multiple of in_f, or 32 for 4- and 8-bit codes), a scale for every group, and "
+                    "16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
         switch (kind) {
         case KIND_I4:
             return launch_bf16<KIND_I4, true>(x, (int)m, in_f, data, scales, n_scales, group, out_f,

@@ -107,6 +107,32 @@ def test_dequantize_short_scales_and_odd_groups(dev, hip):
             assert np.array_equal(out.view(np.uint32), exp.view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt,gs", [(O.QF_INT4, 128), (O.QF_INT8, 64), (O.QF_INT4, 32)],
+                         ids=["INT4-g128", "INT8-g64", "INT4-g32"])
+def test_linear_forward_short_scales(dev, hip, fmt, gs):
+    """QuantizedLinear::forward with a caller-shortened scales array (the
+    reference reads scales[min(i/group, len-1)]): every fused path that takes
+    it -- the VALU GEMV, the f32-MFMA GEMV, AUTO at m = 1 and 8 -- matches the
+    dequantized weight within the GEMM bound; the bf16 GEMV, which reads a
+    row's scales as a run, refuses it when forced."""
+    rng = np.random.default_rng(gs + fmt)
+    n, k = 300, 4096
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    d, s, g = O.qt_quantize(fmt, w, gs)
+    for ns in (s.size // 2 + 3, 1):
+        sh = s[:ns]
+        wdeq = O.qt_dequantize(fmt, d, sh, g, n * k).reshape(n, k)
+        dd, sd = to_dev(d, dev), to_dev(sh, dev)
+        for m in (1, 8):
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            xd = to_dev(x, dev)
+            for algo in (None, hip.ALGO_GEMV, hip.ALGO_GEMV_MFMA):
+                kw = {} if algo is None else {"algo": algo}
+                gemm_check(host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, **kw)), x, wdeq, None)
+            with pytest.raises(hip.RnnError):
+                hip.qt_linear_forward(fmt, xd, dd, sd, g, n, algo=hip.ALGO_GEMV_BF16)
+
+
 def test_argument_errors(dev, hip):
     import torch
     x = torch.zeros(64, device=dev)
