@@ -1425,7 +1425,8 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
         fits && m <= 16 && (kind == KIND_I4 || kind == KIND_I8 || kind == KIND_BF16) &&
         in_f % (kBf16Waves * 4 * ep) == 0 &&
         (!scaled || (group % (4 * ep) == 0 && in_f % group == 0) || group % in_f == 0 ||
-         (group == 32 && kind != KIND_BF16)) &&
+         // (groups of 32: a chunk's scales come in one vector load)
+         (group == 32 && kind != KIND_BF16 && ((uintptr_t)scales % 16) == 0)) &&
         // (a scale for every group: the kernel reads a row's scales from the
         // row's first without the per-index clamp of a shortened array)
         (!scaled || n_scales >= ceil_div(out_f * in_f, group)) &&
@@ -1440,8 +1441,8 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
     if (algo == RNN_ALGO_GEMV_BF16 || (algo == RNN_ALGO_AUTO && bf16_auto)) {
         RNN_REQUIRE(fits_bf16, "%s: the bf16 MFMA GEMV needs INT4/Q4/INT8/Q8/BF16 weights, m <= 16, "
                     "in_f a multiple of %d, a group that is a multiple of %d dividing in_f (or a "
-                    "multiple of in_f, or 32 for 4- and 8-bit codes), a scale for every group, and "
-                    "16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
+                    "multiple of in_f, or 32 for 4- and 8-bit codes with 16-byte aligned scales), a "
+                    "scale for every group, and 16-byte aligned x and data", name, kBf16Waves * 4 * ep, 4 * ep);
         switch (kind) {
         case KIND_I4:
             return launch_bf16<KIND_I4, true>(x, (int)m, in_f, data, scales, n_scales, group, out_f,

@@ -314,6 +314,28 @@ def test_linear_forward_groups_of_32_few_rows(dev, hip, fmt, m):
     gemm_check(host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, algo=hip.ALGO_GEMV_BF16)), x, wdeq, None)
 
 
+def test_linear_forward_groups_of_32_unaligned_scales(dev, hip):
+    """GGUF Q8_0 at m = 8 with its scales 4 bytes past a 16-byte boundary: the
+    bf16 GEMV reads a chunk's scales in one vector load, so AUTO takes
+    another fused path (within the GEMM bound) and the forced bf16 GEMV
+    refuses the call."""
+    import torch
+    rng = np.random.default_rng(77)
+    n, k, m = 1000, 4096, 8
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    d, s, g = O.qt_quantize(O.QF_GGUF_Q8, w, 32)
+    wdeq = O.qt_dequantize(O.QF_GGUF_Q8, d, s, g, n * k).reshape(n, k)
+    buf = torch.zeros(s.size + 1, dtype=torch.float32, device=dev)
+    buf[1:] = torch.from_numpy(s).to(dev)
+    sd = buf[1:]
+    assert sd.data_ptr() % 16 == 4
+    dd, xd = to_dev(d, dev), to_dev(x, dev)
+    gemm_check(host(hip.qt_linear_forward(O.QF_GGUF_Q8, xd, dd, sd, g, n)), x, wdeq, None)
+    with pytest.raises(hip.RnnError):
+        hip.qt_linear_forward(O.QF_GGUF_Q8, xd, dd, sd, g, n, algo=hip.ALGO_GEMV_BF16)
+
+
 def test_linear_forward_bf16_gemv_rejects(dev, hip):
     """Forced bf16 GEMV outside its conditions: NF4 codes, GGUF Q4_0 with
     in_f = 512 (4-bit chunks need in_f % 1024 == 0), m = 17; and a workspace
