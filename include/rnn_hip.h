@@ -89,7 +89,8 @@ size_t rnn_igemm_workspace_size(int64_t m, int64_t k, int64_t n);
  * [k,n] (N-contiguous). Computed on signed int8 MFMA with the exact identity
  * sum (a_s8+128)*b = sum a_s8*b + 128*colsum(b). `workspace` must hold
  * rnn_igemm_workspace_size() bytes, or be NULL to let the call allocate and
- * free stream-ordered memory. */
+ * free stream-ordered memory; problems with m*n*k <= 2^28 run in one launch
+ * that stages both operands in LDS and use no workspace. */
 int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m,
               int64_t k, int64_t n, void *workspace, size_t workspace_bytes,
               void *stream);

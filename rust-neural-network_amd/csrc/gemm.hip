@@ -2110,6 +2110,124 @@ extern "C" int rnn_ternary_prepack(const uint32_t *packed, int64_t rows, int64_t
     return check_launch(name);
 }
 
+// ------------------------------------------------ igemm, small problems
+// igemm in one launch for problems whose pack / transpose / column-sum / GEMM
+// sequence would spend most of its time in its four launches (512^3: 16.9
+// us, 3.3 of them in the GEMM's MFMAs and loads). A workgroup of 4 waves
+// owns a 32 x 32 tile of c, a wave a 16 x 16 quarter. Per K chunk of 256 it
+// stages the tile's rows of a as signed bytes (x ^ 0x80, i.e. a - 128) and
+// the chunk's rows of b written transposed ([n][k]) in LDS, zero past M, N
+// and K, so that both operands' fragments are 16 consecutive k per lane
+// (one 16-byte LDS read). The column sums of b come from a second MFMA per
+// step whose A operand is all ones; the store adds 128 x that sum (the
+// identity sum (a_s8 + 128) b = sum a_s8 b + 128 colsum(b), wrapping int32).
+constexpr int kIgBM = 32, kIgBN = 32, kIgKC = 256, kIgPad = 16;
+constexpr double kIgSmallOps = 268435456.0;  // m n k at or below: one launch
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void igemm_small_kernel(const uint8_t *__restrict__ a,
+                                                          const int8_t *__restrict__ b,
+                                                          int32_t *__restrict__ c, int64_t M,
+                                                          int64_t K, int64_t N, int tiles_n) {
+    __shared__ __attribute__((aligned(16))) int8_t as[kIgBM][kIgKC + kIgPad];
+    __shared__ __attribute__((aligned(16))) int8_t bs[kIgBN][kIgKC + kIgPad];  // b transposed
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid & 1, wn = wid >> 1, fi = lane & 15, fq = lane >> 4;
+    const int64_t m0 = (int64_t)(blockIdx.x / tiles_n) * kIgBM;
+    const int64_t n0 = (int64_t)(blockIdx.x % tiles_n) * kIgBN;
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    v4i acc = {0, 0, 0, 0}, accs = {0, 0, 0, 0};  // a_s8 . b and the column sums of b
+    for (int64_t k0 = 0; k0 < K; k0 += kIgKC) {
+        {  // a: row tid / 8 of the tile, 32 bytes at (tid % 8) * 32 of the chunk
+            const int r = tid >> 3, c0 = (tid & 7) * 32;
+            const int64_t row = m0 + r;
+            uint32_t w[8];
+            if constexpr (VEC) {  // (K % 16 == 0: a 16-byte piece is wholly inside or past K)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int64_t kk = k0 + c0 + 16 * h;
+                    uint4 v = {0u, 0u, 0u, 0u};
+                    if (row < M && kk < K) {
+                        v = *reinterpret_cast<const uint4 *>(a + row * K + kk);
+                        v.x ^= 0x80808080u, v.y ^= 0x80808080u, v.z ^= 0x80808080u, v.w ^= 0x80808080u;
+                    }
+                    w[4 * h] = v.x, w[4 * h + 1] = v.y, w[4 * h + 2] = v.z, w[4 * h + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    uint32_t x = 0u;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int64_t kk = k0 + c0 + 4 * d + e;
+                        if (row < M && kk < K) x |= (uint32_t)(a[row * K + kk] ^ 0x80u) << (8 * e);
+                    }
+                    w[d] = x;
+                }
+            }
+            uint4 *dst = reinterpret_cast<uint4 *>(&as[r][c0]);
+            dst[0] = uint4{w[0], w[1], w[2], w[3]};
+            dst[1] = uint4{w[4], w[5], w[6], w[7]};
+        }
+        {  // b: k row tid of the chunk, columns n0 .. n0+31, written transposed
+            const int64_t kk = k0 + tid;
+            int8_t v[kIgBN];
+            if constexpr (VEC) {  // (N % 16 == 0: a 16-byte half is wholly inside or past N)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint4 u = {0u, 0u, 0u, 0u};
+                    if (kk < K && n0 + 16 * h < N)
+                        u = *reinterpret_cast<const uint4 *>(b + kk * N + n0 + 16 * h);
+                    const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) v[16 * h + j] = (int8_t)(uw[j / 4] >> (8 * (j % 4)));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < kIgBN; ++j)
+                    v[j] = kk < K && n0 + j < N ? b[kk * N + n0 + j] : (int8_t)0;
+            }
+#pragma unroll
+            for (int j = 0; j < kIgBN; ++j) bs[j][tid] = v[j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kb = 0; kb < kIgKC / 64; ++kb) {
+            const v4i af = *reinterpret_cast<const v4i *>(&as[16 * wm + fi][64 * kb + 16 * fq]);
+            const v4i bf = *reinterpret_cast<const v4i *>(&bs[16 * wn + fi][64 * kb + 16 * fq]);
+            // D[m][n]: A = rows of a, B = columns of b
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, acc, 0, 0, 0);
+            accs = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, bf, accs, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // lane: column n0 + 16 wn + fi, rows m0 + 16 wm + 4 fq .. + 3
+    const int64_t col = n0 + 16 * wn + fi;
+    if (col >= N) return;
+    const int32_t av[4] = {acc.x, acc.y, acc.z, acc.w}, sv[4] = {accs.x, accs.y, accs.z, accs.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + 16 * wm + 4 * fq + r;
+        if (row < M) c[row * N + col] = (int32_t)((uint32_t)av[r] + 128u * (uint32_t)sv[r]);
+    }
+}
+
+static bool igemm_small(int64_t m, int64_t k, int64_t n) {
+    return (double)m * (double)n * (double)k <= kIgSmallOps;
+}
+
+static int launch_igemm_small(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m, int64_t k,
+                              int64_t n, hipStream_t st, const char *name) {
+    const int64_t tm = ceil_div(m, kIgBM), tn = ceil_div(n, kIgBN);
+    RNN_REQUIRE(tm * tn <= 0x7fffffffLL, "%s: too many tiles", name);
+    const bool vec = k % 16 == 0 && n % 16 == 0 && aligned16(a) && aligned16(b);
+    if (vec)
+        igemm_small_kernel<true><<<(unsigned)(tm * tn), 256, 0, st>>>(a, b, c, m, k, n, (int)tn);
+    else
+        igemm_small_kernel<false><<<(unsigned)(tm * tn), 256, 0, st>>>(a, b, c, m, k, n, (int)tn);
+    return check_launch(name);
+}
+
 static int64_t igemm_kp(int64_t k) { return (k + 63) / 64 * 64; }
 
 extern "C" size_t rnn_igemm_workspace_size(int64_t m, int64_t k, int64_t n) {
@@ -2166,6 +2284,9 @@ extern "C" int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t 
     if (k == 0) return igemm_empty(c, m, n, st, name);
     RNN_REQUIRE(a && b, "%s: null operand", name);
     const size_t need = rnn_igemm_workspace_size(m, k, n);
+    RNN_REQUIRE(!workspace || workspace_bytes >= need, "%s: workspace %zu < %zu bytes", name,
+                workspace_bytes, need);
+    if (igemm_small(m, k, n)) return launch_igemm_small(a, b, c, m, k, n, st, name);
     if (workspace != nullptr) {
         RNN_REQUIRE(workspace_bytes >= need, "%s: workspace %zu < %zu bytes", name,
                     workspace_bytes, need);
@@ -2221,6 +2342,7 @@ extern "C" int rnn_igemm_noalloc(const uint8_t *a, const int8_t *b, int32_t *c, 
                          "%zu-byte device array (use rnn_igemm)",
                          name, (long long)m, (long long)k, (long long)n, need,
                          (size_t)RNN_IGEMM_NOALLOC_MAX_BYTES);
+    if (igemm_small(m, k, n)) return launch_igemm_small(a, b, c, m, k, n, st, name);
     void *ws = nullptr;
     RNN_TRY(scratch_address(&ws, name));
     return igemm_on_workspace(a, b, c, m, k, n, ws, st, name);

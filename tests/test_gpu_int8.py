@@ -113,7 +113,10 @@ def test_igemm_lcg_shapes(dev, hip, shape):
 
 
 @pytest.mark.parametrize("m,k,n", [(512, 512, 512), (17, 300, 1000), (300, 4096, 129),
-                                   (7, 2048, 300), (16, 4096, 5000)])
+                                   (7, 2048, 300), (16, 4096, 5000),
+                                   # m n k above 2^28: pack + transpose + column sums + the
+                                   # 64 x 64 and the 128 x 128 tiled GEMMs
+                                   (1024, 512, 1024), (2048, 128, 2048)])
 def test_igemm_full_u8_range(dev, hip, m, k, n):
     # benches/core_ops.rs:152-153 inputs: a = i % 251 (u8), b = i % 255 (as i8)
     a = (np.arange(m * k) % 251).astype(np.uint8).reshape(m, k)
@@ -123,6 +126,23 @@ def test_igemm_full_u8_range(dev, hip, m, k, n):
     got = host(hip.igemm(to_dev(a, dev), to_dev(b, dev), m, k, n, workspace=ws))
     exp, _ = O.igemm(a, b, m, k, n, 8)
     assert np.array_equal(got, exp)
+
+
+def test_igemm_small_unaligned_operands(dev, hip):
+    """The one-launch kernel of small problems with a and b one byte past a
+    16-byte boundary (byte loads instead of 16-byte ones), K over two 256-k
+    chunks and a ragged last tile."""
+    import torch
+    m, k, n = 45, 300, 70
+    a, b = lcg_case(m, k, n)
+    ab = torch.zeros(m * k + 1, dtype=torch.uint8, device=dev)
+    bb = torch.zeros(k * n + 1, dtype=torch.int8, device=dev)
+    ab[1:] = torch.from_numpy(a.ravel()).to(dev)
+    bb[1:] = torch.from_numpy(b.ravel()).to(dev)
+    da, db = ab[1:].view(m, k), bb[1:].view(k, n)
+    assert da.data_ptr() % 16 == 1 and db.data_ptr() % 16 == 1
+    got = host(hip.igemm(da, db, m, k, n))
+    assert np.array_equal(got, O.igemm_scalar(a, b, m, k, n))
 
 
 def test_igemm_wrapping(dev, hip):

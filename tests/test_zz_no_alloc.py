@@ -24,9 +24,12 @@ def _case(m, k, n, seed):
 @pytest.mark.gpu
 def test_igemm_noalloc_matches_igemm_on_consecutive_calls(dev, hip):
     import torch
-    # tiled path (m > 16), then a smaller GEMV-path call (m <= 16, k not a
-    # multiple of 64), then a larger k again
-    for m, k, n, seed in ((96, 1000, 320, 1), (5, 70, 33, 2), (40, 4096, 64, 3)):
+    # (m n k above 2^28 runs on the array: the tiled path (m > 16), then a
+    # smaller tiled call, then the GEMV path (m <= 16, k not a multiple of
+    # 64); a small problem last, which takes the one-launch kernel and no
+    # workspace)
+    for m, k, n, seed in ((600, 1000, 640, 1), (400, 900, 800, 2), (12, 3000, 8000, 3),
+                          (5, 70, 33, 4)):
         a, b = _case(m, k, n, seed)
         da, db = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
         ws = torch.empty(hip.igemm_workspace_size(m, k, n), dtype=torch.uint8, device=dev)
