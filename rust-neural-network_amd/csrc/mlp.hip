@@ -9,7 +9,8 @@
 // layers, passed through max(., 0) (src/tensor.rs:2025-2032). The result is
 // bit-identical to chaining rnn_quant_rows_i8 and rnn_w8a8_linear per layer.
 //
-// A workgroup owns 16 rows for the whole chain: the activation stays in LDS
+// A workgroup owns up to 16 rows for the whole chain (fewer when the batch
+// would not fill the CUs otherwise): the activation stays in LDS
 // (f32 for the quantization pass, int8 codes for the MFMAs), so a layer's
 // output never goes to HBM and the chain costs one launch instead of two per
 // layer. Each of the 8 waves takes 16-column tiles of a layer; a tile's
@@ -67,16 +68,25 @@ __device__ __forceinline__ void mlp_load_tile(const MlpLayer &L, int t, int lane
     }
 }
 
+// rows: rows of x per workgroup (1 .. 16). The MFMAs always take a 16-row
+// block; rows past `rows` hold zero codes and their outputs are dropped.
+// Fewer rows per workgroup spread a small batch over more CUs: each
+// workgroup still streams every weight, but its quantization passes (a
+// wave's rows) and its share of x shrink.
 __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *__restrict__ x,
-                                                                  int64_t M, MlpArgs args,
+                                                                  int64_t M, int rows, MlpArgs args,
                                                                   float *__restrict__ y) {
     __shared__ __attribute__((aligned(16))) float xf[kMlpRows][kMlpMaxDim];  // running activation
     __shared__ __attribute__((aligned(16))) int8_t xq[kMlpRows][kMlpMaxDim + 64];  // its codes
     __shared__ float sa[kMlpRows];                                        // row scales
     const int tid = threadIdx.x, wid = tid / 64, lane = tid % 64;
     const int row = lane & 15, q = lane >> 4;
-    const int64_t r0 = (int64_t)blockIdx.x * kMlpRows;
-    const int mr = (int)std::min<int64_t>(kMlpRows, M - r0);  // valid rows
+    const int64_t r0 = (int64_t)blockIdx.x * rows;
+    const int mr = (int)std::min<int64_t>(rows, M - r0);  // valid rows
+    // the block's rows past `rows`: zero codes and scales, never written again
+    for (int t = tid; t < (kMlpRows - rows) * ((kMlpMaxDim + 64) / 16); t += kMlpWaves * 64)
+        reinterpret_cast<uint4 *>(&xq[rows][0])[t] = uint4{0u, 0u, 0u, 0u};
+    if (tid >= rows && tid < kMlpRows) sa[tid] = 0.0f;
 
     // The weights of the wave's first tile of layer 0 are requested right
     // after the input rows, and each layer requests the next layer's first
@@ -95,7 +105,7 @@ __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *_
     const int k0 = args.layer[0].k;
     if (k0 % 4 == 0 && ((uintptr_t)x & 15) == 0) {
         constexpr int XV = kMlpRows * kMlpMaxDim / 4 / (kMlpWaves * 64);
-        const int k4 = k0 / 4, total = kMlpRows * k4;
+        const int k4 = k0 / 4, total = rows * k4;
         const float4 *x4 = reinterpret_cast<const float4 *>(x + r0 * k0);
         const int last4 = mr * k4 - 1;  // the last valid float4 of the block's rows
         float4 v[XV];
@@ -114,7 +124,7 @@ __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *_
             }
         }
     } else {
-        for (int t = tid; t < kMlpRows * k0; t += kMlpWaves * 64) {
+        for (int t = tid; t < rows * k0; t += kMlpWaves * 64) {
             const int r = t / k0, c = t % k0;
             xf[r][c] = r < mr ? x[(r0 + r) * k0 + c] : 0.0f;
         }
@@ -143,8 +153,10 @@ __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *_
         // write. q = round(x / s) through the reciprocal with the exact
         // division only next to a half-integer (round_quotient), the same
         // integer as the IEEE quotient rounded.
-#pragma unroll  // (the wave's two rows: their latency chains overlap)
-        for (int r = wid; r < kMlpRows; r += kMlpWaves) {
+#pragma unroll  // (a wave's rows: their latency chains overlap)
+        for (int rr = 0; rr < kMlpRows / kMlpWaves; ++rr) {
+            const int r = wid + rr * kMlpWaves;
+            if (r >= rows) break;
             float mx = 0.0f;
             for (int c0 = 4 * lane; c0 < K; c0 += 256) {
                 const float4 v = *reinterpret_cast<const float4 *>(&xf[r][c0]);
@@ -255,8 +267,14 @@ extern "C" int rnn_w8a8_mlp(const float *x, int64_t m, int nlayers, const int64_
     }
     if (m == 0) return RNN_OK;
     RNN_REQUIRE(x && y, "%s: null x or y", name);
-    const int64_t blocks = ceil_div(m, kMlpRows);
+    // rows per workgroup: the fewest (a power of two) that keep the
+    // workgroups within one per CU (batch 32, 784-256-128-10: 16 rows per
+    // workgroup 16.3 us, 4 rows 13.3, 2 rows 12.8, 1 row 12.9; batch 1024: 4
+    // rows 13.5, 2 rows 25.0)
+    int rows = 1;
+    while (rows < kMlpRows && ceil_div(m, rows) > device_cu_count()) rows *= 2;
+    const int64_t blocks = ceil_div(m, rows);
     RNN_REQUIRE(blocks <= 0x7fffffffLL, "%s: m too large", name);
-    w8a8_mlp_kernel<<<(unsigned)blocks, kMlpWaves * 64, 0, as_stream(stream)>>>(x, m, args, y);
+    w8a8_mlp_kernel<<<(unsigned)blocks, kMlpWaves * 64, 0, as_stream(stream)>>>(x, m, rows, args, y);
     return check_launch(name);
 }

@@ -93,12 +93,17 @@ def test_ternary_model_from_model(dev):
 
 @pytest.mark.parametrize("m,dims,relu", [(32, (784, 256, 128, 10), True), (1, (64, 48), False),
                                          (40, (1024, 1024, 16), True), (17, (32, 80, 112, 96, 5), True),
-                                         (5, (16, 7), True)])
+                                         (5, (16, 7), True),
+                                         # 2, 4, 8 and 16 rows per workgroup (256 CUs)
+                                         (300, (784, 256, 128, 10), True),
+                                         (777, (784, 256, 128, 10), True),
+                                         (1500, (128, 64, 10), True), (4111, (64, 32), False)])
 def test_w8a8_mlp_one_launch_matches_chain(dev, hip, m, dims, relu):
     """rnn_w8a8_mlp against the oracle chain (per-row quantization + W8A8 +
-    epilogue per layer, ReLU between), bit for bit; rows beyond a multiple of
-    16 and widths that are not multiples of 16 included; the per-layer launches
-    must give the same bits."""
+    epilogue per layer, ReLU between), bit for bit; batches that give 1, 2,
+    4, 8 and 16 rows of x per workgroup (the MFMAs' other rows zero), rows
+    beyond a multiple of the workgroup's and widths that are not multiples of
+    16 included; the per-layer launches must give the same bits."""
     params = []
     for i, (fi, fo) in enumerate(zip(dims[:-1], dims[1:])):
         params += [W.weights(fo, fi, seed=60 + i), W.weights(1, fo, seed=70 + i)[0]]
