@@ -193,7 +193,16 @@ def bench_prefill(H, W, dev, steps, warmup):
     ms = timed(fn, steps, warmup)
     ops = 2.0 * m * n * k
     tops = ops / (ms * 1e-3) / 1e12
-    state = dict(aq=aq, sa=sa, wq=wq, sw=sw, m=m, k=k, n=n)
+    # The whole W8A8 layer as a caller runs it: the fp32 activations quantized
+    # per row (rnn_quant_rows_i8) and then the GEMM with its epilogue.
+    layer = lambda: H.w8a8_linear(*H.quant_rows_i8(x, aq, sa), wq, sw, y=y)  # noqa: E731
+    settle(layer, 0.1)
+    ms_layer = timed(layer, steps, warmup)
+    quant = lambda: H.quant_rows_i8(x, aq, sa)  # noqa: E731
+    ms_quant = graph_timed(lambda i: quant(), 50)
+    state = dict(aq=aq, sa=sa, wq=wq, sw=sw, m=m, k=k, n=n,
+                 layer={"us": round(ms_layer * 1e3, 2), "quant_us": round(ms_quant * 1e3, 2),
+                        "TOPS": round(ops / (ms_layer * 1e-3) / 1e12, 1)})
     return ms, tops, state
 
 
@@ -770,6 +779,92 @@ def bench_clock_probe(dev):
 COMPONENTS = ["gemv", "mlp", "ternary", "rotorquant", "rq_attention", "qt_gemv", "igemm512",
               "sgemm", "copy", "clock"]
 
+# QuantizedLinear entries carried on the printed line (all of them go to --full-json)
+QT_LINE = ("INT4_g128_m1_k4096_n11008", "INT4_g128_m16_k4096_n11008", "GGUF_Q8_0_m16_k4096_n11008")
+
+
+def _pick(d, *keys):
+    return {k: d[k] for k in keys if k in d}
+
+
+def compact(result):
+    """The printed line: the headline fields, then the secondary rows, then
+    BASELINE configs 1, 2, 4 and 5 last (so that a reader keeping only the
+    tail of stdout still has every configuration). The full record, with the
+    per-entry method strings, is what --full-json writes."""
+    comp = result.get("components", {})
+    line = {k: result[k] for k in result if k != "components"}
+    if "cpu_baseline" in line:
+        cb = line["cpu_baseline"]
+        line["cpu_baseline"] = dict(_pick(cb, "value", "unit", "cores", "kind", "sample"),
+                                    cpu=cb.get("cpu", {}).get("model"))
+    other = {}
+    if "rotorquant_kv_attention" in comp:
+        a = comp["rotorquant_kv_attention"]
+        other["rq_kv_attention"] = {"us": a["us"], "frac_hbm": a["frac_hbm"],
+                                    "b1_us": a["batch1"]["us"],
+                                    "b1_frac_hbm": a["batch1"]["frac_hbm"],
+                                    "f32_sdpa_us": a["f32_kv_sdpa_us"]}
+    if "quantized_linear_gemv" in comp:
+        q = comp["quantized_linear_gemv"]
+        other["qt_gemv"] = {k: _pick(q[k], "us", "frac_hbm", "frac_of_read_floor")
+                            for k in QT_LINE if k in q}
+    if "igemm_512" in comp:
+        g = comp["igemm_512"]
+        other["igemm_512"] = _pick(g, "us", "speedup_vs_published", "bit_exact_vs_scalar")
+        if "cpu_baseline" in g:
+            other["igemm_512"]["cpu_us"] = g["cpu_baseline"]["us"]
+    if "f32_sgemm" in comp:
+        other["f32_sgemm"] = _pick(comp["f32_sgemm"], "TFLOP/s", "frac_fp32_mfma_peak",
+                                   "torch_matmul_TFLOP/s")
+    if "copy_ceiling" in comp:
+        other["copy_ceiling_GBs"] = comp["copy_ceiling"]["GB/s"]
+    if "mfma_clock_probe" in comp:
+        c = comp["mfma_clock_probe"]
+        other["mfma_clock_probe"] = {"ghz": c["ghz_median"], "TOPS": c["int8_TOPS"]}
+    if other:
+        line["other"] = other
+    if "int8_mlp_784_256_128_10" in comp:
+        e = comp["int8_mlp_784_256_128_10"]
+        c1 = _pick(e, "us_graph", "us_eager", "us_graph_per_layer_launches", "ops",
+                   "max_abs_diff_vs_cpu")
+        if "cpu_baseline" in e:
+            c1["cpu_us"] = e["cpu_baseline"]["us"]
+            c1["cpu_cores"] = e["cpu_baseline"]["cores"]
+        line["C1_mlp_784_256_128_10_b32"] = c1
+    if "w8a8_decode_gemv" in comp:
+        c2 = {}
+        for name, e in comp["w8a8_decode_gemv"].items():
+            s = {"us": e["us"], "GB/s": e["GB/s"], "frac_hbm": e["frac_hbm"]}
+            if "read_floor_us" in e:
+                s["floor_us"] = e["read_floor_us"]
+                s["of_floor"] = e["frac_of_read_floor"]
+            if "cpu_baseline" in e:
+                s["cpu_us"] = e["cpu_baseline"]["us"]
+                s["cpu_cores"] = e["cpu_baseline"]["cores"]
+            c2[name] = s
+        c2["note"] = ("floor = same-bytes one-launch read (probe), timed as the GEMV; "
+                      "cpu = oracle igemm + epilogue, 4-row blocks over threads")
+        line["C2_decode_gemv"] = c2
+    if "ternary_gemm" in comp:
+        e = comp["ternary_gemm"]
+        c4 = _pick(e, "us", "TOPS", "frac_int8_peak", "us_reference_layout", "traffic")
+        if e.get("counters"):
+            c4["mfma_busy"] = e["counters"].get("mfma_busy")
+            c4["clock_ghz"] = e["counters"].get("clock_ghz")
+        if "cpu_baseline" in e:
+            c4["cpu_us"] = e["cpu_baseline"]["us"]
+            c4["cpu_cores"] = 1
+        line["C4_ternary_512x4096x4096"] = c4
+    if "rotorquant_kv" in comp:
+        e = comp["rotorquant_kv"]
+        c5 = _pick(e, "us_per_step", "GB/s", "frac_hbm", "traffic")
+        if "cpu_baseline" in e:
+            c5["cpu_us_per_step"] = e["cpu_baseline"]["us_per_step"]
+            c5["cpu_cores"] = 1
+        line["C5_rotorquant_kv_8x32x4096x128"] = c5
+    return line
+
 
 def main():
     ap = argparse.ArgumentParser()
@@ -780,6 +875,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="all", choices=["all", "prefill"] + COMPONENTS)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--full-json", default=None,
+                    help="also write the full record (every entry with its method) to this file")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
@@ -822,6 +919,8 @@ def main():
                                    f"launches; {SETTLE_S} s clock settle and {args.warmup} "
                                    f"warmup launches before them"},
         })
+        result["prefill_layer"] = dict(state["layer"], note="rnn_quant_rows_i8 of the fp32 "
+                                       "activations + the GEMM, events over back-to-back calls")
         if with_cpu:
             log("cpu baseline: oracle igemm over the whole workload")
             result["cpu_baseline"] = cpu_baseline(state)
@@ -862,7 +961,10 @@ def main():
     if "value" not in result:  # a single non-headline component was requested
         result.update({"value": None, "unit": None, "ms_per_step": None,
                        "config": {"workload": args.only}})
-    print(json.dumps(result), flush=True)
+    if args.full_json:
+        with open(args.full_json, "w") as f:
+            json.dump(result, f, indent=1)
+    print(json.dumps(compact(result)), flush=True)
 
 
 if __name__ == "__main__":

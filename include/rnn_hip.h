@@ -99,8 +99,10 @@ int rnn_igemm(const uint8_t *a, const int8_t *b, int32_t *c, int64_t m,
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). Same contract and results as rnn_igemm; the workspace is
  * a file-scope device array of RNN_IGEMM_NOALLOC_MAX_BYTES that each GPU the
- * library runs on holds until the process ends. Sizes whose
- * rnn_igemm_workspace_size() exceeds it return RNN_ERR_UNSUPPORTED. Nothing
+ * library runs on holds until the process ends. Problems with
+ * m*n*k <= 2^28 run in one launch and use no workspace, at any size; larger
+ * ones whose rnn_igemm_workspace_size() exceeds the array return
+ * RNN_ERR_UNSUPPORTED. Nothing
  * is allocated and nothing needs clearing between calls. Calls on one GPU
  * share that GPU's array: calls ordered on one stream are safe, calls that
  * overlap on one GPU (other streams, other threads) race. */

@@ -12,6 +12,17 @@
 
 #include "../../include/rnn_hip.h"
 
+// The kernels are written for gfx950 only. Beyond the MFMA and LDS-DMA forms,
+// two split-merge hand-offs (the split-K GEMV partials of qformat.hip and the
+// sequence-split attention states of rqattn.hip) rely on gfx9 memory
+// behaviour: device-scope atomic stores write through the XCD's L2 to the
+// coherence point, and `s_waitcnt vmcnt(0)` waits for stores as well as
+// loads, so a relaxed counter increment issued after it is ordered behind the
+// partials. A target that counts stores separately (vscnt) would race there.
+#if defined(__HIP_DEVICE_COMPILE__) && !(defined(__gfx950__) && defined(__GFX9__))
+#error "librnn_hip is built for gfx950 only (gfx9 store counting is assumed by the split merges)"
+#endif
+
 namespace rnn {
 
 typedef int v4i __attribute__((ext_vector_type(4)));

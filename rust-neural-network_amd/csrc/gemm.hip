@@ -2335,6 +2335,8 @@ extern "C" int rnn_igemm_noalloc(const uint8_t *a, const int8_t *b, int32_t *c, 
     hipStream_t st = as_stream(stream);
     if (k == 0) return igemm_empty(c, m, n, st, name);
     RNN_REQUIRE(a && b, "%s: null operand", name);
+    // one-launch problems use no workspace, so the array's size does not limit them
+    if (igemm_small(m, k, n)) return launch_igemm_small(a, b, c, m, k, n, st, name);
     const size_t need = rnn_igemm_workspace_size(m, k, n);
     if (need > (size_t)RNN_IGEMM_NOALLOC_MAX_BYTES)
         return set_error(RNN_ERR_UNSUPPORTED,
@@ -2342,7 +2344,6 @@ extern "C" int rnn_igemm_noalloc(const uint8_t *a, const int8_t *b, int32_t *c, 
                          "%zu-byte device array (use rnn_igemm)",
                          name, (long long)m, (long long)k, (long long)n, need,
                          (size_t)RNN_IGEMM_NOALLOC_MAX_BYTES);
-    if (igemm_small(m, k, n)) return launch_igemm_small(a, b, c, m, k, n, st, name);
     void *ws = nullptr;
     RNN_TRY(scratch_address(&ws, name));
     return igemm_on_workspace(a, b, c, m, k, n, ws, st, name);

@@ -673,6 +673,8 @@ extern "C" int rnn_rotorquant_kv_attention_ws(const float *q, int64_t bh, int64_
     RNN_ENTRY();
     const char *name = "rnn_rotorquant_kv_attention";
     RNN_REQUIRE(bh >= 0 && nq >= 0 && seq >= 0 && dim > 0, "%s: bad size", name);
+    // the split counts and states are updated with 4-byte atomics
+    RNN_REQUIRE(((uintptr_t)workspace % 16) == 0, "%s: workspace must be 16-byte aligned", name);
     const int64_t ngw = ceil_div(dim, 3);
     // the wide kernel's LDS: the rotated query (16 bytes per group, 8-group
     // blocks), the accumulators, and the static probabilities and merge rows

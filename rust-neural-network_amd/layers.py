@@ -21,6 +21,8 @@ quantized layers, which implement it too, sit in one `Sequential` next to f32
 layers."""
 from __future__ import annotations
 
+import weakref
+
 import rnn_hip as H
 
 
@@ -311,9 +313,15 @@ class TernaryLinear(Module):
         aq, sa = H.quant_rows_i8(x)
         tw = self.ternary_weight
         if self.in_features % 16 == 0:
-            if getattr(self, "_mfma_packed", None) is None:
+            # the prepacked copy follows `ternary_weight.packed`: another
+            # tensor there (a replaced struct or field; held by weak reference,
+            # so a freed one is never mistaken for a new one) or an in-place
+            # write to it (torch's version counter) rebuilds it
+            src = getattr(self, "_mfma_src", None)
+            if src is None or src[0]() is not tw.packed or src[1] != tw.packed._version:
                 self._mfma_packed = H.ternary_prepack(tw.packed, self.out_features,
                                                       self.in_features)
+                self._mfma_src = (weakref.ref(tw.packed), tw.packed._version)
             y, _ = H.ternary_gemm(aq, sa, self._mfma_packed, tw.scales, self.out_features,
                                   self.bias, relu=relu, mfma_layout=True)
         else:
@@ -515,8 +523,12 @@ class RotorQuant(Module):
     round trip (`impl Module`, :242-252); `parameters()` is empty."""
 
     def __init__(self, dim, bits, rotors):
-        if not 2 <= bits <= 8:
-            raise ValueError("bits must be in [2, 8]")  # src/quant.rs:136
+        # src/quant.rs:136 asserts bits >= 2; qmax = (1u32 << (bits - 1)) - 1
+        # (:164-166) overflows past 32 bits. forward() never asks for the int8
+        # codes, so widths above 8 are served too (the C ABI limits only code
+        # output to 8 bits).
+        if not 2 <= bits <= 32:
+            raise ValueError("bits must be in [2, 32]")
         ng = (dim + 2) // 3
         if tuple(rotors.shape) != (ng, 4):
             raise ValueError(f"rotors must be [{ng}, 4], got {tuple(rotors.shape)}")

@@ -167,6 +167,18 @@ def test_new_elementwise_argument_rules(lib):
     assert lib.rnn_bias_act(FAKE, None, 4, 4, 0, None) == H.RNN_OK  # nothing to do: no launch
 
 
+def test_attention_workspace_alignment(lib):
+    """The attention's split counts and states take 4-byte atomics: a caller
+    workspace must be 16-byte aligned, as rnn_qt_linear_forward_ws requires."""
+    def call(ws):
+        return lib.rnn_rotorquant_kv_attention_ws(FAKE, 32, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                                   4096, 128, 0.1, FAKE, ws, 1 << 20, None)
+    _status(call(ctypes.c_void_p(258)), H.RNN_ERR_INVALID_ARG, "16-byte aligned")
+    _status(lib.rnn_qt_linear_forward_ws(3, FAKE, 1, 4096, FAKE, 1 << 20, FAKE, 1 << 15, 128,
+                                         11008, None, FAKE, ctypes.c_void_p(260), 1 << 24, 0, None),
+            H.RNN_ERR_INVALID_ARG, "misaligned")
+
+
 # ------------------------------------------------- binding size checks (no GPU)
 class _Stand:
     """Quacks like a contiguous device tensor for the binding's argument checks;

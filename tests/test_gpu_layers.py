@@ -91,6 +91,30 @@ def test_ternary_model_from_model(dev):
     np.testing.assert_array_equal(host(model.forward(to_dev(x, dev))), h)
 
 
+def test_ternary_int8_forward_follows_replaced_weights(dev):
+    """TernaryLinear's int8 path keeps a prepacked copy of the codes; it must
+    follow `ternary_weight` when the struct is replaced (from_linear again,
+    load_model) or its `packed` words are rewritten in place (the reference's
+    pub fields, src/ternary.rs:81-90)."""
+    import torch
+    w1, w2 = W.weights(48, 256, seed=40), W.weights(48, 256, seed=41)
+    x = W.activations(9, 256, seed=42)
+    lin = L.TernaryLinear.from_linear(to_dev(w1, dev), None, int8=True)
+
+    def want(w):
+        t, s = O.ternary_quantize_rows(w)
+        aq, sa = O.quant_rows_i8(x)
+        return O.ternary_gemm_i8(aq, sa, O.pack_ternary(t), s, 48)[0]
+    np.testing.assert_array_equal(host(lin.forward(to_dev(x, dev))), want(w1))
+    lin.ternary_weight = L.TernaryTensor.quantize(to_dev(w2, dev))     # a new struct
+    np.testing.assert_array_equal(host(lin.forward(to_dev(x, dev))), want(w2))
+    t1 = L.TernaryTensor.quantize(to_dev(w1, dev))
+    with torch.no_grad():                                               # the same tensor, rewritten
+        lin.ternary_weight.packed.copy_(t1.packed)
+        lin.ternary_weight.scales.copy_(t1.scales)
+    np.testing.assert_array_equal(host(lin.forward(to_dev(x, dev))), want(w1))
+
+
 @pytest.mark.parametrize("m,dims,relu", [(32, (784, 256, 128, 10), True), (1, (64, 48), False),
                                          (40, (1024, 1024, 16), True), (17, (32, 80, 112, 96, 5), True),
                                          (5, (16, 7), True),

@@ -94,6 +94,17 @@ def test_sequential_quantized_linear_and_rotorquant(dev):
     assert seq.parameters() == []
 
 
+@pytest.mark.parametrize("bits", [12, 16])
+def test_rotorquant_module_wide_codes(dev, bits):
+    """RotorQuant::new(dim, bits) with bits above 8 (src/quant.rs:135-166):
+    the Module round trip, bit for bit against the oracle."""
+    x = W.activations(200, 128, seed=60 + bits)
+    rot = W.rotors(43, seed=62)
+    got = host(L.RotorQuant(128, bits, to_dev(rot, dev)).forward(to_dev(x, dev)))
+    want, _, _ = O.rotorquant_quantize(x, rot, bits)
+    np.testing.assert_array_equal(got, want)
+
+
 def test_relu_matches_f32_max(dev, hip):
     x = W.activations(7, 333, seed=53)
     x[0, :4] = [np.nan, -0.0, 0.0, -np.inf]

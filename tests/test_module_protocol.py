@@ -61,6 +61,9 @@ def test_rotorquant_module_checks_its_arguments():
     rq = L.RotorQuant(128, 4, _R())
     assert rq.padded_dim == 129 and rq.parameters() == []
     with pytest.raises(ValueError):
-        L.RotorQuant(128, 1, _R())      # bits in [2, 8] (src/quant.rs:136)
+        L.RotorQuant(128, 1, _R())      # at least 2 bits (src/quant.rs:136)
+    with pytest.raises(ValueError):
+        L.RotorQuant(128, 33, _R())     # qmax's u32 shift (src/quant.rs:164-166)
+    assert L.RotorQuant(128, 16, _R()).bits == 16   # RotorQuant::new(dim, 16) is valid
     with pytest.raises(ValueError):
         L.RotorQuant(126, 4, _R())      # 42 groups need 42 rotors

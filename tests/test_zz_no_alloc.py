@@ -61,3 +61,29 @@ def test_igemm_noalloc_rejects_sizes_beyond_the_array():
     assert rc == H.RNN_ERR_UNSUPPORTED
     assert "device array" in H.last_error()
     assert lib.rnn_igemm_noalloc(fake, fake, fake, -1, 4, 4, None) == H.RNN_ERR_INVALID_ARG
+    # A one-launch problem uses no workspace: m = n = 1, k = 2^25 needs more
+    # workspace than the array holds under the packed plan, yet is not refused
+    # for it. Only where no GPU is present: the call then reaches the launch
+    # and fails there with a HIP error (with a GPU the fake pointers would be
+    # read; test_igemm_noalloc_small_problem_beyond_the_array runs it for real).
+    import torch
+    assert H.igemm_workspace_size(1, 2**25, 1) > H.IGEMM_NOALLOC_MAX_BYTES
+    if torch.cuda.device_count() == 0:
+        rc = lib.rnn_igemm_noalloc(fake, fake, fake, 1, 2**25, 1, None)
+        assert rc == H.RNN_ERR_HIP, H.last_error()
+
+
+@pytest.mark.gpu
+def test_igemm_noalloc_small_problem_beyond_the_array(dev, hip):
+    """m = n = 1, k = 2^25: m n k is within the one-launch bound, so no
+    workspace is needed although the packed plan's would exceed the array."""
+    import torch
+    k = 2**25
+    g = np.random.default_rng(5)
+    a = g.integers(0, 256, size=(1, k), dtype=np.uint8)
+    b = g.integers(-128, 128, size=(k, 1), dtype=np.int8)
+    c = torch.full((1, 1), 7, dtype=torch.int32, device=dev)
+    hip.igemm_noalloc(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), 1, k, 1, c)
+    exact = int((a.astype(np.int64) @ b.astype(np.int64))[0, 0])
+    want = (exact + 2**31) % 2**32 - 2**31   # wrapping int32
+    assert int(c.cpu().numpy()[0, 0]) == want
