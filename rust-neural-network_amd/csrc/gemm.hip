@@ -1617,24 +1617,24 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wl_kernel(
 // Decode GEMV over balanced row ranges: workgroup b of G (8 waves, at most
 // one per CU) owns weight rows [b*N/G, (b+1)*N/G), processed as up to TPW
 // 16-row tiles. Its loads are all issued up front, in this order: the
-// activation fragments of each wave's K range (K/8 bytes of rows < 16; rows
-// past M read row M-1 and are zeroed before use), loaded once for all tiles
-// (the per-tile kernels below load them once per tile, as many bytes as the
-// weights at M = 16), the epilogue operands, then every weight byte of every
-// tile, tile by tile, so the row range is in flight from the start. Weights
-// are read through a buffer descriptor that ends at the last
-// row of the range: the rows that pad the last tile to 16 read zeros and
+// activations of each wave's K range (K/8 bytes of each row < M, in whole
+// cache lines; loaded once for all tiles, where the per-tile kernels below
+// load them once per tile, as many bytes as the weights at M = 16), the
+// epilogue operands, then every weight byte of every tile, tile by tile, so
+// the row range is in flight from the start. Weights and
+// activations are read through buffer descriptors that end at the range's
+// last row and at row M - 1: the rows that pad a tile to 16 read zeros and
 // fetch nothing. Balanced ranges keep every CU's byte count within one row of
-// the others (16-row tiles dealt out whole leave up to 12% of the CUs'
-// time idle, e.g. 688 tiles over 256 CUs). Each wave takes K/8 of a tile:
+// the others (16-row tiles dealt out whole leave up to 12% of the CUs' time
+// idle, e.g. 688 tiles over 256 CUs). Each wave takes K/8 of a tile:
 // whole-line weight loads (4 rows x 256 bytes per instruction,
-// non-temporal), regrouped into MFMA fragments through the wave's 4 KiB LDS
-// slice, 256 bytes of each row at a time (16-byte chunk c of row r at c ^ r),
-// 16x16x64 MFMAs against the activation
-// fragments held in registers for all tiles, then the 8 partial tiles are
-// summed through LDS (exact: wrapping int32) and the epilogue runs once per
-// output. Barriers order LDS only, so the later tiles' loads stay in flight
-// while earlier tiles compute. K = 2048 * H bytes (H = 1, 2).
+// non-temporal), regrouped into MFMA fragments through the wave's LDS slice,
+// 256 bytes of each row at a time (16-byte chunk c of row r at c ^ r),
+// 16x16x64 MFMAs against the activation fragments (regrouped once through
+// the same slice and held in registers for all tiles), then the 8 partial
+// tiles are summed through LDS (exact: wrapping int32) and the epilogue runs
+// once per output. Barriers order LDS only, so the later tiles' loads stay in
+// flight while earlier tiles compute. K = 2048 * H bytes (H = 1, 2).
 constexpr int kGlWaves = 8;
 
 __device__ __forceinline__ void lds_only_barrier() {
@@ -1650,7 +1650,12 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
     constexpr int KW = 256 * H;        // K bytes per wave and tile
     constexpr int K = kGlWaves * KW;   // 2048 or 4096
     constexpr int KB = KW / 64;        // MFMA k-steps per wave and tile
-    __shared__ __attribute__((aligned(16))) int8_t stage[kGlWaves][16 * 256];
+    constexpr int LPR = KW / 16;       // lanes per activation row in a whole-line load
+    constexpr int RPI = 64 / LPR;      // activation rows per load instruction
+    static_assert(RPI * KB == 16, "KB whole-line loads cover the 16 activation rows");
+    // per wave: the 16 activation rows of its K range (regrouped once), then
+    // 256 bytes of each of the 16 weight rows at a time
+    __shared__ __attribute__((aligned(16))) int8_t stage[kGlWaves][16 * KW];
     __shared__ int32_t part[kGlWaves][16][16];
     const int tid = threadIdx.x, wid = tid / 64, lane = tid % 64;
     const int row = lane & 15, q = lane >> 4;
@@ -1667,19 +1672,28 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
     const uint32_t r0 = blockIdx.x * (uint32_t)N / gridDim.x;
     const int nrows = (int)((blockIdx.x + 1) * (uint32_t)N / gridDim.x - r0);
 
-    // 1. activation fragments of this wave's K range (lane: row m, chunk q)
-    v4i a[KB];
-    const int8_t *ap = A + (row < M ? row : M - 1) * (int64_t)K + k0 + 16 * q;
+    // every weight byte of the row range; offsets past nrows rows read 0
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(W + (int64_t)r0 * K), 0, nrows * K, 0x00020000);
+    // the activations, rows < M only: offsets past row M - 1 read 0
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(A), 0, (int)(M * K), 0x00020000);
+    // 1. this wave's K range of the activations in whole lines, RPI rows (KW
+    //    bytes each) per instruction, regrouped into MFMA fragments through
+    //    LDS below while the weights are in flight. Fragment-layout loads (16
+    //    rows x 64 bytes per instruction) touch twice the cache lines.
+    v4i al[KB];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) a[kb] = *reinterpret_cast<const v4i *>(ap + 64 * kb);
+    for (int j = 0; j < KB; ++j)
+        al[j] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                     ar, (RPI * j + lane / LPR) * K + k0 + 16 * (lane % LPR), 0, 0));
     // 2. epilogue operands of the outputs this thread finishes (one per tile)
     const int em = (tid / 16) & 15, en = tid % 16;
     EpiOps eo[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) eo[i] = epi.load_ops(em, r0 + std::min(16 * i + en, nrows - 1));
-    // 3. every weight byte of the row range; offsets past nrows rows read 0
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t *>(W + (int64_t)r0 * K), 0, nrows * K, 0x00020000);
+    // 3. every weight byte of the row range
     v4i w[TPW][4][H];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
@@ -1702,8 +1716,19 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
     // keep every load above ahead of the first wait
     __builtin_amdgcn_sched_barrier(0);
 
-    const v4i zero = {0, 0, 0, 0};
+    // the activation fragments (lane (row, q) of step kb: row `row`, bytes
+    // 64 kb + 16 q of the K range), through this wave's LDS slice with the
+    // 16-byte chunk c of row r at c ^ r; rows past M arrived as zeros
     int8_t *st = stage[wid];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+        const int r = RPI * j + lane / LPR;
+        *reinterpret_cast<v4i *>(st + r * KW + 16 * ((lane % LPR) ^ r)) = al[j];
+    }
+    v4i a[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+        a[kb] = *reinterpret_cast<const v4i *>(st + row * KW + 16 * ((4 * kb + q) ^ row));
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
         // (no early exit for a tile past the range: it multiplies zeros and
@@ -1726,8 +1751,7 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
             for (int kb = 0; kb < 4; ++kb) {
                 const int ch = 4 * kb + q;
                 const v4i b = *reinterpret_cast<const v4i *>(st + row * 256 + 16 * (ch ^ row));
-                const v4i af = row < M ? a[4 * h + kb] : zero;  // rows past M are zero
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, b, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[4 * h + kb], b, acc, 0, 0, 0);
             }
         }
         part[wid][4 * q + 0][row] = acc.x;
@@ -1949,14 +1973,13 @@ static int launch_gemv(const int8_t *A, const int8_t *W, int64_t M, int64_t N, i
     // (N 4096), 14.96 vs 13.57 (N 11008, 688 workgroups: not taken).
     //
     // The balanced-row kernel (activations loaded once per workgroup) takes
-    // M > 8, and M <= 4 while the rows fit one tile per CU. Measured against
-    // the kernels below, K = 4096 (us): M = 16 5.84 vs 6.18 (N 4096), 11.03
-    // vs 13.59 (N 11008), 13.79 vs 16.97 (N 14336); M = 1 4.97 vs 5.19
-    // (N 4096); not taken: M = 1 10.02 vs 9.15 and M = 8 10.34 vs 10.15
-    // (N 11008), M = 8 5.26 vs 5.19 (N 4096).
+    // M > 8, and any M while the rows fit one tile per CU. Measured against
+    // the per-tile kernels below, K = 4096 (us, one process): N = 4096: M = 1
+    // 4.84 vs 5.39 (<4,4>), M = 8 4.92 vs 5.24 (<4,8>); N = 11008: M = 16
+    // 10.56 (the <4,16> kernel 13.6), not taken: M = 1 10.26 vs 9.17 (<4,4>),
+    // M = 4 10.63 vs 9.59, M = 8 10.72 vs 10.33 (<4,8>).
     const unsigned wgs = (unsigned)ceil_div(N, 16);
-    if ((M > 8 || (M <= 4 && (int64_t)wgs <= device_cu_count())) &&
-        launch_gemv_rows(A, W, M, N, K, epi, st))
+    if ((M > 8 || (int64_t)wgs <= device_cu_count()) && launch_gemv_rows(A, W, M, N, K, epi, st))
         return check_launch(name);
     if (K % 4096 == 0 && M <= 4)
         gemv_wl_kernel<4, 4><<<wgs, 256, 0, st>>>(A, W, M, N, K, epi);
