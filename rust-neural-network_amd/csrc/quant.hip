@@ -50,6 +50,51 @@ __global__ __launch_bounds__(kQuantBlock) void quant_rows_kernel(
     }
 }
 
+// The same rule with the row held in registers (cols % 4 == 0, 16-byte
+// aligned x, cols <= 1024 R): each thread loads its R float4 at once, so a
+// row is one round trip instead of a strided loop and a second pass over L2,
+// and the quotient is a multiply by 1/scale (round_quotient: rint of it
+// wherever that provably equals the rounded IEEE quotient, the division
+// itself near a half-integer). The scale itself is the IEEE m / 127.
+template <int R>
+__global__ __launch_bounds__(kQuantBlock) void quant_rows_reg_kernel(
+    const float *__restrict__ x, int64_t cols, int8_t *__restrict__ q,
+    float *__restrict__ scale) {
+    const int64_t r = blockIdx.x;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 *row4 = reinterpret_cast<const f32x4 *>(x + r * cols);
+    uint32_t *q4 = reinterpret_cast<uint32_t *>(q + r * cols);
+    const int64_t n4 = cols / 4;
+    f32x4 v[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int64_t j = threadIdx.x + (int64_t)u * kQuantBlock;
+        v[u] = j < n4 ? __builtin_nontemporal_load(row4 + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        m = fmaxf(m, fabsf(v[u].x));
+        m = fmaxf(m, fabsf(v[u].y));
+        m = fmaxf(m, fabsf(v[u].z));
+        m = fmaxf(m, fabsf(v[u].w));
+    }
+    __shared__ float red[kQuantBlock / 64];
+    m = block_max<kQuantBlock>(m, red);
+    const float s = m > 0.0f ? m / 127.0f : 1.0f;
+    const float inv = __builtin_amdgcn_rcpf(s);
+    if (threadIdx.x == 0) scale[r] = s;
+    auto code = [&](float e) -> uint32_t {
+        return (uint8_t)to_i8_rs(clamp_rs(round_quotient(e, s, inv), -128.0f, 127.0f));
+    };
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int64_t j = threadIdx.x + (int64_t)u * kQuantBlock;
+        if (j < n4)
+            q4[j] = code(v[u].x) | (code(v[u].y) << 8) | (code(v[u].z) << 16) | (code(v[u].w) << 24);
+    }
+}
+
 __global__ void int8_dequant_kernel(const int8_t *__restrict__ q, const float *__restrict__ s,
                                     int64_t rows, int64_t cols, float *__restrict__ w) {
     const int64_t total = rows * cols;
@@ -96,7 +141,17 @@ extern "C" int rnn_quant_rows_i8(const float *x, int64_t rows, int64_t cols, int
     RNN_REQUIRE(scale != nullptr, "rnn_quant_rows_i8: null scale");
     RNN_REQUIRE(cols == 0 || (x != nullptr && q != nullptr), "rnn_quant_rows_i8: null pointer");
     const bool vec = cols % 4 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 4) == 0;
-    if (vec)
+    hipStream_t st = as_stream(stream);
+    const unsigned g = (unsigned)rows;
+    if (vec && cols <= 1024)
+        quant_rows_reg_kernel<1><<<g, kQuantBlock, 0, st>>>(x, cols, q, scale);
+    else if (vec && cols <= 2048)
+        quant_rows_reg_kernel<2><<<g, kQuantBlock, 0, st>>>(x, cols, q, scale);
+    else if (vec && cols <= 4096)
+        quant_rows_reg_kernel<4><<<g, kQuantBlock, 0, st>>>(x, cols, q, scale);
+    else if (vec && cols <= 8192)
+        quant_rows_reg_kernel<8><<<g, kQuantBlock, 0, st>>>(x, cols, q, scale);
+    else if (vec)
         quant_rows_kernel<true><<<(unsigned)rows, kQuantBlock, 0, as_stream(stream)>>>(x, cols, q, scale);
     else
         quant_rows_kernel<false><<<(unsigned)rows, kQuantBlock, 0, as_stream(stream)>>>(x, cols, q, scale);

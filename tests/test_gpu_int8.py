@@ -46,6 +46,32 @@ def test_quant_rows_i8_parity(dev, hip, rows, cols):
     assert np.array_equal(host(q), qo)
 
 
+@pytest.mark.parametrize("cols", [4, 1020, 1024, 2048, 3000, 4096, 8192, 8196])
+def test_quant_rows_register_path_edges(dev, hip, cols):
+    """The register-resident quantizer (cols % 4 == 0 up to 8192; the strided
+    kernel past it) against the oracle: exact half-integer quotients (where
+    round() and a rounded reciprocal product could disagree), NaN and +-inf
+    in aligned rows, a zero row, a subnormal-only row, and ordinary rows."""
+    g = np.random.Generator(np.random.PCG64(cols))
+    x = g.standard_normal((8, cols), dtype=np.float32)
+    # row 0: scale 0.25 (max 31.75), every other value an exact (k + 0.5) * 0.25
+    k = g.integers(-127, 127, size=cols).astype(np.float32)
+    x[0] = (k + np.float32(0.5)) * np.float32(0.25)
+    x[0, 0] = np.float32(31.75)
+    # row 1: the same with a scale that is not a power of two (half quotients
+    # are then whatever m / 127 makes of them: the division decides)
+    x[1] = x[0] * np.float32(1.3)
+    x[2, cols // 2] = np.nan
+    x[3, 0] = np.inf
+    x[4, -1] = -np.inf
+    x[5] = 0.0
+    x[6] = g.standard_normal(cols).astype(np.float32) * np.float32(1e-39)   # subnormal
+    q, s = hip.quant_rows_i8(to_dev(x, dev))
+    qo, so = O.quant_rows_i8(x)
+    assert np.array_equal(host(s), so, equal_nan=True)
+    assert np.array_equal(host(q), qo)
+
+
 def test_quant_rows_nan_and_unaligned(dev, hip):
     import torch
     x = W.activations(4, 33, seed=1)
