@@ -187,11 +187,13 @@ def test_ternary_prepack_layout(dev, hip):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 256, 16), (64, 512, 128), (512, 4096, 512), (37, 48, 29),
-                                   (200, 1024, 300), (17, 256, 4)])
+                                   (200, 1024, 300), (17, 256, 4), (130, 512, 200),
+                                   (96, 1536, 260), (33, 2048, 132), (64, 768, 128)])
 def test_ternary_gemm_mfma_layout(dev, hip, m, k, n):
     """The GEMM on prepacked codes (RNN_FLAG_TERNARY_MFMA_LAYOUT) against the
-    oracle on the reference layout: the LDS-DMA kernel (k % 256 == 0) and the
-    tiled kernel (other k, unaligned activations), int32 and fp32 bit-exact."""
+    oracle on the reference layout: the LDS-DMA kernel (k % 256 == 0; one to
+    four 128-K stages per K group, ragged M and N edges) and the tiled kernel
+    (other k, unaligned activations), int32 and fp32 bit-exact."""
     import torch
     t, p = rand_ternary(n, k, seed=3 * m + n, with_code3=True)
     pm = hip.ternary_prepack(to_dev(p.view(np.int32), dev), n, k)
