@@ -525,16 +525,35 @@ __device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int &t
 //    merge its wait-count state at every join and drain the stores there.
 //  * The arithmetic is the reference's: ((float)acc * sa[m]) * sw[n], then
 //    + bias[n], then max(., 0) (src/int8.rs:159-162).
+//  * WT (write-through): the stores are device-scope buffer stores (sc1),
+//    which pass through the XCD's L2 instead of leaving the output dirty in
+//    it. The prefill writes 117 MB of output in two chip-wide bursts; with
+//    the lines left dirty the launch took 103.7-104.6 us against 101.1-102.8
+//    with write-through (one process, bit-identical output); non-temporal
+//    stores were slower (107 us). The host takes it only when y and acc_out
+//    span less than 4 GiB (the buffer range).
 // True when the wave tile at (m0, n0) (lane-adjusted as in tile_epilogue) lies
 // inside M x N, so that every lane issues all of its FM * FN stores.
 template <int FM, int FN>
 __device__ __forceinline__ bool tile_interior(const Epilogue &epi, int64_t m0, int64_t n0) {
     return m0 - (m0 & 15) + 16 * FM <= epi.M && n0 - (n0 & 15) + 16 * FN <= epi.N;
 }
-template <int FM, int FN, bool OUT_Y, bool OUT_ACC, int G = (FN < 4 ? FN : 4)>
+template <int FM, int FN, bool OUT_Y, bool OUT_ACC, bool WT = false, int G = (FN < 4 ? FN : 4)>
 __device__ __forceinline__ void tile_epilogue(const Epilogue &epi, const v4i (&acc)[FN][FM],
                                               int64_t m0, int64_t n0) {
     const bool has_bias = epi.bias != nullptr, relu = epi.relu != 0;
+    // (WT only) buffer ranges of the outputs: byte offsets of whole rows
+    const int out_bytes = WT ? (int)(epi.M * epi.N * 4) : 0;
+    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+        OUT_Y ? (void *)epi.y : (void *)epi.acc_out, 0, out_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        OUT_ACC ? (void *)epi.acc_out : (void *)epi.y, 0, out_bytes, 0x00020000);
+    auto put = [&](const __amdgpu_buffer_rsrc_t &r, void *base, int64_t idx, v4i v) {
+        if constexpr (WT)
+            __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)(idx * 4), 0, 16 /* sc1 */);
+        else
+            *reinterpret_cast<v4i *>(static_cast<int32_t *>(base) + idx) = v;
+    };
     float sam[FM];
 #pragma unroll
     for (int j = 0; j < FM; ++j)
@@ -571,7 +590,7 @@ __device__ __forceinline__ void tile_epilogue(const Epilogue &epi, const v4i (&a
                 o.y = (int)((uint32_t)a.y + 128u * (uint32_t)csv[k].y);
                 o.z = (int)((uint32_t)a.z + 128u * (uint32_t)csv[k].z);
                 o.w = (int)((uint32_t)a.w + 128u * (uint32_t)csv[k].w);
-                *reinterpret_cast<v4i *>(epi.acc_out + m * epi.N + n) = o;
+                put(ar, epi.acc_out, m * epi.N + n, o);
             }
             if (OUT_Y) {
                 float4 v;
@@ -587,7 +606,7 @@ __device__ __forceinline__ void tile_epilogue(const Epilogue &epi, const v4i (&a
                 v.y = relu ? fmaxf(v.y, 0.0f) : v.y;
                 v.z = relu ? fmaxf(v.z, 0.0f) : v.z;
                 v.w = relu ? fmaxf(v.w, 0.0f) : v.w;
-                *reinterpret_cast<float4 *>(epi.y + m * epi.N + n) = v;
+                put(yr, epi.y, m * epi.N + n, __builtin_bit_cast(v4i, v));
             }
         };
         if (interior) {
@@ -1309,7 +1328,7 @@ void gemm_l128_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B
 // ops of a sequence in its two load phases of the window [4s+3, 4s+7), weight
 // loads first. At the end of phase 4s+2 every wave waits until only its A
 // loads of the latest sequence are in flight: stage s+1 has landed.
-template <class C, bool OUT_Y, bool OUT_ACC>
+template <class C, bool OUT_Y, bool OUT_ACC, bool WT>
 __global__ __launch_bounds__(C::NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_pp_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, int64_t M,
                     int64_t N, int64_t K, int tiles_m, int tiles_n, Epilogue epi) {
@@ -1454,8 +1473,8 @@ void gemm_pp_kernel(const int8_t *__restrict__ A, const int8_t *__restrict__ B, 
     }
     wait_vmcnt<0>();  // drain the trailing DMA before the block's LDS is released
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-    tile_epilogue<C::FM, C::FN, OUT_Y, OUT_ACC>(epi, acc, bm0 + wm * C::WM + fr,
-                                                bn0 + wn * C::WN + 4 * fq);
+    tile_epilogue<C::FM, C::FN, OUT_Y, OUT_ACC, WT>(epi, acc, bm0 + wm * C::WM + fr,
+                                                    bn0 + wn * C::WN + 4 * fq);
 }
 
 // ------------------------------------------------------------ skinny GEMV
@@ -1939,12 +1958,18 @@ static int launch_pp(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int
     RNN_REQUIRE(K % kL == 0, "%s: K must be a multiple of %d here", name, kL);
     RNN_REQUIRE(l128_fits(M, N, K, false), "%s: operands of 4 GiB or more", name);
     const unsigned grid = (unsigned)(tm * tn);
+    // write-through output stores while the outputs fit a buffer range
+    const bool wt = (uint64_t)M * (uint64_t)N * 4u < (1ull << 31);
+#define RNN_PP(Y, ACC)                                                                          \
+    (wt ? gemm_pp_kernel<C, Y, ACC, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi) \
+        : gemm_pp_kernel<C, Y, ACC, false><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi))
     if (epi.y && epi.acc_out)
-        gemm_pp_kernel<C, true, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+        RNN_PP(true, true);
     else if (epi.y)
-        gemm_pp_kernel<C, true, false><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+        RNN_PP(true, false);
     else
-        gemm_pp_kernel<C, false, true><<<grid, C::NT, 0, st>>>(A, B, M, N, K, (int)tm, (int)tn, epi);
+        RNN_PP(false, true);
+#undef RNN_PP
     return check_launch(name);
 }
 static int launch_dma_auto(const int8_t *A, const int8_t *B, int64_t M, int64_t N, int64_t K,
