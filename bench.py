@@ -104,8 +104,8 @@ def counters_for(name):
     c = _profile_entry(COUNTERS_FILE, name)
     if c is None:
         return None
-    return {k: c[k] for k in ("mfma_busy", "clock_ghz", "lds_bank_conflict_cycles", "source")
-            if k in c}
+    return {k: c[k] for k in ("mfma_busy", "clock_ghz", "duration_us_under_counters",
+                              "lds_bank_conflict_cycles", "source") if k in c}
 
 
 # ---------------------------------------------------------------- CPU side
@@ -206,6 +206,37 @@ def bench_prefill(H, W, dev, steps, warmup):
     return ms, tops, state
 
 
+def prefill_ksweep(H, W, dev, steps, warmup, ks=(1024, 2048, 3072, 4096)):
+    """The prefill GEMM at the same M and N for several K, and the least-squares
+    line T(K) = fixed + slope * K through them: `fixed_us` is what a launch
+    costs whatever its K (launch ramp, prologue, the fp32 epilogue of M x N
+    outputs, the tail), `loop_us` = slope * K the K loop of the configured K.
+    Each K is settled and timed as the headline launch. The shorter launches
+    draw less power, so their clock can be higher: the split is a model, its
+    residuals are reported with it."""
+    import torch
+    c = W.PREFILL
+    m, n = c["m"], c["n"]
+    us = []
+    for k in ks:
+        wq, sw = H.quant_rows_i8(gen_f32((n, k), 1, dev, 0.02))
+        aq, sa = H.quant_rows_i8(gen_f32((m, k), 2, dev))
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        fn = lambda: H.w8a8_linear(aq, sa, wq, sw, y=y)  # noqa: E731
+        settle(fn)
+        us.append(timed(fn, steps, warmup) * 1e3)
+        del wq, sw, aq, sa, y
+        torch.cuda.empty_cache()
+    mk, mu = sum(ks) / len(ks), sum(us) / len(us)
+    slope = (sum((k - mk) * (u - mu) for k, u in zip(ks, us)) /
+             sum((k - mk) ** 2 for k in ks))
+    fixed = mu - slope * mk
+    return {"k": list(ks), "us": [round(u, 2) for u in us], "fixed_us": round(fixed, 2),
+            "loop_us": round(slope * c["k"], 2),
+            "residual_us": [round(u - fixed - slope * k, 2) for k, u in zip(ks, us)],
+            "note": f"T(K) = fixed + slope*K at M={m}, N={n}; loop_us = slope*{c['k']}"}
+
+
 def cpu_baseline(state, budget_s=20.0):
     """The reference CPU path for the whole prefill workload (all 2048 rows),
     see cpu_w8a8."""
@@ -231,11 +262,14 @@ def cpu_baseline(state, budget_s=20.0):
 
 # ---------------------------------------------------------------- graph timing
 def graph_timed(launch, n_launch, replays=5, settle_s=0.1):
-    """Average ms per launch of `launch(i)` for i in range(n_launch), captured
-    once into a HIP graph and replayed (events on the replay stream), so the
+    """ms per launch of `launch(i)` for i in range(n_launch), captured once
+    into a HIP graph and replayed (events on the replay stream), so the
     per-call host overhead of the Python binding is not part of the figure.
     Untimed replays for `settle_s` seconds come first, so the clocks have
-    settled for this kernel before the timed replays."""
+    settled for this kernel before the timed replays. Each replay is timed on
+    its own and the median replay is reported, so that one slow replay (a
+    replay of a short kernel lasts about a millisecond) does not move the
+    figure."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -255,14 +289,15 @@ def graph_timed(launch, n_launch, replays=5, settle_s=0.1):
         g.replay()
         torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for _ in range(replays):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    ev[0].record(st)
+    for r in range(replays):
         g.replay()
-    e1.record(st)
+        ev[r + 1].record(st)
     torch.cuda.synchronize()
     del g
-    return e0.elapsed_time(e1) / (replays * n_launch)
+    per = [ev[r].elapsed_time(ev[r + 1]) for r in range(replays)]
+    return statistics.median(per) / n_launch
 
 
 class ReadFloor:
@@ -327,7 +362,7 @@ def bench_gemv(H, W, dev, steps, floor, with_cpu):
         ent = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
                "weight_copies": copies, "launches_timed": 5 * n_launch,
-               "timing": "HIP graph replay, events / launches"}
+               "timing": "HIP graph replay: events around each replay, median replay / launches per replay"}
         fl = _floor(floor, ws, k * n, n_launch)
         if fl is not None:
             ent["read_floor_us"] = round(fl * 1e3, 3)
@@ -412,7 +447,7 @@ def bench_qt_gemv(H, dev, steps, floor):
             ent = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
                    "weight_copies": copies, "launches_timed": 5 * n_launch,
-                   "timing": "HIP graph replay, events / launches"}
+                   "timing": "HIP graph replay: events around each replay, median replay / launches per replay"}
             if qt_bf16_path(fmt, m, k, n, g, cus):
                 # three bf16 MFMAs per product (x split in three parts)
                 tf = 3 * 2.0 * 16 * k * n / (ms * 1e-3) / 1e12
@@ -515,7 +550,7 @@ def bench_ternary(H, W, dev, steps, with_cpu):
     nbytes = n * k // 4 + 4 * n + m * k + 4 * m + 4 * m * n
     ent = {"us": round(ms * 1e3, 3), "TOPS": round(tops, 1),
            "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4), "ops": ops, "bytes": nbytes,
-           "launches_timed": 5 * n_launch, "timing": "HIP graph replay, events / launches",
+           "launches_timed": 5 * n_launch, "timing": "HIP graph replay: events around each replay, median replay / launches per replay",
            "weights": "2-bit codes in the MFMA layout of rnn_ternary_prepack (decoded by byte "
                       "permutes); us_reference_layout: the same GEMM on TernaryTensor::packed "
                       "as the reference lays it out (decoded through an LDS table)",
@@ -794,6 +829,8 @@ def compact(result):
     per-entry method strings, is what --full-json writes."""
     comp = result.get("components", {})
     line = {k: result[k] for k in result if k != "components"}
+    if "prefill_ksweep" in line:
+        line["prefill_ksweep"] = _pick(line["prefill_ksweep"], "k", "us", "fixed_us", "loop_us")
     if "cpu_baseline" in line:
         cb = line["cpu_baseline"]
         line["cpu_baseline"] = dict(_pick(cb, "value", "unit", "cores", "kind", "sample"),
@@ -852,6 +889,7 @@ def compact(result):
         if e.get("counters"):
             c4["mfma_busy"] = e["counters"].get("mfma_busy")
             c4["clock_ghz"] = e["counters"].get("clock_ghz")
+            c4["counter_run_us"] = e["counters"].get("duration_us_under_counters")
         if "cpu_baseline" in e:
             c4["cpu_us"] = e["cpu_baseline"]["us"]
             c4["cpu_cores"] = 1
@@ -926,6 +964,8 @@ def main():
             result["cpu_baseline"] = cpu_baseline(state)
         del state
         torch.cuda.empty_cache()
+        log("prefill: the same M and N at K = 1024..4096")
+        result["prefill_ksweep"] = prefill_ksweep(H, W, dev, args.steps, args.warmup)
     if args.only in ("all", "gemv"):
         log("decode GEMV: 6 shapes")
         components["w8a8_decode_gemv"] = bench_gemv(H, W, dev, args.steps, floor, with_cpu)

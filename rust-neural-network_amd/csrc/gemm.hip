@@ -1638,6 +1638,52 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_wl_kernel(
     epi.store_ops(em, n0 + en, (int32_t)sum, eo);
 }
 
+// Single-row decode GEMV (M = 1, K % 4096 == 0): one weight row per wave and
+// two waves per workgroup, so the grid is N/2 small workgroups that the
+// dispatcher deals out to CUs as they free up -- the launch shape of a plain
+// streaming read -- instead of 16-row tiles dealt out whole. Per 4 KiB of the
+// row a lane loads 4 x 16 bytes (each instruction 1 KiB contiguous over the
+// wave, non-temporal) and the same 64 bytes of x (4 KiB shared by every wave,
+// L1/L2 hits), forms the int8 dot products with v_dot4_i32_i8 (no clamp),
+// and the wave's 64 partial sums are added by lane exchanges; lane 0 runs the
+// epilogue. K <= 65536 bounds every partial and total sum by 2^30, so no
+// int32 sum can wrap. Measured by graph replay against the per-tile and
+// balanced-row kernels, weights rotated past the MALL: N = 11008 8.47 vs
+// 9.18 us (same-bytes read floor 8.03), N = 4096 4.59 vs 4.77 (4.13),
+// K = 8192, N = 4096 6.90 vs 7.80 (6.42); at M = 2 (x loaded per wave
+// twice) 9.62 vs 9.21, so only M = 1 takes it.
+constexpr int kRowWaves = 2;
+constexpr int64_t kRowMaxK = 65536;
+__global__ __launch_bounds__(kRowWaves * 64) void gemv_row_kernel(
+    const int8_t *__restrict__ A, const int8_t *__restrict__ W, int64_t N, int64_t K,
+    Epilogue epi) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int64_t n = (int64_t)blockIdx.x * kRowWaves + wid;
+    // a row past N (the last workgroup of an odd N) re-reads row N-1 and
+    // stores nothing
+    const int8_t *wr = W + std::min<int64_t>(n, N - 1) * K + lane * 16;
+    const int8_t *xr = A + lane * 16;
+    int32_t acc = 0;
+    for (int64_t kc = 0; kc < K; kc += 4096) {
+        v4i x[4], w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const v4i *>(xr + kc + u * 1024);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            w[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wr + kc + u * 1024));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            acc = __builtin_amdgcn_sdot4(w[u].x, x[u].x, acc, false);
+            acc = __builtin_amdgcn_sdot4(w[u].y, x[u].y, acc, false);
+            acc = __builtin_amdgcn_sdot4(w[u].z, x[u].z, acc, false);
+            acc = __builtin_amdgcn_sdot4(w[u].w, x[u].w, acc, false);
+        }
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) acc += __shfl_xor(acc, s, 64);
+    if (lane == 0) epi.store(0, n, acc);
+}
+
 // Decode GEMV over balanced row ranges: workgroup b of G (8 waves, at most
 // one per CU) owns weight rows [b*N/G, (b+1)*N/G), processed as up to TPW
 // 16-row tiles. Its loads are all issued up front, in this order: the
@@ -2015,6 +2061,11 @@ static int launch_gemv(const int8_t *A, const int8_t *W, int64_t M, int64_t N, i
     // 4.84 vs 5.39 (<4,4>), M = 8 4.92 vs 5.24 (<4,8>); N = 11008: M = 16
     // 10.56 (the <4,16> kernel 13.6), not taken: M = 1 10.26 vs 9.17 (<4,4>),
     // M = 4 10.63 vs 9.59, M = 8 10.72 vs 10.33 (<4,8>).
+    // M = 1 over at least 512 rows: the single-row kernel above.
+    if (M == 1 && K % 4096 == 0 && K <= kRowMaxK && N >= 512 && ceil_div(N, kRowWaves) <= 0x7fffffff) {
+        gemv_row_kernel<<<(unsigned)ceil_div(N, kRowWaves), kRowWaves * 64, 0, st>>>(A, W, N, K, epi);
+        return check_launch(name);
+    }
     const unsigned wgs = (unsigned)ceil_div(N, 16);
     if ((M > 8 || (int64_t)wgs <= device_cu_count()) && launch_gemv_rows(A, W, M, N, K, epi, st))
         return check_launch(name);

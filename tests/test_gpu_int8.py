@@ -314,6 +314,46 @@ def test_w8a8_gemv_balanced_rows(dev, hip, m, k, n):
     assert np.array_equal(host(acc2), acce)
 
 
+@pytest.mark.parametrize("k,n", [(4096, 512), (4096, 1001), (8192, 1025), (65536, 513),
+                                 (69632, 520), (4096, 511), (12288, 11008)])
+def test_w8a8_gemv_single_row(dev, hip, k, n):
+    """The single-row GEMV (M = 1, K % 4096 == 0, K <= 65536, N >= 512): odd N
+    (the last workgroup's second wave stores nothing), several 4 KiB K
+    chunks, the largest K it takes, and the shapes just outside it (K =
+    69632, N = 511: the other kernels) -- int32 and fp32 bit-exact against
+    the oracle with bias + ReLU and with the accumulator alone, and equal to
+    the tiled kernel bit for bit. Activations with outliers and the int8
+    extremes -128 / 127 in both operands."""
+    aq, sa, wq, sw, bias = w8a8_case(1, k, n, seed=k + n, outliers=0.01)
+    aq[0, :64] = -128
+    aq[0, 64:128] = 127
+    wq[:3, :128] = -128
+    wq[3:6, :128] = 127
+    ye, acce = O.w8a8_linear(aq, sa, wq, sw, bias, True)
+    d = [to_dev(a, dev) for a in (aq, sa, wq, sw, bias)]
+    y, acc = hip.w8a8_linear(*d, relu=True, want_acc=True)
+    assert np.array_equal(host(acc), acce)
+    assert_f32_equal(host(y), ye)
+    _, acc2 = hip.w8a8_linear(d[0], None, d[2], None, None, want_y=False, want_acc=True)
+    assert np.array_equal(host(acc2), acce)
+    y3, acc3 = hip.w8a8_linear(*d, relu=True, want_acc=True, algo=hip.ALGO_TILED)
+    assert np.array_equal(host(acc3), acce) and np.array_equal(host(y3), host(y))
+
+
+def test_igemm_single_row_gemv(dev, hip):
+    """igemm at M = 1 above the one-launch size (m n k > 2^28): the packed
+    operands go through the single-row GEMV with the zero-point column sums
+    in its epilogue, against the oracle over the full u8 range."""
+    m, k, n = 1, 4096, 70000
+    a = (np.arange(m * k) % 251).astype(np.uint8).reshape(m, k)
+    b = (np.arange(k * n) % 255).astype(np.uint8).view(np.int8).reshape(k, n)
+    import torch
+    ws = torch.empty(hip.igemm_workspace_size(m, k, n), dtype=torch.uint8, device=dev)
+    got = host(hip.igemm(to_dev(a, dev), to_dev(b, dev), m, k, n, workspace=ws))
+    exp, _ = O.igemm(a, b, m, k, n, 8)
+    assert np.array_equal(got, exp)
+
+
 def test_w8a8_prefill_full_size_sampled_rows(dev, hip):
     """BASELINE prefill config (2048 x 4096 x 14336): every output of 24
     sampled rows (covering all 16 row tiles) against the oracle, plus the
