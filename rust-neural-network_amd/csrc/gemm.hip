@@ -1686,25 +1686,36 @@ __global__ __launch_bounds__(kRowWaves * 64) void gemv_row_kernel(
 
 // Decode GEMV over balanced row ranges: workgroup b of G (8 waves, at most
 // one per CU) owns weight rows [b*N/G, (b+1)*N/G), processed as up to TPW
-// 16-row tiles. Its loads are all issued up front, in this order: the
-// activations of each wave's K range (K/8 bytes of each row < M, in whole
-// cache lines; loaded once for all tiles, where the per-tile kernels below
-// load them once per tile, as many bytes as the weights at M = 16), the
-// epilogue operands, then every weight byte of every tile, tile by tile, so
-// the row range is in flight from the start. Weights and
-// activations are read through buffer descriptors that end at the range's
-// last row and at row M - 1: the rows that pad a tile to 16 read zeros and
-// fetch nothing. Balanced ranges keep every CU's byte count within one row of
-// the others (16-row tiles dealt out whole leave up to 12% of the CUs' time
-// idle, e.g. 688 tiles over 256 CUs). Each wave takes K/8 of a tile:
-// whole-line weight loads (4 rows x 256 bytes per instruction,
-// non-temporal), regrouped into MFMA fragments through the wave's LDS slice,
-// 256 bytes of each row at a time (16-byte chunk c of row r at c ^ r),
-// 16x16x64 MFMAs against the activation fragments (regrouped once through
-// the same slice and held in registers for all tiles), then the 8 partial
-// tiles are summed through LDS (exact: wrapping int32) and the epilogue runs
-// once per output. Barriers order LDS only, so the later tiles' loads stay in
-// flight while earlier tiles compute. K = 2048 * H bytes (H = 1, 2).
+// 16-row tiles. First the activations of each wave's K range (K/8 bytes of
+// each row < M, in whole cache lines; loaded once for all tiles, where the
+// per-tile kernels below load them once per tile, as many bytes as the
+// weights at M = 16) and the epilogue operands; then the weights as a stream
+// of 1 KiB load units (4 rows x 256 bytes of the wave's K range, tile by
+// tile), with P units in flight per wave: a unit is issued as the one P
+// earlier has been written to LDS. Weights and activations are read through
+// buffer descriptors that end at the range's last row and at row M - 1: the
+// rows that pad a tile to 16 read zeros and fetch nothing. Balanced ranges
+// keep every CU's byte count within one row of the others (16-row tiles dealt
+// out whole leave up to 12% of the CUs' time idle, e.g. 688 tiles over 256
+// CUs). Each wave takes K/8 of a tile: the units (non-temporal) are regrouped
+// into MFMA fragments through the wave's LDS slice, 256 bytes of each row at
+// a time (16-byte chunk c of row r at c ^ r), 16x16x64 MFMAs against the
+// activation fragments (regrouped once through the same slice and held in
+// registers for all tiles), then the 8 partial tiles are summed through LDS
+// (exact: wrapping int32) and the epilogue runs once per output. K = 2048 * H
+// bytes (H = 1, 2).
+//
+// The window: a plain read of 45 MB by one workgroup per CU, each streaming
+// its contiguous share, takes 8.8 us with 32 KiB in flight per CU (4 or 8
+// waves x 8 or 4 KiB), 9.2 with 24 KiB, 9.1 with 64 KiB and 10.7 with 192
+// KiB (the same bytes by small streaming workgroups: 7.9). Issuing every
+// weight load up front (192 KiB per CU at M = 16, N = 11008) cost the GEMV
+// the difference. Measured against that, K = 4096 (us, graph replay, weights
+// rotated past the MALL): N = 11008 M = 16 10.54 -> 9.32 (P = 8; 9.55 at P =
+// 4), M = 8 10.17 -> 9.07 (per-tile kernel before), M = 4 9.51 -> 8.98;
+// N = 4096 M = 16 5.16 -> 5.05 (P = 4), M = 8 4.87 -> 4.70; N = 16383 M = 16
+// 14.12 -> 12.28; K = 2048, N = 11008 M = 16 6.04 -> 5.73 (P = 4; 6.47 at
+// P = 8), M = 8 7.98 -> 5.63.
 constexpr int kGlWaves = 8;
 
 __device__ __forceinline__ void lds_only_barrier() {
@@ -1713,7 +1724,7 @@ __device__ __forceinline__ void lds_only_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int TPW, int H>
+template <int TPW, int H, int P>
 __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
     const int8_t *__restrict__ A, const int8_t *__restrict__ W, int64_t M, int64_t N,
     Epilogue epi) {
@@ -1722,6 +1733,8 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
     constexpr int KB = KW / 64;        // MFMA k-steps per wave and tile
     constexpr int LPR = KW / 16;       // lanes per activation row in a whole-line load
     constexpr int RPI = 64 / LPR;      // activation rows per load instruction
+    constexpr int UPT = 4 * H;         // weight load units per wave and tile
+    constexpr int U = TPW * UPT;
     static_assert(RPI * KB == 16, "KB whole-line loads cover the 16 activation rows");
     // per wave: the 16 activation rows of its K range (regrouped once), then
     // 256 bytes of each of the 16 weight rows at a time
@@ -1733,10 +1746,10 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
     // first, so its slices should not be one contiguous half of every row:
     // with one workgroup per CU, slices are interleaved (0, 2, 4, 6 for waves
     // 0-3); with several tiles per workgroup, rotated by the workgroup, so
-    // that the CUs' concurrent requests spread over the whole rows. (Measured,
-    // K = 4096, M = 16: N = 4096 6.5 us with slices in wave order, 5.7
-    // interleaved; N = 11008 12.5 in wave order, 11.0 rotated; the barriers
-    // between tiles' loads gave 12.5 -> 11.5 before the rotation.)
+    // that the CUs' concurrent requests spread over the whole rows. (Measured
+    // with every load issued up front, K = 4096, M = 16: N = 4096 6.5 us with
+    // slices in wave order, 5.7 interleaved; N = 11008 12.5 in wave order,
+    // 11.0 rotated.)
     const int k0 = (TPW == 1 ? 2 * (wid & 3) + (wid >> 2) : (wid + blockIdx.x) & 7) * KW;
     // (32-bit: the launch keeps N <= 64 rows per CU)
     const uint32_t r0 = blockIdx.x * (uint32_t)N / gridDim.x;
@@ -1763,27 +1776,21 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
     EpiOps eo[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) eo[i] = epi.load_ops(em, r0 + std::min(16 * i + en, nrows - 1));
-    // 3. every weight byte of the row range
-    v4i w[TPW][4][H];
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-            for (int h = 0; h < H; ++h)
-                w[i][g][h] = __builtin_bit_cast(
-                    v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                             wr, (16 * i + 4 * g + q) * K + k0 + 256 * h + 16 * row, 0, 2 /* nt */));
-        // tile-major issue: a SIMD issues its older wave's loads first, so
-        // without this barrier the CU would request waves 0-3's bytes of
-        // every tile before waves 4-7's bytes of the first
-        if (i + 1 < TPW) {
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_sched_barrier(0);
+    // 3. the first P weight units. Unit u: tile u / UPT, 256-byte half
+    //    (u % UPT) / 4 of the wave's K range, rows 4 (u % 4) + q of the tile.
+    v4i wv[U];
+    auto issue = [&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        if constexpr (u < U) {
+            constexpr int i = u / UPT, h = (u % UPT) / 4, g = u % 4;
+            wv[u] = __builtin_bit_cast(
+                v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                         wr, (16 * i + 4 * g + q) * K + k0 + 256 * h + 16 * row, 0, 2 /* nt */));
         }
-    }
-    // keep every load above ahead of the first wait
+    };
+    static_for<P>([&](auto uc) { issue(uc); });
+    // (sched_barrier: the compiler would otherwise hoist the later units'
+    // loads up here)
     __builtin_amdgcn_sched_barrier(0);
 
     // the activation fragments (lane (row, q) of step kb: row `row`, bytes
@@ -1799,31 +1806,34 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
         a[kb] = *reinterpret_cast<const v4i *>(st + row * KW + 16 * ((4 * kb + q) ^ row));
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
+    static_for<TPW>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
         // (no early exit for a tile past the range: it multiplies zeros and
-        // stores nothing. A branch here would let the compiler sink the
-        // weight loads behind it, out of the prologue.)
-        // regroup: lane (q, row) holds row 4g + q, chunk 16h + row of this
-        // wave's K range; stored at (chunk - 16h) ^ row
-        // 256 bytes of each row at a time (4 KiB per wave); one wave's LDS
-        // operations complete in order, so no barrier is needed between the
-        // writes, the reads and the next half's writes
+        // stores nothing)
         v4i acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int h = 0; h < H; ++h) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
+        static_for<H>([&](auto hc) {
+            constexpr int h = decltype(hc)::value;
+            // regroup: lane (q, row) of unit (i, h, g) holds row 4g + q,
+            // chunk 16h + row of this wave's K range; stored at (chunk - 16h)
+            // ^ row. One wave's LDS operations complete in order, so no
+            // barrier is needed between the writes, the reads and the next
+            // half's writes.
+            static_for<4>([&](auto gc) {
+                constexpr int g = decltype(gc)::value;
+                constexpr int u = i * UPT + h * 4 + g;
                 const int rw = 4 * g + q;
-                *reinterpret_cast<v4i *>(st + rw * 256 + 16 * (row ^ rw)) = w[i][g][h];
-            }
+                *reinterpret_cast<v4i *>(st + rw * 256 + 16 * (row ^ rw)) = wv[u];
+                __builtin_amdgcn_sched_barrier(0);
+                issue(std::integral_constant<int, u + P>{});  // unit u landed: the next one
+                __builtin_amdgcn_sched_barrier(0);
+            });
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
                 const int ch = 4 * kb + q;
                 const v4i b = *reinterpret_cast<const v4i *>(st + row * 256 + 16 * (ch ^ row));
                 acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[4 * h + kb], b, acc, 0, 0, 0);
             }
-        }
+        });
         part[wid][4 * q + 0][row] = acc.x;
         part[wid][4 * q + 1][row] = acc.y;
         part[wid][4 * q + 2][row] = acc.z;
@@ -1836,19 +1846,27 @@ __global__ __launch_bounds__(kGlWaves * 64) void gemv_rows_kernel(
             epi.store_ops(em, r0 + 16 * i + en, (int32_t)sum, eo[i]);
         }
         lds_only_barrier();  // part is rewritten by the next tile
-    }
+    });
 }
+
+// the load window: 8 units (8 KiB per wave) for three or more 4096-byte
+// tiles, else 4
+template <int TPW, int H>
+constexpr int kRowsWindow = H == 2 && TPW >= 3 ? 8 : 4;
 
 template <int H>
 static bool launch_gemv_rows_h(const int8_t *A, const int8_t *W, int64_t M, int64_t N, int grid,
                                int tpw, const Epilogue &epi, hipStream_t st) {
+#define RNN_ROWS(T) \
+    gemv_rows_kernel<T, H, kRowsWindow<T, H>><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi)
     switch (tpw) {
-    case 1: gemv_rows_kernel<1, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
-    case 2: gemv_rows_kernel<2, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
-    case 3: gemv_rows_kernel<3, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
-    case 4: gemv_rows_kernel<4, H><<<grid, kGlWaves * 64, 0, st>>>(A, W, M, N, epi); return true;
+    case 1: RNN_ROWS(1); return true;
+    case 2: RNN_ROWS(2); return true;
+    case 3: RNN_ROWS(3); return true;
+    case 4: RNN_ROWS(4); return true;
     default: return false;
     }
+#undef RNN_ROWS
 }
 
 // The balanced-row GEMV for M <= 16, K in {2048, 4096} and at most 64 rows
@@ -2055,19 +2073,18 @@ static int launch_gemv(const int8_t *A, const int8_t *W, int64_t M, int64_t N, i
     // 6.04 us (N 4096), 10.17 vs 11.31 (N 11008); M = 16 6.21 vs 6.75
     // (N 4096), 14.96 vs 13.57 (N 11008, 688 workgroups: not taken).
     //
-    // The balanced-row kernel (activations loaded once per workgroup) takes
-    // M > 8, and any M while the rows fit one tile per CU. Measured against
-    // the per-tile kernels below, K = 4096 (us, one process): N = 4096: M = 1
-    // 4.84 vs 5.39 (<4,4>), M = 8 4.92 vs 5.24 (<4,8>); N = 11008: M = 16
-    // 10.56 (the <4,16> kernel 13.6), not taken: M = 1 10.26 vs 9.17 (<4,4>),
-    // M = 4 10.63 vs 9.59, M = 8 10.72 vs 10.33 (<4,8>).
-    // M = 1 over at least 512 rows: the single-row kernel above.
+    // M = 1 over at least 512 rows: the single-row kernel above. The
+    // balanced-row kernel (activations loaded once per workgroup, a bounded
+    // load window) takes M >= 2, and M = 1 while the rows fit one tile per
+    // CU; the per-tile kernels below take what it does not (K other than
+    // 2048 and 4096, more than 64 rows per CU). With every weight load issued
+    // up front it lost to the per-tile kernels at N = 11008, M <= 8.
     if (M == 1 && K % 4096 == 0 && K <= kRowMaxK && N >= 512 && ceil_div(N, kRowWaves) <= 0x7fffffff) {
         gemv_row_kernel<<<(unsigned)ceil_div(N, kRowWaves), kRowWaves * 64, 0, st>>>(A, W, N, K, epi);
         return check_launch(name);
     }
     const unsigned wgs = (unsigned)ceil_div(N, 16);
-    if ((M > 8 || (int64_t)wgs <= device_cu_count()) && launch_gemv_rows(A, W, M, N, K, epi, st))
+    if ((M > 1 || (int64_t)wgs <= device_cu_count()) && launch_gemv_rows(A, W, M, N, K, epi, st))
         return check_launch(name);
     if (K % 4096 == 0 && M <= 4)
         gemv_wl_kernel<4, 4><<<wgs, 256, 0, st>>>(A, W, M, N, K, epi);

@@ -295,15 +295,18 @@ def test_w8a8_gemv_whole_line_variants(dev, hip, m, k, n):
 @pytest.mark.parametrize("m,k,n", [(1, 4096, 4100), (3, 2048, 11008), (5, 4096, 14336),
                                    (8, 2048, 16), (9, 4096, 4096), (16, 4096, 12289),
                                    (16, 2048, 7), (13, 4096, 16400), (4, 4096, 1), (2, 4096, 300),
-                                   (11, 2048, 16383)])
+                                   (11, 2048, 16383), (8, 4096, 11008), (2, 4096, 11008),
+                                   (4, 2048, 11008), (6, 4096, 5000), (16, 2048, 16383),
+                                   (7, 4096, 16384)])
 def test_w8a8_gemv_balanced_rows(dev, hip, m, k, n):
     """The balanced-row GEMV (M <= 16, K = 2048 or 4096, up to 64 rows per
-    workgroup on a 256-CU part): 1-4 tiles per workgroup, row ranges that are
-    not multiples of 16 (the last tile padded with zero rows read past the
-    range's buffer descriptor), fewer rows than CUs, rows past M, and a shape
-    with more than 64 rows per CU (the per-tile kernel) -- int32 and fp32
-    bit-exact against the oracle, with bias + ReLU and with the accumulator
-    alone."""
+    workgroup on a 256-CU part): 1-4 tiles per workgroup (load windows of 4
+    and 8 units, the last tiles' units issued while the first compute), row
+    ranges that are not multiples of 16 (the last tile padded with zero rows
+    read past the range's buffer descriptor), fewer rows than CUs, rows past
+    M, exactly 64 rows per CU, and a shape with more than 64 rows per CU (the
+    per-tile kernel) -- int32 and fp32 bit-exact against the oracle, with
+    bias + ReLU and with the accumulator alone."""
     aq, sa, wq, sw, bias = w8a8_case(m, k, n, seed=5 * m + n + k, outliers=0.01)
     ye, acce = O.w8a8_linear(aq, sa, wq, sw, bias, True)
     d = [to_dev(a, dev) for a in (aq, sa, wq, sw, bias)]
