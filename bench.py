@@ -913,6 +913,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="all", choices=["all", "prefill"] + COMPONENTS)
     ap.add_argument("--no-cpu", action="store_true")
+    # (a separate run: its launches share the headline kernel's name, so they
+    # would enter that kernel's rocprofv3 --stats average)
+    ap.add_argument("--ksweep", action="store_true",
+                    help="also time the prefill GEMM at K = 1024..4096 (fixed vs K-loop cost)")
     ap.add_argument("--full-json", default=None,
                     help="also write the full record (every entry with its method) to this file")
     args = ap.parse_args()
@@ -964,8 +968,9 @@ def main():
             result["cpu_baseline"] = cpu_baseline(state)
         del state
         torch.cuda.empty_cache()
-        log("prefill: the same M and N at K = 1024..4096")
-        result["prefill_ksweep"] = prefill_ksweep(H, W, dev, args.steps, args.warmup)
+        if args.ksweep:
+            log("prefill: the same M and N at K = 1024..4096")
+            result["prefill_ksweep"] = prefill_ksweep(H, W, dev, args.steps, args.warmup)
     if args.only in ("all", "gemv"):
         log("decode GEMV: 6 shapes")
         components["w8a8_decode_gemv"] = bench_gemv(H, W, dev, args.steps, floor, with_cpu)
