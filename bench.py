@@ -778,6 +778,43 @@ def bench_copy(dev, steps):
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_launch": 2 * COPY_BYTES}
 
 
+# ---------------------------------------------------------------- load window
+def bench_read_window(dev, floor):
+    """Streaming reads of the decode GEMV's weight bytes (4096 x 11008 and
+    4096 x 4096) in the launch shape of the balanced-row GEMV -- one workgroup
+    per CU streaming its contiguous share -- at several depths of loads in
+    flight per CU (waves x loads per lane x 1 KiB), beside the read floor
+    (small streaming workgroups). The same buffer rotation and graph timing as
+    the GEMV. It measures how the in-flight depth of one-workgroup-per-CU
+    streams sets their rate, which fixes the GEMV's load window."""
+    import torch
+    lib = floor.lib
+    lib.rnn_probe_range_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_uint32,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = {}
+    for nbytes in (4096 * 11008, 4096 * 4096):
+        copies = max(2, -(-640 * 2**20 // nbytes))
+        bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev)
+                for _ in range(copies)]
+        n_launch = 15 * copies if nbytes > 2**25 else 40 * copies
+        ent = {"floor_us": round(_floor(floor, bufs, nbytes, n_launch) * 1e3, 3)}
+        for waves, per in ((4, 2), (4, 4), (4, 8), (4, 24), (8, 2), (8, 4), (8, 8), (8, 24)):
+            def launch(i, waves=waves, per=per):
+                rc = lib.rnn_probe_range_read(
+                    ctypes.c_void_p(bufs[i % copies].data_ptr()), nbytes, cus, waves, per,
+                    0x9E3779B9, ctypes.c_void_p(floor.sink.data_ptr()),
+                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                if rc != 0:
+                    raise RuntimeError("rnn_probe_range_read failed")
+            ms = graph_timed(launch, n_launch)
+            ent[f"w{waves}_p{per}_{waves * per}KiB_us"] = round(ms * 1e3, 3)
+        out[f"{nbytes}_bytes"] = ent
+        del bufs
+    return out
+
+
 # ---------------------------------------------------------------- clock probe
 def bench_clock_probe(dev):
     """The shader clock under a plain int8 MFMA load: librnn_probe.so's
@@ -812,7 +849,7 @@ def bench_clock_probe(dev):
 
 
 COMPONENTS = ["gemv", "mlp", "ternary", "rotorquant", "rq_attention", "qt_gemv", "igemm512",
-              "sgemm", "copy", "clock"]
+              "sgemm", "copy", "clock", "window"]
 
 # QuantizedLinear entries carried on the printed line (all of them go to --full-json)
 QT_LINE = ("INT4_g128_m1_k4096_n11008", "INT4_g128_m16_k4096_n11008", "GGUF_Q8_0_m16_k4096_n11008")
@@ -1001,6 +1038,10 @@ def main():
     if args.only in ("all", "clock") and os.path.exists(PROBE_LIB):
         log("MFMA clock probe")
         components["mfma_clock_probe"] = bench_clock_probe(dev)
+    # (not part of "all": a study of the GEMV's load window, run on its own)
+    if args.only == "window" and floor is not None:
+        log("one-workgroup-per-CU streaming reads at several load depths")
+        components["read_window"] = bench_read_window(dev, floor)
     if components:
         result["components"] = components
     if "value" not in result:  # a single non-headline component was requested

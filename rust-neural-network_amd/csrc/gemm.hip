@@ -1705,14 +1705,15 @@ __global__ __launch_bounds__(kRowWaves * 64) void gemv_row_kernel(
 // (exact: wrapping int32) and the epilogue runs once per output. K = 2048 * H
 // bytes (H = 1, 2).
 //
-// The window: a plain read of 45 MB by one workgroup per CU, each streaming
-// its contiguous share, takes 8.8 us with 32 KiB in flight per CU (4 or 8
-// waves x 8 or 4 KiB), 9.2 with 24 KiB, 9.1 with 64 KiB and 10.7 with 192
-// KiB (the same bytes by small streaming workgroups: 7.9). Issuing every
-// weight load up front (192 KiB per CU at M = 16, N = 11008) cost the GEMV
-// the difference. Measured against that, K = 4096 (us, graph replay, weights
-// rotated past the MALL): N = 11008 M = 16 10.54 -> 9.32 (P = 8; 9.55 at P =
-// 4), M = 8 10.17 -> 9.07 (per-tile kernel before), M = 4 9.51 -> 8.98;
+// The window: plain reads of the same bytes in this launch shape (one
+// workgroup per CU streaming its contiguous share; librnn_probe.so's range
+// read) are fastest with 8 waves and 4 to 8 loads of 1 KiB in flight per
+// wave: 45 MB in 8.38 us at 32 KiB per CU, 8.58 at 192 KiB; 16.8 MB in 4.21
+// and 7.56 us (small streaming workgroups: 7.90 and 4.19). Measured against
+// the previous kernel, which issued every weight load up front (192 KiB per
+// CU at M = 16, N = 11008) with a barrier between tiles' loads, K = 4096
+// (us, graph replay, weights rotated past the MALL): N = 11008 M = 16 10.54 -> 9.32 (P = 8; 9.55 at P = 4),
+// M = 8 10.17 -> 9.07 (the per-tile kernel before), M = 4 9.51 -> 8.98;
 // N = 4096 M = 16 5.16 -> 5.05 (P = 4), M = 8 4.87 -> 4.70; N = 16383 M = 16
 // 14.12 -> 12.28; K = 2048, N = 11008 M = 16 6.04 -> 5.73 (P = 4; 6.47 at
 // P = 8), M = 8 7.98 -> 5.63.

@@ -73,6 +73,64 @@ extern "C" int rnn_probe_read(const void *p, int64_t bytes, uint32_t magic, uint
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
+// ---------------------------------------------------------------- range read
+// One workgroup of WAVES waves per CU-sized share: workgroup g reads the
+// contiguous 1 KiB chunks [g*C/G, (g+1)*C/G) of the buffer (C chunks, G
+// workgroups), wave w taking chunks w, w + WAVES, ... of its share, PER loads
+// (16 bytes per lane, non-temporal) issued before any is used: each workgroup
+// keeps WAVES * PER KiB in flight. The access pattern of a GEMV whose
+// workgroups each stream one row range, at a chosen depth of loads in flight.
+// Every load stays inside the share (the last loop step re-reads the share's
+// first chunk where its own would pass the end, and discards it).
+template <int WAVES, int PER>
+__global__ __launch_bounds__(WAVES * 64) void range_read_kernel(const u32x4 *__restrict__ p,
+                                                                 int64_t nchunks, uint32_t magic,
+                                                                 uint32_t *sink) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t g = blockIdx.x, G = gridDim.x;
+    const int64_t c0 = nchunks * g / G, c1 = nchunks * (g + 1) / G;
+    uint32_t acc = 0;
+    for (int64_t j0 = 0; c0 + w + (int64_t)WAVES * j0 < c1; j0 += PER) {
+        u32x4 v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int64_t c = c0 + w + (int64_t)WAVES * (j0 + u);
+            v[u] = __builtin_nontemporal_load(p + (c < c1 ? c : c0) * 64 + lane);
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u)
+            if (c0 + w + (int64_t)WAVES * (j0 + u) < c1) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (int off = 32; off > 0; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
+    if (lane == 0 && acc == magic) atomicXor(sink, acc);
+}
+
+// Reads `bytes` (a multiple of 1024, 16-byte aligned, at least `groups` KiB)
+// from p with `groups` workgroups of `waves` (4 or 8) waves, each keeping
+// `per_lane` (2, 4, 8 or 24) loads per lane in flight. Returns 0, or 1 for bad
+// arguments / a failed launch.
+extern "C" int rnn_probe_range_read(const void *p, int64_t bytes, int groups, int waves,
+                                    int per_lane, uint32_t magic, uint32_t *sink, void *stream) {
+    if (bytes <= 0 || bytes % 1024 != 0 || ((uintptr_t)p & 15) != 0 || sink == nullptr ||
+        groups <= 0 || bytes / 1024 < groups)
+        return 1;
+    const u32x4 *q = reinterpret_cast<const u32x4 *>(p);
+    const int64_t nc = bytes / 1024;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define RNN_RR(W, P) range_read_kernel<W, P><<<(unsigned)groups, (W) * 64, 0, st>>>(q, nc, magic, sink)
+    if (waves == 4 && per_lane == 2) RNN_RR(4, 2);
+    else if (waves == 4 && per_lane == 4) RNN_RR(4, 4);
+    else if (waves == 4 && per_lane == 8) RNN_RR(4, 8);
+    else if (waves == 4 && per_lane == 24) RNN_RR(4, 24);
+    else if (waves == 8 && per_lane == 2) RNN_RR(8, 2);
+    else if (waves == 8 && per_lane == 4) RNN_RR(8, 4);
+    else if (waves == 8 && per_lane == 8) RNN_RR(8, 8);
+    else if (waves == 8 && per_lane == 24) RNN_RR(8, 24);
+    else return 1;
+#undef RNN_RR
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
 // ---------------------------------------------------------------- clock probe
 // A fixed amount of int8 MFMA work on constant operands, one wave per SIMD on
 // every CU, with the shader-clock counter (s_memtime) and the 100 MHz
