@@ -1,9 +1,10 @@
-"""The benchmark's read-floor helper (librnn_probe.so, rnn_probe_read): it must
-read every byte it is given, or the floor it times would be too fast. One
-planted 16-byte word in an otherwise zero buffer makes exactly one block's XOR
-equal the magic value, and only then is the sink written; the cases put it at
-the start, in the middle and in the last chunk, including a ragged last
-block."""
+"""The benchmark's read helpers (librnn_probe.so: rnn_probe_read, the read
+floor, and rnn_probe_range_read, the one-workgroup-per-share read): each must
+read every byte it is given, or the rate it times would be too high. One
+planted 16-byte word in an otherwise zero buffer makes exactly one block's
+(range read: one wave's) XOR equal the magic value, and only then is the sink
+written; the cases put it at the start, in the middle and in the last chunk,
+including a ragged last block."""
 import ctypes
 import os
 
@@ -36,3 +37,33 @@ def test_read_floor_reads_every_chunk(dev, nbytes, where, per):
                               ctypes.c_void_p(sink.data_ptr()), 16, ctypes.c_void_p(st)) == 1
     assert lib.rnn_probe_read(ctypes.c_void_p(buf.data_ptr()), 64, magic,
                               ctypes.c_void_p(sink.data_ptr()), 3, ctypes.c_void_p(st)) == 1
+
+
+@pytest.mark.parametrize("nbytes,where,groups,waves,per",
+                         [(1 << 20, 0, 256, 8, 4), (1 << 20, (1 << 20) - 16, 256, 4, 24),
+                          (45088768, 22544384 + 48, 256, 8, 8), (300 * 1024, 299 * 1024 + 512, 7, 4, 2),
+                          (64 * 1024, 33 * 1024, 64, 8, 24)])
+def test_range_read_reads_every_chunk(dev, nbytes, where, groups, waves, per):
+    """rnn_probe_range_read (one workgroup per share, a chosen load depth):
+    the same planted-word check, with shares of one chunk, ragged shares
+    (300 chunks over 7 workgroups) and a depth larger than a wave's part of
+    its share."""
+    import torch
+    lib = ctypes.CDLL(PROBE)
+    lib.rnn_probe_range_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_uint32,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
+    magic = 0x5EED4321
+    buf[where // 4] = magic
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = ctypes.c_void_p(buf.data_ptr())
+    assert lib.rnn_probe_range_read(p, nbytes, groups, waves, per, magic,
+                                    ctypes.c_void_p(sink.data_ptr()), st) == 0
+    assert int(sink.item()) == magic
+    # bad arguments: a ragged byte count, fewer chunks than workgroups, an
+    # unbuilt depth
+    assert lib.rnn_probe_range_read(p, 1000, 1, 4, 4, magic, ctypes.c_void_p(sink.data_ptr()), st) == 1
+    assert lib.rnn_probe_range_read(p, 4096, 8, 4, 4, magic, ctypes.c_void_p(sink.data_ptr()), st) == 1
+    assert lib.rnn_probe_range_read(p, 4096, 1, 4, 3, magic, ctypes.c_void_p(sink.data_ptr()), st) == 1
