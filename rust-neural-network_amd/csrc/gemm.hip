@@ -1663,6 +1663,9 @@ __global__ __launch_bounds__(kRowWaves * 64) void gemv_row_kernel(
     // stores nothing
     const int8_t *wr = W + std::min<int64_t>(n, N - 1) * K + lane * 16;
     const int8_t *xr = A + lane * 16;
+    // the epilogue operands first: loaded after the sum they would add a
+    // dependent round trip to every wave's tail
+    const EpiOps eo = epi.load_ops(0, n);
     int32_t acc = 0;
     for (int64_t kc = 0; kc < K; kc += 4096) {
         v4i x[4], w[4];
@@ -1681,7 +1684,7 @@ __global__ __launch_bounds__(kRowWaves * 64) void gemv_row_kernel(
     }
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) acc += __shfl_xor(acc, s, 64);
-    if (lane == 0) epi.store(0, n, acc);
+    if (lane == 0) epi.store_ops(0, n, acc, eo);
 }
 
 // Decode GEMV over balanced row ranges: workgroup b of G (8 waves, at most
