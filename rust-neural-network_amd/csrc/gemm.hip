@@ -1715,11 +1715,11 @@ __global__ __launch_bounds__(kRowWaves * 64) void gemv_row_kernel(
 // and 7.56 us (small streaming workgroups: 7.90 and 4.19). Measured against
 // the previous kernel, which issued every weight load up front (192 KiB per
 // CU at M = 16, N = 11008) with a barrier between tiles' loads, K = 4096
-// (us, graph replay, weights rotated past the MALL): N = 11008 M = 16 10.54 -> 9.32 (P = 8; 9.55 at P = 4),
-// M = 8 10.17 -> 9.07 (the per-tile kernel before), M = 4 9.51 -> 8.98;
-// N = 4096 M = 16 5.16 -> 5.05 (P = 4), M = 8 4.87 -> 4.70; N = 16383 M = 16
-// 14.12 -> 12.28; K = 2048, N = 11008 M = 16 6.04 -> 5.73 (P = 4; 6.47 at
-// P = 8), M = 8 7.98 -> 5.63.
+// (us, graph replay, weights rotated past the MALL): N = 11008 M = 16
+// 10.54 -> 9.32 (P = 8; 9.55 at P = 4), M = 8 10.17 -> 9.07 (the per-tile
+// kernel before), M = 4 9.51 -> 8.98; N = 4096 M = 16 5.16 -> 5.05 (P = 4),
+// M = 8 4.87 -> 4.70; N = 16383 M = 16 14.12 -> 12.28; K = 2048, N = 11008
+// M = 16 6.04 -> 5.73 (P = 4; 6.47 at P = 8), M = 8 7.98 -> 5.63.
 constexpr int kGlWaves = 8;
 
 __device__ __forceinline__ void lds_only_barrier() {
