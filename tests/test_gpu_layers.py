@@ -121,13 +121,17 @@ def test_ternary_int8_forward_follows_replaced_weights(dev):
                                          # 2, 4, 8 and 16 rows per workgroup (256 CUs)
                                          (300, (784, 256, 128, 10), True),
                                          (777, (784, 256, 128, 10), True),
-                                         (1500, (128, 64, 10), True), (4111, (64, 32), False)])
+                                         (1500, (128, 64, 10), True), (4111, (64, 32), False),
+                                         # 4 and 8 loads of x per thread (8 and 16 rows of 1024)
+                                         (1100, (1024, 32), True), (2100, (1024, 64, 10), True)])
 def test_w8a8_mlp_one_launch_matches_chain(dev, hip, m, dims, relu):
     """rnn_w8a8_mlp against the oracle chain (per-row quantization + W8A8 +
     epilogue per layer, ReLU between), bit for bit; batches that give 1, 2,
-    4, 8 and 16 rows of x per workgroup (the MFMAs' other rows zero), rows
-    beyond a multiple of the workgroup's and widths that are not multiples of
-    16 included; the per-layer launches must give the same bits."""
+    4, 8 and 16 rows of x per workgroup (the MFMAs' other rows zero; 8, 4, 2
+    and 1 waves per row in the quantization pass) and 1 to 8 loads of x per
+    thread, rows beyond a multiple of the workgroup's and widths that are not
+    multiples of 16 included; the per-layer launches must give the same
+    bits."""
     params = []
     for i, (fi, fo) in enumerate(zip(dims[:-1], dims[1:])):
         params += [W.weights(fo, fi, seed=60 + i), W.weights(1, fo, seed=70 + i)[0]]
