@@ -815,6 +815,42 @@ def bench_read_window(dev, floor):
     return out
 
 
+def bench_l2_rate(dev, steps):
+    """The rate at which a CU takes in L2-resident data (librnn_probe.so's
+    l2_rate_kernel): one block of 8 waves per CU, each wave reading its own
+    64 KiB window of a 4 MiB buffer (resident in every XCD's L2 after the
+    first launch) 1 MiB over, with 4 or 8 loads of 1 KiB in flight, into VGPRs
+    or into LDS (the GEMM kernels' DMA). It prices the operand bytes a GEMM
+    block pulls through its CU."""
+    import torch
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.rnn_probe_l2_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_uint32, ctypes.c_void_p,
+                                      ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    nbytes = 4 << 20
+    buf = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    per_wave = 1 << 20
+    out = {"buffer_bytes": nbytes, "blocks": cus, "bytes_per_wave": per_wave}
+    for to_lds in (0, 1):
+        for per in (4, 8):
+            def launch(i, to_lds=to_lds, per=per):
+                rc = lib.rnn_probe_l2_rate(ctypes.c_void_p(buf.data_ptr()), nbytes, cus, to_lds, per,
+                                           per_wave // 1024 // per, 0x9E3779B9,
+                                           ctypes.c_void_p(sink.data_ptr()),
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+                if rc != 0:
+                    raise RuntimeError("rnn_probe_l2_rate failed")
+            ms = graph_timed(launch, max(steps, 20))
+            key = f"{'lds' if to_lds else 'vgpr'}_p{per}"
+            out[key + "_us"] = round(ms * 1e3, 2)
+            out[key + "_GBps_per_cu"] = round(8 * per_wave / (ms * 1e-3) / 1e9, 1)
+    out["method"] = ("HIP graph replay: events around each replay, median replay / launches per "
+                     "replay; GB/s per CU = 8 waves x 1 MiB / launch time")
+    return out
+
+
 # ---------------------------------------------------------------- clock probe
 def bench_clock_probe(dev):
     """The shader clock under a plain int8 MFMA load: librnn_probe.so's
@@ -849,7 +885,7 @@ def bench_clock_probe(dev):
 
 
 COMPONENTS = ["gemv", "mlp", "ternary", "rotorquant", "rq_attention", "qt_gemv", "igemm512",
-              "sgemm", "copy", "clock", "window"]
+              "sgemm", "copy", "clock", "window", "l2rate"]
 
 # QuantizedLinear entries carried on the printed line (all of them go to --full-json)
 QT_LINE = ("INT4_g128_m1_k4096_n11008", "INT4_g128_m16_k4096_n11008", "GGUF_Q8_0_m16_k4096_n11008")
@@ -1038,10 +1074,14 @@ def main():
     if args.only in ("all", "clock") and os.path.exists(PROBE_LIB):
         log("MFMA clock probe")
         components["mfma_clock_probe"] = bench_clock_probe(dev)
-    # (not part of "all": a study of the GEMV's load window, run on its own)
+    # (not part of "all": studies of the GEMV's load window and of the
+    # per-CU load rate, run on their own)
     if args.only == "window" and floor is not None:
         log("one-workgroup-per-CU streaming reads at several load depths")
         components["read_window"] = bench_read_window(dev, floor)
+    if args.only == "l2rate" and os.path.exists(PROBE_LIB):
+        log("per-CU rate of L2-resident loads into VGPRs and into LDS")
+        components["l2_load_rate"] = bench_l2_rate(dev, args.steps)
     if components:
         result["components"] = components
     if "value" not in result:  # a single non-headline component was requested

@@ -150,11 +150,11 @@ __global__ __launch_bounds__(kMlpWaves * 64) void w8a8_mlp_kernel(const float *_
     // requested before the current one's MFMAs, and each layer requests the
     // next layer's first tile (when its k <= 256) before its quantization
     // pass, so weight latency overlaps the x load, the quantization passes and
-    // the epilogues. Each CU passes its loads at about 64 bytes a clock, so a
-    // load requested early holds up the waves that request more behind it:
-    // only the first tile goes out with x. Loads complete in issue order, so
-    // each wait is placed behind the loads it needs and in front of the ones
-    // that may stay in flight.
+    // the epilogues. Each CU takes in loads at about 136 GB/s, so a load
+    // requested early holds up the waves that request more behind it: only
+    // the first tile goes out with x. Loads complete in issue order, so each
+    // wait is placed behind the loads it needs and in front of the ones that
+    // may stay in flight.
     MlpTile<kMlpMaxKb> cur, ahead;
     MlpTile<kMlpPrefetchKb> nxt;
     bool have_cur = wid < (args.layer[0].n + 15) / 16;

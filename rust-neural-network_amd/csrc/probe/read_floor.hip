@@ -1,9 +1,11 @@
-// read_floor.hip -- measurement helper for bench.py, not part of the C ABI of
-// include/rnn_hip.h: a streaming read of a device buffer at the best rate a
-// plain kernel reaches (16-byte non-temporal loads, 4 in flight per lane,
-// grid sized to keep every CU busy), so the decode GEMV and QuantizedLinear
-// GEMV can be set beside a same-bytes, read-only floor timed the same way.
-// Built into librnn_probe.so.
+// read_floor.hip -- measurement helpers for bench.py, not part of the C ABI of
+// include/rnn_hip.h, built into librnn_probe.so: a streaming read of a device
+// buffer at the best rate a plain kernel reaches (16-byte non-temporal loads,
+// 4 in flight per lane, grid sized to keep every CU busy), so the decode GEMV
+// and QuantizedLinear GEMV can be set beside a same-bytes, read-only floor
+// timed the same way; the same read with one workgroup per CU at a chosen
+// depth of loads in flight; the per-CU rate of L2-resident loads into VGPRs
+// and into LDS; and a shader-clock probe.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -128,6 +130,75 @@ extern "C" int rnn_probe_range_read(const void *p, int64_t bytes, int groups, in
     else if (waves == 8 && per_lane == 24) RNN_RR(8, 24);
     else return 1;
 #undef RNN_RR
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+// ---------------------------------------------------------- L2 load rate
+// The rate at which a CU takes in L2-resident data, with the loads writing
+// VGPRs (buffer_load_dwordx4) or LDS (buffer_load_dwordx4 ... lds, the GEMM
+// kernels' DMA): blocks of 8 waves, wave (b, w) walking its own 64 KiB window
+// (window (8 b + w) mod the buffer's windows) in `rounds` rounds of PER 1 KiB
+// loads (16 bytes per lane), each round waited for before the next is
+// issued. Load j of a wave reads chunk j mod 64 of its window, so 64 loads
+// read every chunk once. VGPR loads: the XOR of everything a wave loaded;
+// LDS loads: the XOR of what its last round left in LDS. The sink is written
+// only when that XOR equals `magic`.
+template <bool TO_LDS, int PER>
+__global__ __launch_bounds__(512) void l2_rate_kernel(const int8_t *__restrict__ p, uint32_t bytes,
+                                                      int rounds, uint32_t magic, uint32_t *sink) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[TO_LDS ? 8 * PER * 1024 : 16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t base = ((blockIdx.x * 8u + (uint32_t)w) % (bytes >> 16)) << 16;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p), 0, (int)bytes, 0x00020000);
+    uint32_t acc = 0;
+    for (int r = 0; r < rounds; ++r) {
+        u32x4 v[PER];
+#pragma unroll
+        for (int d = 0; d < PER; ++d) {
+            const uint32_t off = base + (uint32_t)(((r * PER + d) & 63) << 10) + 16u * lane;
+            if constexpr (TO_LDS)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs, (__attribute__((address_space(3))) void *)(lds + (w * PER + d) * 1024), 16,
+                    off, 0, 0, 0);
+            else
+                v[d] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if constexpr (!TO_LDS) {
+#pragma unroll
+            for (int d = 0; d < PER; ++d) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+        }
+    }
+    if constexpr (TO_LDS) {
+#pragma unroll
+        for (int d = 0; d < PER; ++d) {
+            const u32x4 t = *reinterpret_cast<const u32x4 *>(lds + (w * PER + d) * 1024 + 16 * lane);
+            acc ^= t.x ^ t.y ^ t.z ^ t.w;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
+    if (lane == 0 && acc == magic) atomicXor(sink, acc);
+}
+
+// `groups` blocks of 8 waves over a buffer of `bytes` (a multiple of 64 KiB,
+// at most 1 GiB, 16-byte aligned), `rounds` rounds of `per_lane` (4 or 8)
+// loads per wave, into VGPRs (to_lds 0) or LDS (1). Returns 0, or 1 for bad
+// arguments / a failed launch.
+extern "C" int rnn_probe_l2_rate(const void *p, int64_t bytes, int groups, int to_lds, int per_lane,
+                                 int rounds, uint32_t magic, uint32_t *sink, void *stream) {
+    if (bytes < 65536 || bytes % 65536 != 0 || bytes > (int64_t)1 << 30 || ((uintptr_t)p & 15) != 0 ||
+        sink == nullptr || groups <= 0 || rounds <= 0 || (to_lds != 0 && to_lds != 1))
+        return 1;
+    const int8_t *q = static_cast<const int8_t *>(p);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define RNN_L2(L, P) l2_rate_kernel<L, P><<<(unsigned)groups, 512, 0, st>>>(q, (uint32_t)bytes, rounds, magic, sink)
+    if (to_lds && per_lane == 4) RNN_L2(true, 4);
+    else if (to_lds && per_lane == 8) RNN_L2(true, 8);
+    else if (!to_lds && per_lane == 4) RNN_L2(false, 4);
+    else if (!to_lds && per_lane == 8) RNN_L2(false, 8);
+    else return 1;
+#undef RNN_L2
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 

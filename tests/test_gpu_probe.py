@@ -1,6 +1,7 @@
 """The benchmark's read helpers (librnn_probe.so: rnn_probe_read, the read
-floor, and rnn_probe_range_read, the one-workgroup-per-share read): each must
-read every byte it is given, or the rate it times would be too high. One
+floor, rnn_probe_range_read, the one-workgroup-per-share read, and
+rnn_probe_l2_rate, the per-CU load rate): each must read what it is given,
+or the rate it times would be too high. One
 planted 16-byte word in an otherwise zero buffer makes exactly one block's
 (range read: one wave's) XOR equal the magic value, and only then is the sink
 written; the cases put it at the start, in the middle and in the last chunk,
@@ -67,3 +68,34 @@ def test_range_read_reads_every_chunk(dev, nbytes, where, groups, waves, per):
     assert lib.rnn_probe_range_read(p, 1000, 1, 4, 4, magic, ctypes.c_void_p(sink.data_ptr()), st) == 1
     assert lib.rnn_probe_range_read(p, 4096, 8, 4, 4, magic, ctypes.c_void_p(sink.data_ptr()), st) == 1
     assert lib.rnn_probe_range_read(p, 4096, 1, 4, 3, magic, ctypes.c_void_p(sink.data_ptr()), st) == 1
+
+
+@pytest.mark.parametrize("to_lds,per,window,chunk", [(0, 4, 5, 10), (0, 8, 13, 0), (1, 4, 9, 63),
+                                                     (1, 8, 2, 60)])
+def test_l2_rate_reads_what_it_times(dev, to_lds, per, window, chunk):
+    """rnn_probe_l2_rate: 2 blocks of 8 waves over 16 windows of 64 KiB, one
+    window per wave, 64 / per rounds: VGPR loads XOR every chunk of the
+    window once; LDS loads leave the last round's chunks (60..63 at 4 per
+    round, 56..63 at 8) in LDS. One planted word makes that wave's XOR the
+    magic value; bad arguments return 1."""
+    import torch
+    lib = ctypes.CDLL(PROBE)
+    lib.rnn_probe_l2_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_uint32,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    nbytes = 16 << 16
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
+    magic = 0x5EED6789
+    buf[(window * 65536 + chunk * 1024 + 16 * 7) // 4] = magic
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = ctypes.c_void_p(buf.data_ptr())
+    assert lib.rnn_probe_l2_rate(p, nbytes, 2, to_lds, per, 64 // per, magic,
+                                 ctypes.c_void_p(sink.data_ptr()), st) == 0
+    assert int(sink.item()) == magic
+    bad = dict(bytes=nbytes, groups=2, lds=to_lds, per=per)
+    for k, v in (("bytes", 65536 + 16), ("groups", 0), ("lds", 2), ("per", 3)):
+        a = dict(bad, **{k: v})
+        assert lib.rnn_probe_l2_rate(p, a["bytes"], a["groups"], a["lds"], a["per"], 4, magic,
+                                     ctypes.c_void_p(sink.data_ptr()), st) == 1
+
