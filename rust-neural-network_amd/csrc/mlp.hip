@@ -41,7 +41,7 @@ struct MlpArgs {
     int relu;  // ReLU between layers (not after the last)
 };
 
-constexpr int kMlpPrefetchKb = 4;
+constexpr int kMlpPrefetchKb = 4;  // next-layer blocks requested ahead (k <= 256)
 
 // Workgroup barrier for LDS traffic only. __syncthreads() also orders global
 // memory, which makes every wave wait for all of its outstanding loads; here
@@ -50,7 +50,7 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-}  // next-layer blocks requested ahead (k <= 256)
+}
 
 // A 16-column tile of a layer as one lane holds it.
 template <int NKB>
