@@ -762,7 +762,8 @@ constexpr int kBf16Waves = 8, kBf16MaxParts = 8;
 // lanes trade dwords: int8 pieces swap halves between lane groups q and q+2
 // (elements 8q' .. of group j land in step j), 4-bit pieces (one whole group
 // per lane group) are transposed 4 x 4 across the lane groups; both through
-// the gfx950 lane-swap instructions. x is read in the matching order.
+// the gfx950 lane-swap instructions, or (weights staged in LDS) by reading
+// those dwords from the staged rows. x is read in the matching order.
 template <int KIND, int TPW, bool ONE, int SC, bool BIAS>
 __global__ __launch_bounds__(kBf16Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void qt_gemv_bf16_kernel(
@@ -786,7 +787,22 @@ void qt_gemv_bf16_kernel(
     constexpr int XP = 4 * EP + 4;     // floats per staged row (16-byte pad: no bank conflicts)
     constexpr int XRPL = 64 / EP;      // rows per whole-row load instruction
     typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-    __shared__ float part[NW][TPW][16][17];
+    // LINES: several chunks per wave also read the weights of two chunks at
+    // a time as whole 128-byte lines (a load instruction: 8 rows x 128
+    // bytes), which the wave stores in its LDS slice of the pool and reads
+    // back in the fragment layout; the 8 waves' partial tiles reuse the pool
+    // after the loop. Measured at 4096 x 11008 against one chunk's 64 bytes
+    // per row (16 rows x 64 bytes per load instruction, half lines): GGUF
+    // Q8_0 m = 16 / 8 19.7 / 18.5 against 22.7 / 21.2 us, GGUF Q4_0 m = 16
+    // 17.1 against 18.4 us; INT4 in groups of whole chunks, whose time is
+    // the decode and split work, 15.9 / 14.6 / 14.5 against 16.0 / 14.7 /
+    // 14.1 us at m = 16 / 8 / 4, so it keeps the half-line loads.
+    constexpr bool LINES = STAGE && !(KIND == KIND_I4 && SC == 1);
+    constexpr int WSLICE = TPW * 16 * 128;  // bytes of a wave's weight slice
+    constexpr int PART_BYTES = NW * TPW * 16 * 17 * 4;
+    constexpr int POOL = LINES && NW * WSLICE > PART_BYTES ? NW * WSLICE : PART_BYTES;
+    __shared__ __attribute__((aligned(16))) uint8_t pool[POOL];
+    float (*const part)[TPW][16][17] = reinterpret_cast<float (*)[TPW][16][17]>(pool);
     __shared__ __attribute__((aligned(16))) float xs[STAGE ? NW * 16 * XP : 4];
     __shared__ uint32_t last;
     // (the wave index through readfirstlane: uniform to the compiler, so the
@@ -847,8 +863,9 @@ void qt_gemv_bf16_kernel(
         const uint32_t grp = G32 ? c * JS : (kg ? c / cpg : 0u);
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
-            ch.w[t] = __builtin_bit_cast(
-                v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, voff[t], c * 64u, 2 /* nt */));
+            if constexpr (!LINES)
+                ch.w[t] = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(wr, voff[t], c * 64u, 2 /* nt */));
             if constexpr (G32) {
                 // (a row's scales start at a multiple of kg, itself a multiple
                 // of 16: the JS-float load is aligned)
@@ -862,10 +879,67 @@ void qt_gemv_bf16_kernel(
             }
         }
     };
+    // (LINES) The weights of chunks c and c + 1: per tile two loads, the
+    // lane's 16 bytes at row 16t + 8h + lane/8, piece lane%8 of the 128 bytes
+    // from byte 64c of the row. In the wave's slice the piece of tile row rr
+    // sits at (16t + rr) * 128 + 16 * (piece ^ wswz(rr)): the 16 rows of a
+    // fragment read then fall on 16 different 16-byte bank groups. (The rows
+    // of a range are 16-byte aligned and lie in the range's descriptor, so a
+    // pair that runs past the row or the range reads the next row or zeros,
+    // which no MFMA of this wave uses.)
+    v4i wl[LINES ? TPW : 1][2];
+    uint8_t *const wsl = pool + (LINES ? wid * WSLICE : 0);
+    auto wswz = [](int rr) { return (rr >> 1) & 7; };
+    auto load_w = [&](uint32_t c) {
+        if constexpr (LINES) {
+#pragma unroll
+            for (int t = 0; t < TPW; ++t)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    wl[t][h] = __builtin_bit_cast(
+                        v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                 wr, (uint32_t)(16 * t + 8 * h + lane / 8) * rowbytes + 16 * (lane % 8),
+                                 c * 64u, 2 /* nt */));
+        }
+    };
+    auto stage_w = [&]() {
+        if constexpr (LINES) {
+#pragma unroll
+            for (int t = 0; t < TPW; ++t)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int rr = 8 * h + lane / 8;
+                    *reinterpret_cast<v4i *>(wsl + (16 * t + rr) * 128 + 16 * ((lane % 8) ^ wswz(rr))) =
+                        wl[t][h];
+                }
+        }
+    };
+    // Lane (q, i)'s 16 bytes of tile t for the pair's chunk h, in the layout
+    // the MFMA steps take: piece q of the chunk, or (G32) the dwords a step
+    // of one 32-element group needs (int8: bytes 8g .. 8g+7 and 32+8g ..
+    // 32+8g+7 with g = 2(q%2) + q/2; 4-bit: dword q of each of the 4 pieces).
+    auto lds_w = [&](int t, int h) -> v4i {
+        const uint8_t *row = wsl + (16 * t + i) * 128;
+        auto piece = [&](int p) { return row + 16 * ((4 * h + p) ^ wswz(i)); };
+        if constexpr (G32 && EP == 16) {
+            typedef int v2i __attribute__((ext_vector_type(2)));
+            const v2i a = *reinterpret_cast<const v2i *>(piece(q & 1) + 8 * (q >> 1));
+            const v2i b = *reinterpret_cast<const v2i *>(piece(2 + (q & 1)) + 8 * (q >> 1));
+            return v4i{a[0], a[1], b[0], b[1]};
+        } else if constexpr (G32) {
+            v4i w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const int *>(piece(j) + 4 * q);
+            return w;
+        } else {
+            return *reinterpret_cast<const v4i *>(piece(q));
+        }
+    };
     f4v tot[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) tot[t] = f4v{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](const Chunk &ch) {
+    // (h: the chunk's half of the pair staged in the wave's slice)
+    auto compute = [&](const Chunk &ch, int h) {
         // (staged: the whole-row runs into the wave's LDS slice, then the
         // lane's fragment, x[i][q EP .. q EP + EP), back; one wave's LDS
         // operations complete in order)
@@ -899,8 +973,11 @@ void qt_gemv_bf16_kernel(
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
             float v[EP];
-            v4i w = ch.w[t];
-            if constexpr (G32) {
+            v4i w;
+            if constexpr (LINES) {
+                w = lds_w(t, h);
+            } else if constexpr (G32) {
+                w = ch.w[t];
                 // lane group q's dwords to the steps of their groups: swap the
                 // upper 32 lanes of one register with the lower 32 of another
                 // (lane groups 2, 3 <-> 0, 1), then (4-bit) odd rows of 16
@@ -913,6 +990,8 @@ void qt_gemv_bf16_kernel(
                     const auto s23 = __builtin_amdgcn_permlane16_swap((uint32_t)w[2], (uint32_t)w[3], false, false);
                     w = v4i{(int)s01[0], (int)s01[1], (int)s23[0], (int)s23[1]};
                 }
+            } else {
+                w = ch.w[t];
             }
             if (KIND != KIND_BF16) decode_piece<KIND>(w, v, nullptr);
             f4v acc = {0.f, 0.f, 0.f, 0.f};
@@ -953,33 +1032,35 @@ void qt_gemv_bf16_kernel(
         Chunk A;
         load(A, c0);
         __builtin_amdgcn_sched_barrier(0);
-        compute(A);
-    } else if constexpr (G32 && KIND == KIND_I8) {
-        // two chunks in flight ahead of the one being computed (int8 codes in
-        // groups of 32 have the most work per chunk: measured, GGUF Q8_0
-        // 4096 x 11008, m = 16 / 8: 22.5 / 20.8 us against 25.2 / 23.4 with
-        // one chunk ahead; the other instances lose 0.3-1.4 us with it)
-        Chunk A, B, C;
+        compute(A, 0);
+    } else if constexpr (LINES) {
+        // x one chunk ahead of the one being computed, the weights one pair
+        // ahead of the pair being computed, each pair's loads issued before
+        // its chunks' x (the memory counter completes in order: the wait for
+        // a chunk's x then also covers its weights). Past the wave's last
+        // chunk the loads repeat the last chunk or pair.
+        Chunk A, B;
+        const uint32_t last_pair = (cpw - 1) & ~1u;
+        load_w(c0);
         load(A, c0);
-        load(B, c0 + std::min(1u, cpw - 1));
-        for (uint32_t c = 0; c < cpw; c += 3) {
-            load(C, c0 + std::min(c + 2, cpw - 1));
-            compute(A);
-            if (c + 1 >= cpw) break;
-            load(A, c0 + std::min(c + 3, cpw - 1));
-            compute(B);
-            if (c + 2 >= cpw) break;
-            load(B, c0 + std::min(c + 4, cpw - 1));
-            compute(C);
+        load(B, c0 + 1);
+        for (uint32_t c = 0; c < cpw; c += 2) {
+            stage_w();
+            load_w(c0 + std::min(c + 2, last_pair));
+            compute(A, 0);
+            load(A, c0 + std::min(c + 2, cpw - 1));
+            if (c + 1 < cpw) compute(B, 1);
+            load(B, c0 + std::min(c + 3, cpw - 1));
         }
+        __syncthreads();  // every wave's slice read before the pool takes the partials
     } else {  // one chunk in flight ahead of the one being computed
         Chunk A, B;
         load(A, c0);
         for (uint32_t c = 0; c < cpw; c += 2) {
             load(B, c0 + std::min(c + 1, cpw - 1));
-            compute(A);
+            compute(A, 0);
             load(A, c0 + std::min(c + 2, cpw - 1));
-            if (c + 1 < cpw) compute(B);
+            if (c + 1 < cpw) compute(B, 0);
         }
     }
     // lane holds D[m = 4q + r][n = i] of each tile

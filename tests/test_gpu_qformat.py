@@ -217,6 +217,9 @@ def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
 @pytest.mark.parametrize("m,k,n", [(5, 4096, 4096), (16, 4096, 5000), (9, 2048, 11008),
                                    (16, 4096, 16000), (12, 1024, 20000), (7, 4096, 30),
                                    (16, 2048, 1),
+                                   # three chunks per wave (4-bit codes): weight pairs that
+                                   # start mid-line and a last pair with one chunk
+                                   (11, 3072, 700),
                                    # long K, few rows: K split 8 ways, one and two chunks per wave
                                    (16, 8192, 300), (16, 16384, 64)])
 def test_linear_forward_bf16_gemv(dev, hip, fmt, gs, m, k, n):
@@ -224,7 +227,8 @@ def test_linear_forward_bf16_gemv(dev, hip, fmt, gs, m, k, n):
     bf16, one scale per group sum -- for groups of 32 one per MFMA step, the
     pieces traded between lane groups --, K split over 1-8 workgroups as the
     plan's estimate picks): 1-12 row tiles per range, one or several chunks
-    per wave (x staged through LDS), row ranges that are not
+    per wave (x staged through LDS; the weights of two chunks staged as
+    whole lines, an odd count of chunks included), row ranges that are not
     multiples of 16, fewer rows than CUs, rows of x past m; with and without
     bias, forced, with the caller's workspace (bit-identical, and the same
     counters reused) and as AUTO picks it, within the GEMM rounding bound; x
@@ -235,6 +239,8 @@ def test_linear_forward_bf16_gemv(dev, hip, fmt, gs, m, k, n):
     x[:, :7] *= 20.0
     x[0, 7:15] = np.float32(3e-30)
     b = rng.standard_normal(n).astype(np.float32)
+    if gs == 4096 and k % gs and gs % k:
+        gs = k          # "rows": one group per row of W
     d, s, g = O.qt_quantize(fmt, w, gs)
     assert bf16_gemv_fits(fmt, m, k, g)
     wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
