@@ -394,7 +394,8 @@ def qt_bf16_path(fmt, m, k, n, g, cus):
     """Whether AUTO takes the bf16 MFMA GEMV (the conditions of
     rnn_qt_linear_forward for INT4 / GGUF Q4 / INT8 / GGUF Q8_0 / BF16 --
     groups of whole 4-piece chunks, whole rows or 32 elements: m >= 5, or
-    4-bit codes at m = 3, 4 with at least two 16-row tiles of W per CU)."""
+    4- and 8-bit codes at m = 3, 4 with at least two 16-row tiles of W per
+    CU)."""
     kinds = {3: 32, 6: 32, 7: 32, 2: 16, 8: 16, 1: 8}   # format -> elements per 16 bytes
     if fmt not in kinds or m < 3:
         return False
@@ -405,7 +406,7 @@ def qt_bf16_path(fmt, m, k, n, g, cus):
         return False
     if m >= 5:
         return True
-    if ep != 32:
+    if ep == 8:
         return False
     r = max(min(-(-n // 16), cus), -(-n // 64))     # ranges of the m <= 8 plan (S = 1)
     return -(-(-(-n // r)) // 16) >= 2

@@ -331,8 +331,8 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
  * parts in registers, codes exact in bf16, each group's sum scaled once, K
  * split over up to 8 workgroups whose partial sums are added in a fixed order
  * in stream-ordered scratch; RNN_ALGO_GEMV_BF16 forces it; AUTO also takes it
- * for 4-bit codes at m = 3, 4 when every CU gets at least two 16-row tiles of
- * W), else
+ * for 4- and 8-bit codes at m = 3, 4 when every CU gets at least two 16-row
+ * tiles of W), else
  * the f32 MFMA GEMV (RNN_ALGO_GEMV_MFMA forces it); else the VALU GEMV
  * (m <= 4, or per 4 rows); otherwise dequantize
  * into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV forces the

@@ -1513,12 +1513,15 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
         (!scaled || n_scales >= ceil_div(out_f * in_f, group)) &&
         bf16_plan(m, in_f, out_f, ep).S > 0 && 64 * in_f * 16 / ep < (int64_t(1) << 31) &&
         16 * in_f * 4 < (int64_t(1) << 31);
-    // AUTO takes it for m >= 5, and for 4-bit codes at m = 3, 4 when every
-    // CU gets at least two row tiles (measured, 4096 x 11008, m = 4: INT4 g128
-    // 14.0 us against 16.3 for the VALU GEMV, GGUF Q4_0 15.8 against 16.7;
-    // at N = 4096 INT4 8.6 against 7.4; GGUF Q8_0 22.4 against 20.1)
+    // AUTO takes it for m >= 5, and for 4- and 8-bit codes at m = 3, 4 when
+    // every CU gets at least two row tiles (measured, 4096 x 11008, m = 4:
+    // INT4 g128 14.0 us against 16.3 for the VALU GEMV, GGUF Q4_0 15.8 against
+    // 16.3, GGUF Q8_0 17.7 against 19.8, INT8 g64 16.7 against 19.8; at
+    // N = 4096, one tile per CU, INT4 9.0 against 7.5, GGUF Q8_0 10.7 against
+    // 9.1)
     const bool bf16_auto =
-        fits_bf16 && (m >= 5 || (m >= 3 && kind == KIND_I4 && bf16_plan(m, in_f, out_f, ep).TPW >= 2));
+        fits_bf16 && (m >= 5 || (m >= 3 && (kind == KIND_I4 || kind == KIND_I8) &&
+                                 bf16_plan(m, in_f, out_f, ep).TPW >= 2));
     if (algo == RNN_ALGO_GEMV_BF16 || (algo == RNN_ALGO_AUTO && bf16_auto)) {
         RNN_REQUIRE(fits_bf16, "%s: the bf16 MFMA GEMV needs INT4/Q4/INT8/Q8/BF16 weights, m <= 16, "
                     "in_f a multiple of %d, a group that is a multiple of %d dividing in_f (or a "

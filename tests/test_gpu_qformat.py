@@ -303,10 +303,11 @@ def test_linear_forward_nonfinite_x(dev, hip, m):
 @pytest.mark.parametrize("fmt", [O.QF_GGUF_Q4, O.QF_GGUF_Q8], ids=["Q4_0", "Q8_0"])
 @pytest.mark.parametrize("m", [3, 4])
 def test_linear_forward_groups_of_32_few_rows(dev, hip, fmt, m):
-    """GGUF blocks of 32 at m = 3, 4 and N = 11008 (two row tiles per CU): AUTO
-    takes the bf16 GEMV for 4-bit codes (one MFMA step per group, the pieces
-    transposed across lane groups) and the VALU GEMV for Q8_0; both, and the
-    bf16 GEMV forced for Q8_0, within the GEMM bound."""
+    """GGUF blocks of 32 at m = 3, 4 and N = 11008 (three row tiles per CU):
+    AUTO takes the bf16 GEMV for 4- and 8-bit codes (one MFMA step per group,
+    the pieces read from the staged weight lines in the step's order) -- the
+    same bits as the bf16 GEMV forced --, and the VALU GEMV forced; all
+    within the GEMM bound."""
     rng = np.random.default_rng(90 + m + fmt)
     n, k = 11008, 4096
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -316,8 +317,11 @@ def test_linear_forward_groups_of_32_few_rows(dev, hip, fmt, m):
     assert g == 32 and bf16_gemv_fits(fmt, m, k, g)
     wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
     dd, sd, xd = to_dev(d, dev), to_dev(s, dev), to_dev(x, dev)
-    gemm_check(host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n)), x, wdeq, None)
-    gemm_check(host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, algo=hip.ALGO_GEMV_BF16)), x, wdeq, None)
+    auto = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n))
+    gemm_check(auto, x, wdeq, None)
+    bf16 = host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, algo=hip.ALGO_GEMV_BF16))
+    assert np.array_equal(auto, bf16)
+    gemm_check(host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, algo=hip.ALGO_GEMV)), x, wdeq, None)
 
 
 def test_linear_forward_groups_of_32_unaligned_scales(dev, hip):
