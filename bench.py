@@ -733,30 +733,45 @@ SGEMM_MNK = (4096, 4096, 4096)
 
 def bench_sgemm(H, dev, steps):
     """rnn_sgemm (the BlasBackend::sgemm plugin point) on a 4096^3 f32
-    product, C = A*B with both operands as stored (no transpose), beside
-    torch.matmul (the ROCm library GEMM, TF32 off) on the same operands."""
+    product, beside torch.matmul (the ROCm library GEMM, TF32 off) on the same
+    operands, for the two calls the reference makes: C = A*B with both
+    operands as stored (Tensor::matmul, src/tensor.rs:403-412) and
+    C = A*B^T with B stored [n, k] (Linear::forward, x * W^T,
+    src/tensor.rs:765-775)."""
     import torch
     m, n, k = SGEMM_MNK
     a = gen_f32((m, k), 21, dev)
     b = gen_f32((k, n), 22, dev)
+    bt = gen_f32((n, k), 23, dev)
     c = torch.empty((m, n), dtype=torch.float32, device=dev)
     n_iter = max(steps // 4, 20)
-    fn = lambda: H.sgemm(H.NO_TRANS, H.NO_TRANS, m, n, k, 1.0, a, k, b, n, 0.0, c, n)  # noqa: E731
-    settle(fn, 0.1)
-    ms = timed(fn, n_iter, 10)
-    tf32 = torch.backends.cuda.matmul.allow_tf32
-    torch.backends.cuda.matmul.allow_tf32 = False
-    try:
-        ms_lib = timed(lambda: torch.matmul(a, b, out=c), n_iter, 10)
-    finally:
-        torch.backends.cuda.matmul.allow_tf32 = tf32
     flops = 2.0 * m * n * k
-    tflops, tflops_lib = flops / (ms * 1e-3) / 1e12, flops / (ms_lib * 1e-3) / 1e12
+
+    def run(fn, fn_lib):
+        settle(fn, 0.1)
+        ms = timed(fn, n_iter, 10)
+        tf32 = torch.backends.cuda.matmul.allow_tf32
+        torch.backends.cuda.matmul.allow_tf32 = False
+        try:
+            ms_lib = timed(fn_lib, n_iter, 10)
+        finally:
+            torch.backends.cuda.matmul.allow_tf32 = tf32
+        return flops / (ms * 1e-3) / 1e12, flops / (ms_lib * 1e-3) / 1e12, ms
+    tflops, tflops_lib, ms = run(
+        lambda: H.sgemm(H.NO_TRANS, H.NO_TRANS, m, n, k, 1.0, a, k, b, n, 0.0, c, n),
+        lambda: torch.matmul(a, b, out=c))
+    nt, nt_lib, ms_nt = run(
+        lambda: H.sgemm(H.NO_TRANS, H.TRANS, m, n, k, 1.0, a, k, bt, k, 0.0, c, n),
+        lambda: torch.matmul(a, bt.t(), out=c))
     return {"m": m, "n": n, "k": k, "trans": "nn", "us": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
             "frac_fp32_mfma_peak": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "torch_matmul_TFLOP/s": round(tflops_lib, 1), "traffic": traffic_for("f32_sgemm"),
             "kernel": "sgemm_mfma2_kernel<false,false> (v_mfma_f32_16x16x4f32, 128x128 tiles, "
-                      "both operands as 4-k quads in LDS)"}
+                      "both operands as 4-k quads in LDS)",
+            "nt": {"us": round(ms_nt * 1e3, 1), "TFLOP/s": round(nt, 1),
+                   "frac_fp32_mfma_peak": round(nt / PEAK_FP32_MFMA_TFLOPS, 4),
+                   "torch_matmul_TFLOP/s": round(nt_lib, 1),
+                   "kernel": "sgemm_mfma2_kernel<false,true> (B stored [n, k]: both operands K-contiguous)"}}
 
 
 # ---------------------------------------------------------------- copy ceiling
@@ -928,6 +943,9 @@ def compact(result):
     if "f32_sgemm" in comp:
         other["f32_sgemm"] = _pick(comp["f32_sgemm"], "TFLOP/s", "frac_fp32_mfma_peak",
                                    "torch_matmul_TFLOP/s")
+        if "nt" in comp["f32_sgemm"]:
+            other["f32_sgemm"]["nt_TFLOP/s"] = comp["f32_sgemm"]["nt"]["TFLOP/s"]
+            other["f32_sgemm"]["nt_frac"] = comp["f32_sgemm"]["nt"]["frac_fp32_mfma_peak"]
     if "copy_ceiling" in comp:
         other["copy_ceiling_GBs"] = comp["copy_ceiling"]["GB/s"]
     if "mfma_clock_probe" in comp:
