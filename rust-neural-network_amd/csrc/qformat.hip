@@ -773,7 +773,7 @@ constexpr int kBf16Waves = 8, kBf16MaxParts = 8;
 // per lane group) are transposed 4 x 4 across the lane groups; both through
 // the gfx950 lane-swap instructions, or (weights staged in LDS) by reading
 // those dwords from the staged rows. x is read in the matching order.
-template <int KIND, int TPW, bool ONE, int SC, bool BIAS>
+template <int KIND, int TPW, bool ONE, int SC, bool BIAS, bool LN = false>
 __global__ __launch_bounds__(kBf16Waves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void qt_gemv_bf16_kernel(
     const float *__restrict__ x, int mrows, int64_t K, const uint8_t *__restrict__ data,
@@ -804,9 +804,11 @@ void qt_gemv_bf16_kernel(
     // per row (16 rows x 64 bytes per load instruction, half lines): GGUF
     // Q8_0 m = 16 / 8 19.7 / 18.5 against 22.7 / 21.2 us, GGUF Q4_0 m = 16
     // 17.1 against 18.4 us; INT4 in groups of whole chunks, whose time is
-    // the decode and split work, 15.9 / 14.6 / 14.5 against 16.0 / 14.7 /
-    // 14.1 us at m = 16 / 8 / 4, so it keeps the half-line loads.
-    constexpr bool LINES = STAGE && !(KIND == KIND_I4 && SC == 1);
+    // the decode and split work, measured 15.4 / 15.1 / 14.9 / 14.5 against
+    // 15.8 / 15.3 / 14.7 / 13.8 us at m = 16 / 12 / 9 / 4: LN, which the host
+    // sets from 12 rows of x on (more x bytes per chunk), selects whole lines
+    // for it.
+    constexpr bool LINES = STAGE && (LN || !(KIND == KIND_I4 && SC == 1));
     constexpr int WSLICE = TPW * 16 * 128;  // bytes of a wave's weight slice
     constexpr int PART_BYTES = NW * TPW * 16 * 17 * 4;
     constexpr int POOL = LINES && NW * WSLICE > PART_BYTES ? NW * WSLICE : PART_BYTES;
@@ -1401,12 +1403,20 @@ static void launch_bf16_t(const float *xs, int mrows, int64_t K, const uint8_t *
     const uint32_t rpg = !SCALED ? 1u : (kg ? 1u : (uint32_t)(g / K));
     const uint32_t cpg = kg && SC == 1 ? (uint32_t)(g / (4 * EP)) : 1u;  // chunks per group
     const unsigned grid = (unsigned)(pl.R * pl.S);
-    if (bias)
-        qt_gemv_bf16_kernel<KIND, TPW, ONE, SC, true><<<grid, kBf16Waves * 64, 0, st>>>(
-            xs, mrows, K, data, scales, ns, cpg, kg, rpg, N, pl.S, pl.cpw, wpart, cnt, bias, y);
-    else
-        qt_gemv_bf16_kernel<KIND, TPW, ONE, SC, false><<<grid, kBf16Waves * 64, 0, st>>>(
-            xs, mrows, K, data, scales, ns, cpg, kg, rpg, N, pl.S, pl.cpw, wpart, cnt, bias, y);
+    // whole-line weights for INT4 in groups of whole chunks from 12 rows of x on
+    constexpr bool LN_OK = KIND == KIND_I4 && SC == 1 && !ONE;
+    const bool ln = LN_OK && mrows >= 12;
+#define RNN_BF16_GO(B, L)                                                                    \
+    qt_gemv_bf16_kernel<KIND, TPW, ONE, SC, B, L><<<grid, kBf16Waves * 64, 0, st>>>(        \
+        xs, mrows, K, data, scales, ns, cpg, kg, rpg, N, pl.S, pl.cpw, wpart, cnt, bias, y)
+    if (bias) {
+        if (ln) RNN_BF16_GO(true, LN_OK);
+        else RNN_BF16_GO(true, false);
+    } else {
+        if (ln) RNN_BF16_GO(false, LN_OK);
+        else RNN_BF16_GO(false, false);
+    }
+#undef RNN_BF16_GO
 }
 
 template <int KIND, int SC>
