@@ -706,7 +706,8 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
 // x = h + m + l splits exactly into three bf16 parts (h = x with the low 16
 // bits cleared, m likewise of x - h, l = x - h - m, which has at most 8
 // significant bits), so each product is exact and the MFMA sums in f32; the
-// sum of a group's products is scaled once by the group's scale. This is the
+// sum of a group's products enters the tile's total in one fused multiply-add
+// by the group's scale (INT4's 1/16 is applied once to the total). This is the
 // reference's sum of x * (q*s) reassociated, within the same f32 GEMM
 // rounding bound, at 16x the f32 MFMA's rate per MFMA (three of them per
 // product).
@@ -1041,8 +1042,8 @@ void qt_gemv_bf16_kernel(
                     for (int p = 0; p < kSplitParts; ++p)
                         aj = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a[j][p]),
                                                                     __builtin_bit_cast(bf8, b), aj, 0, 0, 0);
-                    const float s = KIND == KIND_I4 ? ch.sc[t][j] * 0.0625f : ch.sc[t][j];
-                    tot[t] = tot[t] + aj * s;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) tot[t][r] = __builtin_fmaf(aj[r], ch.sc[t][j], tot[t][r]);
                 } else {
 #pragma unroll
                     for (int p = 0; p < kSplitParts; ++p)
@@ -1052,8 +1053,8 @@ void qt_gemv_bf16_kernel(
             }
             if constexpr (G32) {
             } else if (SCALED) {
-                const float s = KIND == KIND_I4 ? ch.sc[t][0] * 0.0625f : ch.sc[t][0];
-                tot[t] = tot[t] + acc * s;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tot[t][r] = __builtin_fmaf(acc[r], ch.sc[t][0], tot[t][r]);
             } else {
                 tot[t] = tot[t] + acc;
             }
@@ -1094,11 +1095,13 @@ void qt_gemv_bf16_kernel(
             if (c + 1 < cpw) compute(B, 0);
         }
     }
-    // lane holds D[m = 4q + r][n = i] of each tile
+    // lane holds D[m = 4q + r][n = i] of each tile (INT4 codes entered as
+    // 16q: the 1/16, exact, once here)
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part[wid][t][4 * q + r][i] = tot[t][r];
+        for (int r = 0; r < 4; ++r)
+            part[wid][t][4 * q + r][i] = KIND == KIND_I4 ? tot[t][r] * 0.0625f : tot[t][r];
     __syncthreads();
     // outputs of this workgroup: (tile t, row m, column n), m < mrows
     if (S == 1) {
