@@ -275,9 +275,10 @@ struct Fmt {
 constexpr int kSlice = 2048;  // elements of K per slice (64 lanes x 32)
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// Decodes one 16-byte piece into EP floats. INT4 nibbles are moved into the
-// high half of a byte, where the sign-extending byte conversion reads them
-// as exactly 16*q; the caller multiplies the piece's sum by 1/16. NF4 and
+// Decodes one 16-byte piece into EP floats. INT4 nibbles go through
+// v_cvt_off_f32_i4, which reads the low 4 bits of its (byte-selected) source
+// as a signed nibble q and returns exactly q/16; the caller multiplies the
+// piece's sum by 16. NF4 and
 // E2M1 nibbles index a 16-float table in LDS (the 16 entries sit in 16
 // different banks, so a wave's lookups never conflict).
 template <int KIND>
@@ -294,11 +295,15 @@ __device__ __attribute__((always_inline)) inline void decode_piece(const v4i raw
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const uint32_t w = (uint32_t)raw[d];
-            const uint32_t lo = (w << 4) & 0xF0F0F0F0u, hi = w & 0xF0F0F0F0u;
+            uint32_t h = w >> 4;
+            // keeps h a register of its own, so each conversion below reads
+            // a byte of w or of h through a byte select instead of a
+            // separate bit-field extract per high nibble
+            asm("" : "+v"(h));
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                v[8 * d + 2 * b] = (float)(int8_t)(lo >> (8 * b));
-                v[8 * d + 2 * b + 1] = (float)(int8_t)(hi >> (8 * b));
+                v[8 * d + 2 * b] = __builtin_amdgcn_cvt_off_f32_i4((int)((w >> (8 * b)) & 0xFFu));
+                v[8 * d + 2 * b + 1] = __builtin_amdgcn_cvt_off_f32_i4((int)((h >> (8 * b)) & 0xFFu));
             }
         }
     } else if (KIND == KIND_I8) {
@@ -427,7 +432,7 @@ __device__ __attribute__((always_inline)) inline void compute_slice(const SliceR
                 float p = xr[m][0] * v[0];
 #pragma unroll
                 for (int e = 1; e < F::EP; ++e) p = __builtin_fmaf(xr[m][e], v[e], p);
-                if (KIND == KIND_I4) p = p * 0.0625f;  // the codes were read as 16*q
+                if (KIND == KIND_I4) p = p * 16.0f;  // the codes were read as q/16
                 p = act ? p : 0.0f;
                 acc[r][m] = SCALED ? __builtin_fmaf(s.sc[r][j], p, acc[r][m]) : acc[r][m] + p;
             }
@@ -658,7 +663,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
         for (int nt = 0; nt < NT; ++nt) {
             float v[EP];
             decode_piece<KIND>(c.raw[nt], v, lut);
-            const float s = SCALED ? (KIND == KIND_I4 ? c.sc[nt] * 0.0625f : c.sc[nt]) : 1.0f;
+            const float s = SCALED ? (KIND == KIND_I4 ? c.sc[nt] * 16.0f : c.sc[nt]) : 1.0f;
 #pragma unroll
             for (int t = 0; t < EP; ++t) {
                 const float w = SCALED ? v[t] * s : v[t];
@@ -707,7 +712,7 @@ __global__ __launch_bounds__(kMfmaWaves * 64) void qt_gemv_mfma_kernel(
 // bits cleared, m likewise of x - h, l = x - h - m, which has at most 8
 // significant bits), so each product is exact and the MFMA sums in f32; the
 // sum of a group's products enters the tile's total in one fused multiply-add
-// by the group's scale (INT4's 1/16 is applied once to the total). This is the
+// by the group's scale (INT4's factor 16 is applied once to the total). This is the
 // reference's sum of x * (q*s) reassociated, within the same f32 GEMM
 // rounding bound, at 16x the f32 MFMA's rate per MFMA (three of them per
 // product).
@@ -1096,12 +1101,12 @@ void qt_gemv_bf16_kernel(
         }
     }
     // lane holds D[m = 4q + r][n = i] of each tile (INT4 codes entered as
-    // 16q: the 1/16, exact, once here)
+    // q/16: the factor 16, exact, once here)
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            part[wid][t][4 * q + r][i] = KIND == KIND_I4 ? tot[t][r] * 0.0625f : tot[t][r];
+            part[wid][t][4 * q + r][i] = KIND == KIND_I4 ? tot[t][r] * 16.0f : tot[t][r];
     __syncthreads();
     // outputs of this workgroup: (tile t, row m, column n), m < mrows
     if (S == 1) {
