@@ -44,10 +44,10 @@ enum rnn_status {
 #define RNN_FLAG_RELU 0x1u          /* y = max(y, 0) after bias (src/tensor.rs:2025-2032) */
 #define RNN_ALGO_AUTO 0x00u         /* GEMV for m <= 16, else LDS-DMA tiles (k % 128 == 0, n % 4 == 0) or register-staged tiles */
 #define RNN_ALGO_TILED 0x10u        /* force the register-staged 128x128 MFMA GEMM */
-#define RNN_ALGO_GEMV 0x20u         /* force the skinny GEMV (m <= 16)        */
+#define RNN_ALGO_GEMV 0x20u         /* force the skinny GEMV (m <= 16; rnn_qt_linear_forward: per 16-row slice for any m) */
 #define RNN_ALGO_TILED_DMA 0x30u    /* force the LDS-DMA pipelined big-tile GEMM (k % 128 == 0, n % 4 == 0) */
-#define RNN_ALGO_GEMV_MFMA 0x40u    /* rnn_qt_linear_forward: force the f32-MFMA GEMV (m <= 16) */
-#define RNN_ALGO_GEMV_BF16 0x50u    /* rnn_qt_linear_forward: force the bf16-MFMA GEMV (m <= 16) */
+#define RNN_ALGO_GEMV_MFMA 0x40u    /* rnn_qt_linear_forward: force the f32-MFMA GEMV (per 16-row slice) */
+#define RNN_ALGO_GEMV_BF16 0x50u    /* rnn_qt_linear_forward: force the bf16-MFMA GEMV (per 16-row slice) */
 #define RNN_ALGO_MASK 0xF0u
 #define RNN_FLAG_TERNARY_MFMA_LAYOUT 0x100u /* rnn_ternary_gemm: codes are in the layout of rnn_ternary_prepack */
 
@@ -334,9 +334,14 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
  * for 4- and 8-bit codes at m = 3, 4 when every CU gets at least two 16-row
  * tiles of W), else
  * the f32 MFMA GEMV (RNN_ALGO_GEMV_MFMA forces it); else the VALU GEMV
- * (m <= 4, or per 4 rows); otherwise dequantize
- * into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV forces the
- * former (error if it does not fit), RNN_ALGO_TILED the latter. f32 sums in
+ * (m <= 4, or per 4 rows). For m > 16 the same GEMVs run on 16-row slices
+ * of x and y in turn (each slice reads W again) while that is the faster
+ * route: up to m = 512 when the slices take the bf16 MFMA GEMV with 4-bit
+ * codes, 256 with 8-bit codes, 192 for the other MFMA GEMVs, 32 for the VALU
+ * GEMV; otherwise
+ * dequantize into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV,
+ * _GEMV_MFMA and _GEMV_BF16 force their GEMV (per 16-row slice for any m;
+ * error if it does not fit), RNN_ALGO_TILED the dequantize route. f32 sums in
  * the kernel's own order: within the rnn_sgemm rounding bound of the
  * reference, not bit for bit. */
 int rnn_qt_linear_forward(int format, const float *x, int64_t m, int64_t in_f,

@@ -249,6 +249,59 @@ __global__ void qt_dequant_kernel(int f, const uint8_t *__restrict__ data,
     }
 }
 
+// Eight elements per thread, for n and the group multiples of 8 with the
+// codes and out aligned to their vector width: one group index and one scale
+// per eight elements (a shift for a power-of-two group), the codes in one 4-,
+// 8- or 16-byte load, the values in two 16-byte stores, each value the
+// one-element kernel's. For groups of whole bytes GGUF Q4_0's block offset
+// b*(g/2) + j/2 is i/2, as for INT4.
+template <int F, bool POW2>
+__global__ __launch_bounds__(256) void qt_dequant8_kernel(const uint8_t *__restrict__ data,
+                                                          const float *__restrict__ scales,
+                                                          int64_t ns, int64_t g, int gshift,
+                                                          int64_t n8, float *__restrict__ out) {
+    constexpr bool TABLE = F == RNN_QF_NF4 || F == RNN_QF_NVFP4;
+    __shared__ float lut[16];
+    if (TABLE) {
+        if (threadIdx.x < 16) lut[threadIdx.x] = F == RNN_QF_NF4 ? kNF4[threadIdx.x] : kE2M1[threadIdx.x];
+        __syncthreads();
+    }
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < n8;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = 8 * t;
+        float v[8];
+        if constexpr (F == RNN_QF_FP16 || F == RNN_QF_BF16) {
+            const uint4 h = reinterpret_cast<const uint4 *>(data)[t];
+            const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t u = (hw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+                v[e] = F == RNN_QF_FP16 ? f16_to_f32_rs(u) : __uint_as_float(u << 16);
+            }
+        } else {
+            int64_t gi = POW2 ? (i >> gshift) : i / g;
+            if (F != RNN_QF_GGUF_Q4 && F != RNN_QF_GGUF_Q4K) gi = gi < ns - 1 ? gi : ns - 1;
+            const float sc = scales[gi];
+            if constexpr (F == RNN_QF_INT8 || F == RNN_QF_GGUF_Q8) {
+                const uint2 c = reinterpret_cast<const uint2 *>(data)[t];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    v[e] = (float)(int8_t)((e < 4 ? c.x : c.y) >> (8 * (e & 3))) * sc;
+            } else {
+                const uint32_t w = reinterpret_cast<const uint32_t *>(data)[t];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int nib = (int)((w >> (4 * e)) & 0xFu);
+                    v[e] = TABLE ? lut[nib] * sc : (float)((nib ^ 8) - 8) * sc;
+                }
+            }
+        }
+        float4 *o = reinterpret_cast<float4 *>(out + i);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
 // ------------------------------------------------------------ fused GEMV
 
 // QuantizedLinear::forward (src/quantize.rs:744-754) for few rows of x:
@@ -1275,8 +1328,39 @@ extern "C" int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_b
     RNN_TRY(check_tensor("rnn_qt_dequantize", format, data, data_bytes, scales, n_scales, group, n));
     if (n == 0) return RNN_OK;
     RNN_REQUIRE(out != nullptr, "rnn_qt_dequantize: null out");
-    qt_dequant_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(format, data, scales,
-                                                                       n_scales, group, n, out);
+    hipStream_t st = as_stream(stream);
+    const bool grouped = format != RNN_QF_FP16 && format != RNN_QF_BF16;
+    // bytes of codes per eight elements
+    const int vec = format == RNN_QF_INT8 || format == RNN_QF_GGUF_Q8 ? 8 : grouped ? 4 : 16;
+    if (n % 8 == 0 && (!grouped || group % 8 == 0) && (uintptr_t)data % vec == 0 &&
+        (uintptr_t)out % 16 == 0) {
+        const bool pow2 = grouped && (group & (group - 1)) == 0;
+        const int gshift = pow2 ? __builtin_ctzll((unsigned long long)group) : 0;
+        const int blocks = grid_for(n / 8, 256);
+#define RNN_DQ8(F)                                                                             \
+    do {                                                                                       \
+        if (pow2)                                                                              \
+            qt_dequant8_kernel<F, true><<<blocks, 256, 0, st>>>(data, scales, n_scales, group,  \
+                                                                gshift, n / 8, out);           \
+        else                                                                                   \
+            qt_dequant8_kernel<F, false><<<blocks, 256, 0, st>>>(data, scales, n_scales, group, \
+                                                                 gshift, n / 8, out);          \
+    } while (0)
+        switch (format) {
+        case RNN_QF_FP16: RNN_DQ8(RNN_QF_FP16); break;
+        case RNN_QF_BF16: RNN_DQ8(RNN_QF_BF16); break;
+        case RNN_QF_INT8: RNN_DQ8(RNN_QF_INT8); break;
+        case RNN_QF_GGUF_Q8: RNN_DQ8(RNN_QF_GGUF_Q8); break;
+        case RNN_QF_INT4: RNN_DQ8(RNN_QF_INT4); break;
+        case RNN_QF_NF4: RNN_DQ8(RNN_QF_NF4); break;
+        case RNN_QF_NVFP4: RNN_DQ8(RNN_QF_NVFP4); break;
+        default: RNN_DQ8(RNN_QF_GGUF_Q4); break;  // Q4_0 and Q4_K (stored as Q4_0)
+        }
+#undef RNN_DQ8
+    } else {
+        qt_dequant_kernel<<<grid_for(n, 256), 256, 0, st>>>(format, data, scales, n_scales, group,
+                                                            n, out);
+    }
     return check_launch("rnn_qt_dequantize");
 }
 
@@ -1549,8 +1633,8 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
     // the bf16 MFMA GEMV: integer codes and bf16 weights, whole chunks of
     // 4 pieces per group
     const int ep = kind >= 0 ? piece_elems(kind) : 32;
-    const bool fits_bf16 =
-        fits && m <= 16 && (kind == KIND_I4 || kind == KIND_I8 || kind == KIND_BF16) &&
+    auto bf16_fits = [&](int64_t rows) {
+        return fits && rows <= 16 && (kind == KIND_I4 || kind == KIND_I8 || kind == KIND_BF16) &&
         in_f % (kBf16Waves * 4 * ep) == 0 &&
         (!scaled || (group % (4 * ep) == 0 && in_f % group == 0) || group % in_f == 0 ||
          // (groups of 32: a chunk's scales come in one vector load)
@@ -1558,8 +1642,31 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
         // (a scale for every group: the kernel reads a row's scales from the
         // row's first without the per-index clamp of a shortened array)
         (!scaled || n_scales >= ceil_div(out_f * in_f, group)) &&
-        bf16_plan(m, in_f, out_f, ep).S > 0 && 64 * in_f * 16 / ep < (int64_t(1) << 31) &&
+        bf16_plan(rows, in_f, out_f, ep).S > 0 && 64 * in_f * 16 / ep < (int64_t(1) << 31) &&
         16 * in_f * 4 < (int64_t(1) << 31);
+    };
+    const bool fits_bf16 = bf16_fits(m);
+    // m > 16: the GEMVs run on 16-row slices of x and y, one after the other,
+    // each slice reading the weights again. A forced GEMV does so for every
+    // m; AUTO does so while the slices beat dequantize + f32 GEMM (measured,
+    // 4096 x 11008, slices against the latter: bf16 GEMV INT4 g128 m = 32
+    // 29.7 us against 375, m = 512 467 against 593; GGUF Q8_0 m = 256 294
+    // against 368, m = 512 600 against 594; f32 MFMA GEMV NF4 g64 m = 192
+    // 315 against 381, m = 256 416 against 386)
+    if (m > 16 && algo != RNN_ALGO_TILED) {
+        const int64_t lim = bf16_fits(16) && kind == KIND_I4   ? 512
+                            : bf16_fits(16) && kind == KIND_I8 ? 256
+                            : bf16_fits(16) || (fits && in_f % (kMfmaWaves * 4 * ep) == 0) ? 192
+                                                                                       : 32;
+        if (algo != RNN_ALGO_AUTO || (fits && m <= lim)) {
+            for (int64_t m0 = 0; m0 < m; m0 += 16)
+                RNN_TRY(rnn_qt_linear_forward_ws(format, x + m0 * in_f, std::min<int64_t>(16, m - m0), in_f,
+                                                 data, data_bytes, scales, n_scales, group, out_f,
+                                                 bias, y + m0 * out_f, workspace, workspace_bytes,
+                                                 flags, stream));
+            return RNN_OK;
+        }
+    }
     // AUTO takes it for m >= 5, and for 4- and 8-bit codes at m = 3, 4 when
     // every CU gets at least two row tiles (measured, 4096 x 11008, m = 4:
     // INT4 g128 14.0 us against 16.3 for the VALU GEMV, GGUF Q4_0 15.8 against

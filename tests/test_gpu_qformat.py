@@ -97,14 +97,17 @@ def test_half_conversions_every_pattern(dev, hip):
 
 def test_dequantize_short_scales_and_odd_groups(dev, hip):
     """scales[min(i/group, len-1)] with a caller-shortened scales array, and
-    the odd-group INT4 layout read through data[i/2] (src/quantize.rs:377-396)."""
-    x = weights(1001, 5, 1.0)
-    for fmt in (O.QF_INT8, O.QF_INT4, O.QF_NF4, O.QF_NVFP4):
-        d, s, g = O.qt_quantize(fmt, x, 33)
-        for ns in (s.size, 5, 1):
-            out = host(hip.qt_dequantize(fmt, to_dev(d, dev), to_dev(s[:ns], dev), g, x.size))
-            exp = O.qt_dequantize(fmt, d, s[:ns], g, x.size)
-            assert np.array_equal(out.view(np.uint32), exp.view(np.uint32))
+    the odd-group INT4 layout read through data[i/2] (src/quantize.rs:377-396);
+    groups of 33 over 1001 elements take the one-element kernel, groups of 32
+    and 40 over 1024 the eight-element one (power-of-two shift and division)."""
+    for n, gs in ((1001, 33), (1024, 32), (1040, 40)):
+        x = weights(n, 5 + gs, 1.0)
+        for fmt in (O.QF_INT8, O.QF_INT4, O.QF_NF4, O.QF_NVFP4):
+            d, s, g = O.qt_quantize(fmt, x, gs)
+            for ns in (s.size, 5, 1):
+                out = host(hip.qt_dequantize(fmt, to_dev(d, dev), to_dev(s[:ns], dev), g, x.size))
+                exp = O.qt_dequantize(fmt, d, s[:ns], g, x.size)
+                assert np.array_equal(out.view(np.uint32), exp.view(np.uint32))
 
 
 @pytest.mark.parametrize("fmt,gs", [(O.QF_INT4, 128), (O.QF_INT8, 64), (O.QF_INT4, 32)],
@@ -170,19 +173,21 @@ def gemm_check(got, x, wdeq, bias):
 def bf16_gemv_fits(fmt, m, k, g):
     """The bf16 MFMA GEMV's conditions: integer codes or bf16 weights, whole
     chunks of 4 pieces for each of 8 waves, groups of whole chunks, or groups
-    of 32 (one per MFMA step)."""
+    of 32 (one per MFMA step). Any m: above 16 rows it runs per 16-row
+    slice."""
     if fmt not in (O.QF_INT4, O.QF_GGUF_Q4, O.QF_GGUF_Q4K, O.QF_INT8, O.QF_GGUF_Q8, O.QF_BF16):
         return False
     ep = 32 if O.QF_BITS[fmt] == 4 else (16 if O.QF_BITS[fmt] == 8 else 8)
     grouped = fmt != O.QF_BF16
-    return (m <= 16 and k % (32 * ep) == 0 and
+    return (k % (32 * ep) == 0 and
             (not grouped or (g % (4 * ep) == 0 and k % g == 0) or g % k == 0 or g == 32))
 
 
 @pytest.mark.parametrize("fmt", GEMV_FMTS, ids=[O.QF_NAMES[f] for f in GEMV_FMTS])
 @pytest.mark.parametrize("m,k,n,gs", [(1, 4096, 1000, 128), (3, 2048, 257, 32), (4, 64, 9, 64),
                                       (8, 4096, 512, 32), (16, 2080, 130, 32), (2, 6144, 40, 0),
-                                      (5, 96, 1, 32), (16, 1024, 33, 32), (11, 3072, 70, 1024)])
+                                      (5, 96, 1, 32), (16, 1024, 33, 32), (11, 3072, 70, 1024),
+                                      (17, 1024, 33, 32), (40, 2048, 130, 128)])
 def test_linear_forward_gemv_and_gemm(dev, hip, fmt, m, k, n, gs):
     rng = np.random.default_rng(m * 1000 + k + n)
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -346,10 +351,45 @@ def test_linear_forward_groups_of_32_unaligned_scales(dev, hip):
         hip.qt_linear_forward(O.QF_GGUF_Q8, xd, dd, sd, g, n, algo=hip.ALGO_GEMV_BF16)
 
 
+@pytest.mark.parametrize("fmt,gs", [(O.QF_INT4, 128), (O.QF_GGUF_Q8, 32), (O.QF_NF4, 64),
+                                    (O.QF_FP16, 0)], ids=["INT4-g128", "GGUF-Q8_0", "NF4-g64", "FP16"])
+def test_linear_forward_row_slices(dev, hip, fmt, gs):
+    """Above 16 rows the GEMVs run on 16-row slices of x and y: AUTO at m = 40
+    is bit-identical to AUTO on rows 0-15, 16-31 and 32-39 called one by one
+    (the slice offsets), and every route -- AUTO within and beyond its slice
+    limit (m = 600: dequantize + f32 GEMM for every format) and each
+    forced GEMV -- is within the f32 GEMM bound of the dequantized weight."""
+    import torch
+    rng = np.random.default_rng(40 + fmt)
+    n, k = 200, 2048
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    d, s, g = O.qt_quantize(fmt, w, gs)
+    wdeq = O.qt_dequantize(fmt, d, s, g, n * k).reshape(n, k)
+    dd, sd = to_dev(d, dev), to_dev(s if s.size else np.zeros(1, np.float32), dev)
+    x = rng.standard_normal((600, k)).astype(np.float32)
+    xd = to_dev(x, dev)
+    b = rng.standard_normal(n).astype(np.float32)
+    bd = to_dev(b, dev)
+    y40 = host(hip.qt_linear_forward(fmt, xd[:40], dd, sd, g, n, bd))
+    parts = [host(hip.qt_linear_forward(fmt, xd[a:e], dd, sd, g, n, bd))
+             for a, e in ((0, 16), (16, 32), (32, 40))]
+    np.testing.assert_array_equal(y40, np.concatenate(parts))
+    gemm_check(y40, x[:40], wdeq, b)
+    gemm_check(host(hip.qt_linear_forward(fmt, xd, dd, sd, g, n, bd)), x, wdeq, b)
+    algos = [hip.ALGO_GEMV, hip.ALGO_GEMV_MFMA, hip.ALGO_TILED]
+    if bf16_gemv_fits(fmt, 40, k, g):
+        algos.append(hip.ALGO_GEMV_BF16)
+    for algo in algos:
+        y = torch.full((40, n), float("nan"), device=dev)
+        hip.qt_linear_forward(fmt, xd[:40], dd, sd, g, n, bd, algo=algo, y=y)
+        gemm_check(host(y), x[:40], wdeq, b)
+
+
 def test_linear_forward_bf16_gemv_rejects(dev, hip):
-    """Forced bf16 GEMV outside its conditions: NF4 codes, GGUF Q4_0 with
-    in_f = 512 (4-bit chunks need in_f % 1024 == 0), m = 17; and a workspace
-    one 16-byte step too small -- an RnnError, no launch."""
+    """Forced bf16 GEMV outside its conditions: NF4 codes, GGUF Q4_0 and
+    INT4 with in_f = 512 (4-bit chunks need in_f % 1024 == 0; at m = 17 the
+    first 16-row slice refuses); and a workspace one 16-byte step too small
+    -- an RnnError, no launch."""
     rng = np.random.default_rng(3)
     n, k = 64, 512
     w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
