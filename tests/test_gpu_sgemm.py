@@ -63,7 +63,8 @@ def test_sgemm_reference_cases(dev, hip, case):
     (130, 260, 300, 0.5, 2.0, 0),        # ragged edges in m and n, K tail (MFMA path)
     (32, 256, 784, 1.0, 0.0, 0),         # config-1 MLP layer shape
     (517, 301, 95, -1.25, 1.0, 3),       # odd k and padded strides -> one-thread-per-output path
-    (256, 384, 1024, 1.0, -0.5, 4),      # padded but 16-byte-aligned strides (MFMA path)
+    (256, 384, 1024, 1.0, -0.5, 4),      # padded strides (MFMA path; 6 tiles: K split in 4)
+    (64, 1000, 4128, 1.5, 0.5, 0),       # 8 tiles: K split in 15 ranges, the last one short
 ])
 def test_sgemm_shapes(dev, hip, ta, tb, m, n, k, alpha, beta, pad):
     rng = np.random.default_rng(m * 7 + n * 3 + k + 11 * ta + 13 * tb)
