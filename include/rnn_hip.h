@@ -339,8 +339,8 @@ int rnn_qt_dequantize(int format, const uint8_t *data, int64_t data_bytes,
  * (m <= 4, or per 4 rows). For m > 16 the same GEMVs run on 16-row slices
  * of x and y in turn (each slice reads W again) while that is the faster
  * route: up to m = 512 when the slices take the bf16 MFMA GEMV with 4-bit
- * codes, 256 with 8-bit codes, 192 for the other MFMA GEMVs, 32 for the VALU
- * GEMV; otherwise
+ * codes, 192 with 8-bit codes or bf16 weights, 96 for the f32 MFMA GEMV, 32
+ * for the VALU GEMV; otherwise
  * dequantize into stream-ordered scratch and run rnn_sgemm. RNN_ALGO_GEMV,
  * _GEMV_MFMA and _GEMV_BF16 force their GEMV (per 16-row slice for any m;
  * error if it does not fit), RNN_ALGO_TILED the dequantize route. f32 sums in

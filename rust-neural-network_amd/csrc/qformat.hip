@@ -1650,14 +1650,14 @@ extern "C" int rnn_qt_linear_forward_ws(int format, const float *x, int64_t m, i
     // each slice reading the weights again. A forced GEMV does so for every
     // m; AUTO does so while the slices beat dequantize + f32 GEMM (measured,
     // 4096 x 11008, slices against the latter: bf16 GEMV INT4 g128 m = 32
-    // 29.7 us against 375, m = 512 467 against 593; GGUF Q8_0 m = 256 294
-    // against 368, m = 512 600 against 594; f32 MFMA GEMV NF4 g64 m = 192
-    // 315 against 381, m = 256 416 against 386)
+    // 29.9 us against 182, m = 512 467 against 554; GGUF Q8_0 m = 192 232
+    // against 327, m = 256 316 against 306; BF16 m = 192 249 against 341,
+    // m = 256 305 against 291; f32 MFMA GEMV NF4 g64 m = 96 157 against 178,
+    // m = 128 208 against 194)
     if (m > 16 && algo != RNN_ALGO_TILED) {
-        const int64_t lim = bf16_fits(16) && kind == KIND_I4   ? 512
-                            : bf16_fits(16) && kind == KIND_I8 ? 256
-                            : bf16_fits(16) || (fits && in_f % (kMfmaWaves * 4 * ep) == 0) ? 192
-                                                                                       : 32;
+        const int64_t lim = bf16_fits(16) ? (kind == KIND_I4 ? 512 : 192)
+                            : fits && in_f % (kMfmaWaves * 4 * ep) == 0 ? 96
+                                                                        : 32;
         if (algo != RNN_ALGO_AUTO || (fits && m <= lim)) {
             for (int64_t m0 = 0; m0 < m; m0 += 16)
                 RNN_TRY(rnn_qt_linear_forward_ws(format, x + m0 * in_f, std::min<int64_t>(16, m - m0), in_f,
