@@ -93,16 +93,24 @@ template <bool TA, bool TB>
 __global__ __launch_bounds__(256) void sgemm_mfma_kernel(const float *__restrict__ A, int64_t lda,
                                                          const float *__restrict__ B, int64_t ldb,
                                                          float *__restrict__ C, int64_t ldc,
-                                                         int64_t M, int64_t N, int64_t K,
-                                                         float alpha, float beta, int tiles_m) {
+                                                         int64_t M, int64_t N, int64_t Kall,
+                                                         float alpha, float beta, int tiles_m,
+                                                         int tiles_mn, int64_t kc, int64_t cstride) {
     using OA = SgOperand<TA>;    // op(A) rows m: K-major when A is transposed
     using OB = SgOperand<!TB>;   // op(B) rows n: K-major when B is as stored ([k][n])
     __shared__ __attribute__((aligned(16))) float smem[2 * (OA::TILE + OB::TILE)];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid & 1, wn = wid >> 1;
     const int fr = lane & 15, q = lane >> 4;
-    const int tm = (int)blockIdx.x % tiles_m, tn = (int)blockIdx.x / tiles_m;
+    // the K range and partial output of a split K, as in sgemm_mfma2_kernel
+    const int tile = (int)(blockIdx.x % (unsigned)tiles_mn), split = (int)(blockIdx.x / (unsigned)tiles_mn);
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
     const int64_t m0 = (int64_t)tm * kSgBM, n0 = (int64_t)tn * kSgBN;
+    const int64_t kb = (int64_t)split * kc;
+    const int64_t K = std::min<int64_t>(kc, Kall - kb);
+    A += TA ? kb * lda : kb;
+    B += TB ? kb : kb * ldb;
+    C += split * cstride;
 
     OA a{A, lda, M, K, m0, {}};
     OB b{B, ldb, N, K, n0, {}};
@@ -380,7 +388,7 @@ __global__ __launch_bounds__(256) void sgemm_mfma2_kernel(const float *__restric
 
 // Split K: C = alpha * (P_0 + P_1 + ... + P_{S-1}) + beta * C, the partial
 // products P_s ([M, N], N contiguous, P_s at P + s * pstride) added in order.
-constexpr int64_t kSplitMinK = 256;
+constexpr int64_t kSplitMinK = 64;
 
 __global__ __launch_bounds__(256) void sgemm_split_sum_kernel(const float *__restrict__ P, int S,
                                                               int64_t pstride, float *__restrict__ C,
@@ -474,62 +482,59 @@ extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k
     const int64_t tm = ceil_div(m, kSgBM), tn = ceil_div(n, kSgBN);
     RNN_REQUIRE(tm * tn <= 0x7fffffffLL && tm < 0x7fffffffLL, "%s: too many tiles", name);
     const unsigned grid = (unsigned)(tm * tn);
+    // Fewer tiles than CUs: K is split into S ranges of whole 32-k stages
+    // (the last one takes the rest; at least kSplitMinK each, S <= 16), each
+    // range's tiles go to stream-ordered scratch, and sgemm_split_sum_kernel
+    // adds the S partial tiles in order into C. S minimises the busiest CU's
+    // k count, ceil(tiles S / CUs) (kc + 64), plus the partial sums' traffic
+    // counted as S m n / 65536 k (measured, 128-row tiles at M = 16 and 256,
+    // N = 11008, K = 4096: the times follow that count; the 64 is a workgroup's
+    // prologue and epilogue).
+    int S = 1;
+    int64_t kc = k;
+    if (grid < (unsigned)cus && k >= 2 * kSplitMinK) {
+        int64_t best = k + 64;
+        for (int s = 2; s <= 16 && s * kSplitMinK <= k; ++s) {
+            const int64_t kcs = ceil_div(ceil_div(k, s), kSgBK) * kSgBK;
+            const int64_t ss = ceil_div(k, kcs);
+            const int64_t cost = ceil_div((int64_t)grid * ss, cus) * (kcs + 64) + ss * m * n / 65536;
+            if (cost < best) best = cost, S = (int)ss, kc = kcs;
+        }
+    }
+    float *out = c, *ws = nullptr;
+    int64_t ldo = ldc;
+    float al = alpha, be = beta;
+    if (S > 1) {
+        RNN_TRY(check_hip(hipMallocAsync(reinterpret_cast<void **>(&ws), sizeof(float) * S * m * n, st), name));
+        out = ws, ldo = n, al = 1.0f, be = 0.0f;
+    }
+    const unsigned g2 = grid * (unsigned)S;
+    const int64_t cs = S > 1 ? m * n : 0;
     // K % 32 == 0, and row strides and K below 4M floats (the buffer ranges of
-    // a block or a stage stay under 2 GiB): the single-layout kernel
+    // a block or a stage stay under 2 GiB): the single-layout kernel; else
+    // the guarded one (any K)
+#define RNN_SG(KERNEL, TA, TB) \
+    KERNEL<TA, TB><<<g2, 256, 0, st>>>(a, lda, b, ldb, out, ldo, m, n, k, al, be, (int)tm, (int)grid, kc, cs)
     if (k % kSgBK == 0 && k < (int64_t(1) << 22) && lda < (int64_t(1) << 22) &&
         ldb < (int64_t(1) << 22)) {
-        // Fewer tiles than CUs: K is split into S ranges of whole 32-k
-        // stages (at least kSplitMinK each, S <= 16), each range's tiles go to
-        // stream-ordered scratch, and sgemm_split_sum_kernel adds the S
-        // partial tiles in order into C. S minimises the busiest CU's k
-        // count, ceil(tiles S / CUs) kc, plus the partial sums' traffic
-        // counted as S m n / 65536 k (measured, 128-row tiles at M = 16 and
-        // 256, N = 11008, K = 4096: the times follow that count).
-        int S = 1;
-        int64_t kc = k;
-        if (grid < (unsigned)cus && k >= 2 * kSplitMinK) {
-            int64_t best = k;
-            for (int s = 2; s <= 16 && s * kSplitMinK <= k; ++s) {
-                const int64_t kcs = ceil_div(ceil_div(k, s), kSgBK) * kSgBK;
-                const int64_t ss = ceil_div(k, kcs);
-                const int64_t cost = ceil_div((int64_t)grid * ss, cus) * kcs + ss * m * n / 65536;
-                if (cost < best) best = cost, S = (int)ss, kc = kcs;
-            }
-        }
-        float *out = c, *ws = nullptr;
-        int64_t ldo = ldc;
-        float al = alpha, be = beta;
-        if (S > 1) {
-            RNN_TRY(check_hip(hipMallocAsync(reinterpret_cast<void **>(&ws), sizeof(float) * S * m * n, st), name));
-            out = ws, ldo = n, al = 1.0f, be = 0.0f;
-        }
-        const unsigned g2 = grid * (unsigned)S;
-        const int64_t cs = S > 1 ? m * n : 0;
-        if (!transa && !transb)
-            sgemm_mfma2_kernel<false, false><<<g2, 256, 0, st>>>(a, lda, b, ldb, out, ldo, m, n, k, al, be, (int)tm, (int)grid, kc, cs);
-        else if (!transa && transb)
-            sgemm_mfma2_kernel<false, true><<<g2, 256, 0, st>>>(a, lda, b, ldb, out, ldo, m, n, k, al, be, (int)tm, (int)grid, kc, cs);
-        else if (transa && !transb)
-            sgemm_mfma2_kernel<true, false><<<g2, 256, 0, st>>>(a, lda, b, ldb, out, ldo, m, n, k, al, be, (int)tm, (int)grid, kc, cs);
-        else
-            sgemm_mfma2_kernel<true, true><<<g2, 256, 0, st>>>(a, lda, b, ldb, out, ldo, m, n, k, al, be, (int)tm, (int)grid, kc, cs);
-        if (S == 1) return check_launch(name);
-        const int rc = check_launch(name);
-        if (rc == RNN_OK) {
-            const dim3 sg((unsigned)ceil_div(n, 256), (unsigned)std::min<int64_t>(m, 65535));
-            sgemm_split_sum_kernel<<<sg, 256, 0, st>>>(ws, S, m * n, c, ldc, m, n, alpha, beta);
-        }
-        const int rs = rc == RNN_OK ? check_launch(name) : rc;
-        const int rf = check_hip(hipFreeAsync(ws, st), name);
-        return rs != RNN_OK ? rs : rf;
+        if (!transa && !transb) RNN_SG(sgemm_mfma2_kernel, false, false);
+        else if (!transa && transb) RNN_SG(sgemm_mfma2_kernel, false, true);
+        else if (transa && !transb) RNN_SG(sgemm_mfma2_kernel, true, false);
+        else RNN_SG(sgemm_mfma2_kernel, true, true);
+    } else {
+        if (!transa && !transb) RNN_SG(sgemm_mfma_kernel, false, false);
+        else if (!transa && transb) RNN_SG(sgemm_mfma_kernel, false, true);
+        else if (transa && !transb) RNN_SG(sgemm_mfma_kernel, true, false);
+        else RNN_SG(sgemm_mfma_kernel, true, true);
     }
-    if (!transa && !transb)
-        sgemm_mfma_kernel<false, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
-    else if (!transa && transb)
-        sgemm_mfma_kernel<false, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
-    else if (transa && !transb)
-        sgemm_mfma_kernel<true, false><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
-    else
-        sgemm_mfma_kernel<true, true><<<grid, 256, 0, st>>>(a, lda, b, ldb, c, ldc, m, n, k, alpha, beta, (int)tm);
-    return check_launch(name);
+#undef RNN_SG
+    if (S == 1) return check_launch(name);
+    const int rc = check_launch(name);
+    if (rc == RNN_OK) {
+        const dim3 sg((unsigned)ceil_div(n, 256), (unsigned)std::min<int64_t>(m, 65535));
+        sgemm_split_sum_kernel<<<sg, 256, 0, st>>>(ws, S, m * n, c, ldc, m, n, alpha, beta);
+    }
+    const int rs = rc == RNN_OK ? check_launch(name) : rc;
+    const int rf = check_hip(hipFreeAsync(ws, st), name);
+    return rs != RNN_OK ? rs : rf;
 }
