@@ -386,6 +386,156 @@ __global__ __launch_bounds__(256) void sgemm_mfma2_kernel(const float *__restric
         }
 }
 
+// Decode shapes of Linear::forward (C = alpha A B^T + beta C, B stored
+// [n, k], m <= 16): bound by reading B once. A workgroup owns TPW 16-row
+// tiles of B (n); its 4 waves split K in steps of 32 (128 bytes of a row).
+// Per step lane (r = lane % 16, q = lane / 16) loads 16 bytes at k + 4q and
+// k + 16 + 4q of B row n0 + r of each tile (whole cache lines per 4 lanes,
+// non-temporal) and of A row r, and runs 4 v_mfma_f32_16x16x4f32 per
+// 16 bytes: lane group q supplies k + 4q + s to MFMA s for both operands,
+// so D[m][n] sums every k once. D rows past M (A rows clamped to M - 1) and
+// columns past N (B rows clamped to N - 1) are not stored. The last step of
+// a K that is not a multiple of 32 zeroes the 16-byte pieces past K in both
+// operands. The 4 waves' partial tiles are added in wave order through LDS.
+template <int TPW>
+__global__ __launch_bounds__(256) void sgemm_skinny_nt_kernel(const float *__restrict__ A, int64_t lda,
+                                                              const float *__restrict__ B, int64_t ldb,
+                                                              float *__restrict__ C, int64_t ldc,
+                                                              int M, int64_t N, int64_t K, float alpha,
+                                                              float beta) {
+    constexpr int D = 4;  // steps in flight per wave
+    __shared__ float part[4][TPW][16][17];
+    __shared__ f4 stage[4][TPW][16][8];
+    // (wid in a scalar register: the step offsets below are the buffer loads'
+    // scalar offsets)
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * 16 * TPW;
+    const int64_t nsteps = (K + 31) / 32, full = K / 32;
+    const int64_t s0 = nsteps * wid / 4, s1 = nsteps * (wid + 1) / 4;
+    const int64_t sf = s1 < full ? s1 : full;  // unguarded steps [s0, sf)
+    // B: one buffer descriptor over the tiles' rows (the host keeps the
+    // range under 2 GiB), rows past N clamped to N - 1
+    const int64_t last_row = std::min<int64_t>(n0 + 16 * TPW, N) - 1;
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(B + n0 * ldb), 0, (int)(((last_row - n0) * ldb + K) * 4), 0x00020000);
+    // MFMA layout (the K tail): row r, bytes 16q; whole lines (the steps):
+    // row lane / 8 + 8h, bytes 16 (lane % 8), regrouped through LDS
+    uint32_t boff[TPW], lineoff[TPW][2];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        boff[t] = (uint32_t)((std::min<int64_t>(n0 + 16 * t + r, last_row) - n0) * ldb * 4 + 16 * q);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            lineoff[t][h] = (uint32_t)((std::min<int64_t>(n0 + 16 * t + (lane >> 3) + 8 * h, last_row) - n0) *
+                                           ldb * 4 + 16 * (lane & 7));
+    }
+    const float *ap = A + (int64_t)(r < M ? r : M - 1) * lda + 4 * q;
+    // this wave's regroup slice: 16 rows x 8 16-byte chunks per tile, chunk c
+    // of row j at c ^ (j & 7)
+    f4 (*stg)[16][8] = stage[wid];
+
+    f4 acc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    f4 xa[D][2], wb[D][TPW][2];
+    auto load = [&](int d, int64_t step) {
+        const int64_t k = 32 * step;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            xa[d][h] = *reinterpret_cast<const f4 *>(ap + k + 16 * h);
+#pragma unroll
+            for (int t = 0; t < TPW; ++t)
+                wb[d][t][h] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(br, lineoff[t][h], (uint32_t)(k * 4), 2));
+        }
+    };
+    auto mfmas = [&](const f4 (&x)[2], const f4 (&w)[TPW][2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int t = 0; t < TPW; ++t)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[h][e], w[t][h][e], acc[t], 0, 0, 0);
+    };
+    // a step's whole-line loads into the MFMA layout: lane (r, q) takes
+    // chunks q and 4 + q of row r. One wave's LDS operations complete in
+    // order, so the slice is rewritten by the next step without a barrier.
+    auto consume = [&](int d) {
+        f4 w[TPW][2];
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = (lane >> 3) + 8 * h;
+                stg[t][j][(lane & 7) ^ (j & 7)] = wb[d][t][h];
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) w[t][h] = stg[t][r][(4 * h + q) ^ (r & 7)];
+        }
+        mfmas(xa[d], w);
+    };
+    // D steps in flight: the steady loop refills every buffer unconditionally
+    // (so the compiler's wait counts see D - 1 steps of loads still in flight
+    // at each use); the first D loads are issued whole, a step past the last
+    // one repeated, and the last up to 2D - 1 steps are drained after the loop
+    if (sf > s0) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) load(d, std::min<int64_t>(s0 + d, sf - 1));
+        int64_t s = s0;
+        for (; s + 2 * D <= sf; s += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                consume(d);
+                load(d, s + d + D);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (s + d < sf) consume(d);
+            if (s + d + D < sf) load(d, s + d + D);
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (s + D + d < sf) consume(d);
+    }
+    if (s1 > full && s1 - 1 >= s0) {  // the K tail: 16-byte pieces past K are zero
+        const int64_t k = 32 * full;
+        f4 x[2], w[TPW][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool ok = k + 16 * h + 4 * q < K;
+            x[h] = ok ? *reinterpret_cast<const f4 *>(ap + k + 16 * h) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < TPW; ++t)
+                w[t][h] = ok ? __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          br, boff[t], (uint32_t)((k + 16 * h) * 4), 2))
+                             : f4{0.f, 0.f, 0.f, 0.f};
+        }
+        mfmas(x, w);
+    }
+    // lane holds D[m = 4q + v][n = r] of each tile
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[wid][t][4 * q + v][r] = acc[t][v];
+    __syncthreads();
+    const int m = tid >> 4, nn = tid & 15;
+    if (m < M) {
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            const int64_t n = n0 + 16 * t + nn;
+            if (n < N) {
+                const float sum = ((part[0][t][m][nn] + part[1][t][m][nn]) + part[2][t][m][nn]) + part[3][t][m][nn];
+                float *cp = C + (int64_t)m * ldc + n;
+                const float o = alpha * sum;
+                *cp = beta != 0.0f ? o + beta * *cp : o;
+            }
+        }
+    }
+}
+
 // Split K: C = alpha * (P_0 + P_1 + ... + P_{S-1}) + beta * C, the partial
 // products P_s ([M, N], N contiguous, P_s at P + s * pstride) added in order.
 constexpr int64_t kSplitMinK = 64;
@@ -473,6 +623,18 @@ extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k
     // The MFMA path moves float4 along each operand's contiguous dimension.
     const bool fast = (lda & 3) == 0 && (ldb & 3) == 0 && aligned16f(a) && aligned16f(b) &&
                       (transa ? m % 4 == 0 : k % 4 == 0) && (transb ? k % 4 == 0 : n % 4 == 0);
+    // m <= 16 with B stored [n, k] and at least 256 rows of B: the skinny
+    // kernel, 2 tiles of 16 rows per workgroup while that leaves every CU one
+    // (one tile otherwise); the B range of a workgroup stays under 2 GiB
+    if (fast && !transa && transb && m <= 16 && n >= 256 && k >= 32 &&
+        (32 * ldb + k) * 4 < (int64_t(1) << 31)) {
+        const int64_t tiles = ceil_div(n, 16);
+        if (tiles >= 2 * cus)
+            sgemm_skinny_nt_kernel<2><<<(unsigned)ceil_div(tiles, 2), 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
+        else
+            sgemm_skinny_nt_kernel<1><<<(unsigned)tiles, 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
+        return check_launch(name);
+    }
     if (!fast) {
         const int64_t blocks = std::min<int64_t>(ceil_div(m * n, 256), 8 * cus);
         sgemm_simple_kernel<<<(unsigned)blocks, 256, 0, st>>>(transa, transb, a, lda, b, ldb, c, ldc,

@@ -65,6 +65,10 @@ def test_sgemm_reference_cases(dev, hip, case):
     (517, 301, 95, -1.25, 1.0, 3),       # odd k and padded strides -> one-thread-per-output path
     (256, 384, 1024, 1.0, -0.5, 4),      # padded strides (MFMA path; 6 tiles: K split in 4)
     (64, 1000, 4128, 1.5, 0.5, 0),       # 8 tiles: K split in 15 ranges, the last one short
+    (16, 300, 784, 1.0, 0.5, 0),         # transb: the skinny kernel, a K tail, 19 row tiles
+    (5, 4100, 1056, -1.0, 0.0, 4),       # transb: skinny, padded strides, a ragged last tile
+    (3, 8200, 64, 2.0, 1.0, 0),          # transb: skinny, 2 tiles per workgroup, 2 of 4 waves idle
+    (7, 260, 4096, 0.5, 0.0, 0),         # transb: skinny, 32 steps per wave (the steady loop)
 ])
 def test_sgemm_shapes(dev, hip, ta, tb, m, n, k, alpha, beta, pad):
     rng = np.random.default_rng(m * 7 + n * 3 + k + 11 * ta + 13 * tb)
