@@ -388,31 +388,42 @@ __global__ __launch_bounds__(256) void sgemm_mfma2_kernel(const float *__restric
 
 // Decode shapes of Linear::forward (C = alpha A B^T + beta C, B stored
 // [n, k], m <= 16): bound by reading B once. A workgroup owns TPW 16-row
-// tiles of B (n); its 4 waves split K in steps of 32 (128 bytes of a row).
-// Per step lane (r = lane % 16, q = lane / 16) loads 16 bytes at k + 4q and
-// k + 16 + 4q of B row n0 + r of each tile (whole cache lines per 4 lanes,
-// non-temporal) and of A row r, and runs 4 v_mfma_f32_16x16x4f32 per
-// 16 bytes: lane group q supplies k + 4q + s to MFMA s for both operands,
-// so D[m][n] sums every k once. D rows past M (A rows clamped to M - 1) and
-// columns past N (B rows clamped to N - 1) are not stored. The last step of
-// a K that is not a multiple of 32 zeroes the 16-byte pieces past K in both
-// operands. The 4 waves' partial tiles are added in wave order through LDS.
-template <int TPW>
-__global__ __launch_bounds__(256) void sgemm_skinny_nt_kernel(const float *__restrict__ A, int64_t lda,
+// tiles of B (n); its NW waves split K in steps of KS (4 KS bytes of a row),
+// D steps in flight per wave. A step's B bytes arrive in whole-line loads
+// (lane l: row l / (KS/4) + (64/(KS/4)) i, 16 bytes at 16 (l % (KS/4));
+// non-temporal) and are regrouped through the wave's LDS slice so that lane
+// (r = lane % 16, q = lane / 16) holds the 16-byte pieces at k + 16h + 4q of
+// row n0 + r; the same pieces of A row r come straight from memory. Each
+// piece feeds 4 v_mfma_f32_16x16x4f32: lane group q supplies k + 16h + 4q + s
+// to MFMA s for both operands, so D[m][n] sums every k once. D rows past M
+// (A rows clamped to M - 1) and columns past N (B rows clamped to N - 1) are
+// not stored. The last step of a K that is not a multiple of KS zeroes the
+// 16-byte pieces past K in both operands. The NW waves' partial tiles are
+// added in wave order through LDS. (Measured, 16 x 11008 x 4096, B rotated
+// past the MALL: 4 waves, KS = 64, D = 2, one tile per workgroup 38.1 us;
+// two tiles 39.8; KS = 32 with 4 steps in flight, two tiles 42.3; MFMA-layout
+// B loads instead of whole lines 62; 8 waves 40.4; D = 3 41.1. torch.matmul
+// 36.8.)
+template <int TPW, int KS, int NW>
+__global__ __launch_bounds__(64 * NW) void sgemm_skinny_nt_kernel(const float *__restrict__ A, int64_t lda,
                                                               const float *__restrict__ B, int64_t ldb,
                                                               float *__restrict__ C, int64_t ldc,
                                                               int M, int64_t N, int64_t K, float alpha,
                                                               float beta) {
-    constexpr int D = 4;  // steps in flight per wave
-    __shared__ float part[4][TPW][16][17];
-    __shared__ f4 stage[4][TPW][16][8];
+    constexpr int D = 2;          // steps in flight per wave
+    constexpr int CH = KS / 4;    // 16-byte chunks of a row per step
+    constexpr int RPI = 64 / CH;  // rows per whole-line load
+    constexpr int L = 16 / RPI;   // whole-line loads per tile and step
+    constexpr int H = KS / 16;    // MFMA-layout 16-byte pieces per lane and step
+    __shared__ float part[NW][TPW][16][17];
+    __shared__ f4 stage[NW][TPW][16][CH];
     // (wid in a scalar register: the step offsets below are the buffer loads'
     // scalar offsets)
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 15, q = lane >> 4;
     const int64_t n0 = (int64_t)blockIdx.x * 16 * TPW;
-    const int64_t nsteps = (K + 31) / 32, full = K / 32;
-    const int64_t s0 = nsteps * wid / 4, s1 = nsteps * (wid + 1) / 4;
+    const int64_t nsteps = (K + KS - 1) / KS, full = K / KS;
+    const int64_t s0 = nsteps * wid / NW, s1 = nsteps * (wid + 1) / NW;
     const int64_t sf = s1 < full ? s1 : full;  // unguarded steps [s0, sf)
     // B: one buffer descriptor over the tiles' rows (the host keeps the
     // range under 2 GiB), rows past N clamped to N - 1
@@ -420,39 +431,39 @@ __global__ __launch_bounds__(256) void sgemm_skinny_nt_kernel(const float *__res
     const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(B + n0 * ldb), 0, (int)(((last_row - n0) * ldb + K) * 4), 0x00020000);
     // MFMA layout (the K tail): row r, bytes 16q; whole lines (the steps):
-    // row lane / 8 + 8h, bytes 16 (lane % 8), regrouped through LDS
-    uint32_t boff[TPW], lineoff[TPW][2];
+    // row lane / CH + RPI i, bytes 16 (lane % CH), regrouped through LDS
+    uint32_t boff[TPW], lineoff[TPW][L];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
         boff[t] = (uint32_t)((std::min<int64_t>(n0 + 16 * t + r, last_row) - n0) * ldb * 4 + 16 * q);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-            lineoff[t][h] = (uint32_t)((std::min<int64_t>(n0 + 16 * t + (lane >> 3) + 8 * h, last_row) - n0) *
-                                           ldb * 4 + 16 * (lane & 7));
+        for (int i = 0; i < L; ++i)
+            lineoff[t][i] = (uint32_t)((std::min<int64_t>(n0 + 16 * t + lane / CH + RPI * i, last_row) - n0) *
+                                           ldb * 4 + 16 * (lane % CH));
     }
     const float *ap = A + (int64_t)(r < M ? r : M - 1) * lda + 4 * q;
-    // this wave's regroup slice: 16 rows x 8 16-byte chunks per tile, chunk c
-    // of row j at c ^ (j & 7)
-    f4 (*stg)[16][8] = stage[wid];
+    // this wave's regroup slice: 16 rows x CH 16-byte chunks per tile, chunk
+    // c of row j at c ^ (j % CH)
+    f4 (*stg)[16][CH] = stage[wid];
 
     f4 acc[TPW];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-    f4 xa[D][2], wb[D][TPW][2];
+    f4 xa[D][H], wb[D][TPW][L];
     auto load = [&](int d, int64_t step) {
-        const int64_t k = 32 * step;
+        const int64_t k = KS * step;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            xa[d][h] = *reinterpret_cast<const f4 *>(ap + k + 16 * h);
+        for (int h = 0; h < H; ++h) xa[d][h] = *reinterpret_cast<const f4 *>(ap + k + 16 * h);
+#pragma unroll
+        for (int i = 0; i < L; ++i)
 #pragma unroll
             for (int t = 0; t < TPW; ++t)
-                wb[d][t][h] = __builtin_bit_cast(
-                    f4, __builtin_amdgcn_raw_buffer_load_b128(br, lineoff[t][h], (uint32_t)(k * 4), 2));
-        }
+                wb[d][t][i] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(br, lineoff[t][i], (uint32_t)(k * 4), 2));
     };
-    auto mfmas = [&](const f4 (&x)[2], const f4 (&w)[TPW][2]) {
+    auto mfmas = [&](const f4 (&x)[H], const f4 (&w)[TPW][H]) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < H; ++h)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -463,16 +474,16 @@ __global__ __launch_bounds__(256) void sgemm_skinny_nt_kernel(const float *__res
     // chunks q and 4 + q of row r. One wave's LDS operations complete in
     // order, so the slice is rewritten by the next step without a barrier.
     auto consume = [&](int d) {
-        f4 w[TPW][2];
+        f4 w[TPW][H];
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int j = (lane >> 3) + 8 * h;
-                stg[t][j][(lane & 7) ^ (j & 7)] = wb[d][t][h];
+            for (int i = 0; i < L; ++i) {
+                const int j = lane / CH + RPI * i;
+                stg[t][j][(lane % CH) ^ (j % CH)] = wb[d][t][i];
             }
 #pragma unroll
-            for (int h = 0; h < 2; ++h) w[t][h] = stg[t][r][(4 * h + q) ^ (r & 7)];
+            for (int h = 0; h < H; ++h) w[t][h] = stg[t][r][(4 * h + q) ^ (r % CH)];
         }
         mfmas(xa[d], w);
     };
@@ -501,10 +512,10 @@ __global__ __launch_bounds__(256) void sgemm_skinny_nt_kernel(const float *__res
             if (s + D + d < sf) consume(d);
     }
     if (s1 > full && s1 - 1 >= s0) {  // the K tail: 16-byte pieces past K are zero
-        const int64_t k = 32 * full;
-        f4 x[2], w[TPW][2];
+        const int64_t k = KS * full;
+        f4 x[H], w[TPW][H];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < H; ++h) {
             const bool ok = k + 16 * h + 4 * q < K;
             x[h] = ok ? *reinterpret_cast<const f4 *>(ap + k + 16 * h) : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -522,12 +533,14 @@ __global__ __launch_bounds__(256) void sgemm_skinny_nt_kernel(const float *__res
         for (int v = 0; v < 4; ++v) part[wid][t][4 * q + v][r] = acc[t][v];
     __syncthreads();
     const int m = tid >> 4, nn = tid & 15;
-    if (m < M) {
+    if (tid < 256 && m < M) {
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
             const int64_t n = n0 + 16 * t + nn;
             if (n < N) {
-                const float sum = ((part[0][t][m][nn] + part[1][t][m][nn]) + part[2][t][m][nn]) + part[3][t][m][nn];
+                float sum = part[0][t][m][nn];
+#pragma unroll
+                for (int v = 1; v < NW; ++v) sum += part[v][t][m][nn];
                 float *cp = C + (int64_t)m * ldc + n;
                 const float o = alpha * sum;
                 *cp = beta != 0.0f ? o + beta * *cp : o;
@@ -624,15 +637,16 @@ extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k
     const bool fast = (lda & 3) == 0 && (ldb & 3) == 0 && aligned16f(a) && aligned16f(b) &&
                       (transa ? m % 4 == 0 : k % 4 == 0) && (transb ? k % 4 == 0 : n % 4 == 0);
     // m <= 16 with B stored [n, k] and at least 256 rows of B: the skinny
-    // kernel, 2 tiles of 16 rows per workgroup while that leaves every CU one
-    // (one tile otherwise); the B range of a workgroup stays under 2 GiB
+    // kernel, one 16-row tile of B per workgroup, 8 waves while there are
+    // fewer than two tiles per CU (else 4); the B range of a workgroup stays
+    // under 2 GiB
     if (fast && !transa && transb && m <= 16 && n >= 256 && k >= 32 &&
-        (32 * ldb + k) * 4 < (int64_t(1) << 31)) {
+        (16 * ldb + k) * 4 < (int64_t(1) << 31)) {
         const int64_t tiles = ceil_div(n, 16);
         if (tiles >= 2 * cus)
-            sgemm_skinny_nt_kernel<2><<<(unsigned)ceil_div(tiles, 2), 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
+            sgemm_skinny_nt_kernel<1, 64, 4><<<(unsigned)tiles, 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
         else
-            sgemm_skinny_nt_kernel<1><<<(unsigned)tiles, 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
+            sgemm_skinny_nt_kernel<1, 64, 8><<<(unsigned)tiles, 512, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
         return check_launch(name);
     }
     if (!fast) {
