@@ -401,9 +401,10 @@ __global__ __launch_bounds__(256) void sgemm_mfma2_kernel(const float *__restric
 // 16-byte pieces past K in both operands. The NW waves' partial tiles are
 // added in wave order through LDS. (Measured, 16 x 11008 x 4096, B rotated
 // past the MALL: 4 waves, KS = 64, D = 2, one tile per workgroup 38.1 us;
-// two tiles 39.8; KS = 32 with 4 steps in flight, two tiles 42.3; MFMA-layout
-// B loads instead of whole lines 62; 8 waves 40.4; D = 3 41.1. torch.matmul
-// 36.8.)
+// two tiles 39.8; KS = 32 with 4 steps in flight, two tiles 42.3; 8 waves
+// 40.4; D = 3 41.1; torch.matmul 36.8. Back-to-back calls on one B: the
+// KS = 32 two-tile kernel with B loaded straight in the MFMA layout 62,
+// with whole lines 40.7.)
 template <int TPW, int KS, int NW>
 __global__ __launch_bounds__(64 * NW) void sgemm_skinny_nt_kernel(const float *__restrict__ A, int64_t lda,
                                                               const float *__restrict__ B, int64_t ldb,
