@@ -729,6 +729,7 @@ def bench_igemm_512(H, dev, steps, with_cpu):
 
 # ---------------------------------------------------------------- f32 GEMM
 SGEMM_MNK = (4096, 4096, 4096)
+SGEMM_DECODE_MNK = (16, 11008, 4096)
 
 
 def bench_sgemm(H, dev, steps):
@@ -763,6 +764,27 @@ def bench_sgemm(H, dev, steps):
     nt, nt_lib, ms_nt = run(
         lambda: H.sgemm(H.NO_TRANS, H.TRANS, m, n, k, 1.0, a, k, bt, k, 0.0, c, n),
         lambda: torch.matmul(a, bt.t(), out=c))
+    del a, b, bt, c
+    # Linear::forward at decode (x [16, 4096] * W^T, W [11008, 4096] f32):
+    # bound by reading W once; W rotates over copies past the MALL
+    dm, dn, dk = SGEMM_DECODE_MNK
+    wbytes = 4 * dn * dk
+    copies = max(2, -(-640 * 2**20 // wbytes))
+    ws = [gen_f32((dn, dk), 30 + i, dev) for i in range(copies)]
+    x = gen_f32((dm, dk), 29, dev)
+    y = torch.empty((dm, dn), dtype=torch.float32, device=dev)
+    nl = copies * 10
+    ms_d = graph_timed(lambda i: H.sgemm(H.NO_TRANS, H.TRANS, dm, dn, dk, 1.0, x, dk, ws[i % copies], dk,
+                                         0.0, y, dn), nl)
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        ms_dt = graph_timed(lambda i: torch.matmul(x, ws[i % copies].t(), out=y), nl)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+    dbytes = wbytes + 4 * dm * dk + 4 * dm * dn
+    del ws
+    torch.cuda.empty_cache()
     return {"m": m, "n": n, "k": k, "trans": "nn", "us": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
             "frac_fp32_mfma_peak": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "torch_matmul_TFLOP/s": round(tflops_lib, 1), "traffic": traffic_for("f32_sgemm"),
@@ -771,7 +793,14 @@ def bench_sgemm(H, dev, steps):
             "nt": {"us": round(ms_nt * 1e3, 1), "TFLOP/s": round(nt, 1),
                    "frac_fp32_mfma_peak": round(nt / PEAK_FP32_MFMA_TFLOPS, 4),
                    "torch_matmul_TFLOP/s": round(nt_lib, 1),
-                   "kernel": "sgemm_mfma2_kernel<false,true> (B stored [n, k]: both operands K-contiguous)"}}
+                   "kernel": "sgemm_mfma2_kernel<false,true> (B stored [n, k]: both operands K-contiguous)"},
+            "decode": {"m": dm, "n": dn, "k": dk, "trans": "nt", "us": round(ms_d * 1e3, 2),
+                       "GB/s": round(dbytes / (ms_d * 1e-3) / 1e9, 1),
+                       "frac_hbm": round(dbytes / (ms_d * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                       "torch_matmul_us": round(ms_dt * 1e3, 2),
+                       "kernel": "sgemm_skinny_nt_kernel<1,64,4> (m <= 16, B in whole lines regrouped "
+                                 "through LDS, v_mfma_f32_16x16x4f32)",
+                       "timing": "HIP-graph replay, median replay / launches, W rotated over copies"}}
 
 
 # ---------------------------------------------------------------- copy ceiling
@@ -946,6 +975,10 @@ def compact(result):
         if "nt" in comp["f32_sgemm"]:
             other["f32_sgemm"]["nt_TFLOP/s"] = comp["f32_sgemm"]["nt"]["TFLOP/s"]
             other["f32_sgemm"]["nt_frac"] = comp["f32_sgemm"]["nt"]["frac_fp32_mfma_peak"]
+        if "decode" in comp["f32_sgemm"]:
+            other["f32_sgemm"]["decode_m16_n11008_us"] = comp["f32_sgemm"]["decode"]["us"]
+            other["f32_sgemm"]["decode_frac_hbm"] = comp["f32_sgemm"]["decode"]["frac_hbm"]
+            other["f32_sgemm"]["decode_torch_us"] = comp["f32_sgemm"]["decode"]["torch_matmul_us"]
     if "copy_ceiling" in comp:
         other["copy_ceiling_GBs"] = comp["copy_ceiling"]["GB/s"]
     if "mfma_clock_probe" in comp:
