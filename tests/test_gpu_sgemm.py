@@ -124,3 +124,19 @@ def test_sgemm_large_against_float64(dev, hip):
     u = 2.0 ** -24
     lim = (k + 2) * u / (1 - (k + 2) * u) * scale
     assert bool(((c.double() - exact).abs() <= lim).all())
+
+
+def test_sgemm_split_and_skinny_repeatable(dev, hip):
+    """The split-K route (fewer tiles than CUs: partial tiles in scratch, summed
+    in a fixed order) and the skinny m <= 16 kernel (waves' partial tiles
+    summed in wave order) give the same bits on every call, and agree with a
+    float64 product within the rounding bound."""
+    rng = np.random.default_rng(77)
+    for (m, n, k, tb) in ((64, 1000, 4128, 0), (64, 1000, 4128, 1), (16, 2000, 4096, 1)):
+        a = rng.standard_normal(m * k).astype(np.float32)
+        b = rng.standard_normal(n * k).astype(np.float32)
+        ldb = k if tb else n
+        c0 = np.zeros(m * n, np.float32)
+        runs = [run(dev, hip, 0, tb, m, n, k, 1.0, a, k, b, ldb, 0.0, c0, n) for _ in range(3)]
+        assert all(np.array_equal(runs[0].view(np.uint32), r.view(np.uint32)) for r in runs[1:])
+        check(runs[0], 0, tb, m, n, k, 1.0, a, k, b, ldb, 0.0, c0, n)
