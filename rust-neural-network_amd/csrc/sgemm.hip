@@ -550,6 +550,130 @@ __global__ __launch_bounds__(64 * NW) void sgemm_skinny_nt_kernel(const float *_
     }
 }
 
+// Decode shapes of Tensor::matmul (C = alpha A B + beta C with B stored
+// [k, n], m <= 16): bound by reading B once. A workgroup owns 32 columns of
+// B (two 16-column tiles); its NW waves split K in steps of 16. A step's B
+// bytes arrive as whole 128-byte row segments (lane l: k row l / 8 + 8 i,
+// columns 4 (l % 8) .. + 3; non-temporal) and are written transposed into
+// the wave's LDS slice ([column][k], 20-float pitch), so that lane
+// (r = lane % 16, q = lane / 16) reads the 4 k values 4q .. 4q + 3 of column
+// r of each tile in one 16-byte read; A row r's same 4 k values come straight
+// from memory. MFMA s takes k = 4q + s from both operands, so D[m][n] sums
+// every k once. D rows past M (A rows clamped to M - 1) and columns past N
+// (zeros from the buffer range) are not stored; the last step of a K that is
+// not a multiple of 16 zeroes the k rows past K. The NW waves' partial tiles
+// are added in wave order through LDS.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void sgemm_skinny_nn_kernel(const float *__restrict__ A, int64_t lda,
+                                                                  const float *__restrict__ B, int64_t ldb,
+                                                                  float *__restrict__ C, int64_t ldc,
+                                                                  int M, int64_t N, int64_t K, float alpha,
+                                                                  float beta) {
+    constexpr int D = 4;   // steps in flight per wave
+    constexpr int KS = 16; // k per step
+    constexpr int LP = 20; // LDS floats per column of a step
+    __shared__ float part[NW][2][16][17];
+    __shared__ __attribute__((aligned(16))) float stage[NW][32 * LP];
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * 32;
+    const int64_t nsteps = (K + KS - 1) / KS, full = K / KS;
+    const int64_t s0 = nsteps * wid / NW, s1 = nsteps * (wid + 1) / NW;
+    const int64_t sf = s1 < full ? s1 : full;
+    // B from column n0: the range ends at the last element of B, so columns
+    // past N in the last k row read zeros (other rows' columns past N only
+    // reach outputs that are not stored); the host keeps the range under 2 GiB
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(B + n0), 0, (int)(((K - 1) * ldb + (N - n0)) * 4), 0x00020000);
+    uint32_t boff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) boff[i] = (uint32_t)((((lane >> 3) + 8 * i) * ldb + 4 * (lane & 7)) * 4);
+    const float *ap = A + (int64_t)(r < M ? r : M - 1) * lda + 4 * q;
+    float *stg = stage[wid];
+
+    f4 acc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+    f4 xa[D], wb[D][2];
+    auto load = [&](int d, int64_t step) {
+        const int64_t k = KS * step;
+        xa[d] = *reinterpret_cast<const f4 *>(ap + k);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            wb[d][i] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(br, boff[i], (uint32_t)(k * ldb * 4), 2));
+    };
+    // a step's B rows transposed into the slice, then each tile's 4 k values
+    // of column r for lane group q; one wave's LDS operations complete in
+    // order, so the slice is rewritten by the next step without a barrier
+    auto consume = [&](const f4 &x, const f4 (&w)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int kr = (lane >> 3) + 8 * i, c = 4 * (lane & 7);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) stg[(c + e) * LP + kr] = w[i][e];
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const f4 b = *reinterpret_cast<const f4 *>(stg + (16 * t + r) * LP + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], b[e], acc[t], 0, 0, 0);
+        }
+    };
+    if (sf > s0) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) load(d, std::min<int64_t>(s0 + d, sf - 1));
+        int64_t s = s0;
+        for (; s + 2 * D <= sf; s += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                consume(xa[d], wb[d]);
+                load(d, s + d + D);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (s + d < sf) consume(xa[d], wb[d]);
+            if (s + d + D < sf) load(d, s + d + D);
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (s + D + d < sf) consume(xa[d], wb[d]);
+    }
+    if (s1 > full && s1 - 1 >= s0) {  // the K tail: k rows past K are zero
+        const int64_t k = KS * full;
+        const f4 z = {0.f, 0.f, 0.f, 0.f};
+        const f4 x = k + 4 * q < K ? *reinterpret_cast<const f4 *>(ap + k) : z;
+        f4 w[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            w[i] = k + (lane >> 3) + 8 * i < K
+                       ? __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    br, boff[i], (uint32_t)(k * ldb * 4), 2))
+                       : z;
+        consume(x, w);
+    }
+    // lane holds D[m = 4q + v][n = r] of each tile
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[wid][t][4 * q + v][r] = acc[t][v];
+    __syncthreads();
+    // thread (t, m, nn) of 2 x 16 x 16 outputs: 4 waves take both tiles in
+    // turn, 8 waves one each
+    const int m = (tid >> 4) & 15, nn = tid & 15;
+    for (int t = tid >> 8; t < 2; t += NW / 4) {
+        const int64_t n = n0 + 16 * t + nn;
+        if (m < M && n < N) {
+            float sum = part[0][t][m][nn];
+#pragma unroll
+            for (int v = 1; v < NW; ++v) sum += part[v][t][m][nn];
+            float *cp = C + (int64_t)m * ldc + n;
+            const float o = alpha * sum;
+            *cp = beta != 0.0f ? o + beta * *cp : o;
+        }
+    }
+}
+
 // Split K: C = alpha * (P_0 + P_1 + ... + P_{S-1}) + beta * C, the partial
 // products P_s ([M, N], N contiguous, P_s at P + s * pstride) added in order.
 constexpr int64_t kSplitMinK = 64;
@@ -641,6 +765,18 @@ extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k
     // kernel, one 16-row tile of B per workgroup, 8 waves while there are
     // fewer than two tiles per CU (else 4); the B range of a workgroup stays
     // under 2 GiB
+    // m <= 16 with B as stored ([k, n]) and at least 256 columns: the skinny
+    // NN kernel, 32 columns per workgroup, 8 waves while there are fewer than
+    // two workgroups per CU (else 4); B's whole range stays under 2 GiB
+    if (fast && !transa && !transb && m <= 16 && n >= 256 && k >= 16 &&
+        ((k - 1) * ldb + n) * 4 < (int64_t(1) << 31) && (16 * ldb) * 4 < (int64_t(1) << 31)) {
+        const int64_t blocks = ceil_div(n, 32);
+        if (blocks >= 2 * cus)
+            sgemm_skinny_nn_kernel<4><<<(unsigned)blocks, 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
+        else
+            sgemm_skinny_nn_kernel<8><<<(unsigned)blocks, 512, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
+        return check_launch(name);
+    }
     if (fast && !transa && transb && m <= 16 && n >= 256 && k >= 32 &&
         (16 * ldb + k) * 4 < (int64_t(1) << 31)) {
         const int64_t tiles = ceil_div(n, 16);

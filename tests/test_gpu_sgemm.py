@@ -69,6 +69,8 @@ def test_sgemm_reference_cases(dev, hip, case):
     (5, 4100, 1056, -1.0, 0.0, 4),       # transb: skinny, padded strides, a ragged last tile
     (3, 8200, 64, 2.0, 1.0, 0),          # transb: skinny, 2 tiles per workgroup, 2 of 4 waves idle
     (7, 260, 4096, 0.5, 0.0, 0),         # transb: skinny, 32 steps per wave (the steady loop)
+    (16, 8200, 2056, 1.0, 0.5, 0),       # B as stored: skinny NN, 4 waves, K tail, ragged last block
+    (9, 300, 100, 2.0, 0.0, 8),          # B as stored: skinny NN, 8 waves, short K, padded strides
 ])
 def test_sgemm_shapes(dev, hip, ta, tb, m, n, k, alpha, beta, pad):
     rng = np.random.default_rng(m * 7 + n * 3 + k + 11 * ta + 13 * tb)
@@ -128,11 +130,12 @@ def test_sgemm_large_against_float64(dev, hip):
 
 def test_sgemm_split_and_skinny_repeatable(dev, hip):
     """The split-K route (fewer tiles than CUs: partial tiles in scratch, summed
-    in a fixed order) and the skinny m <= 16 kernel (waves' partial tiles
-    summed in wave order) give the same bits on every call, and agree with a
-    float64 product within the rounding bound."""
+    in a fixed order) and the skinny m <= 16 kernels for both B layouts
+    (waves' partial tiles summed in wave order) give the same bits on every
+    call, and agree with a float64 product within the rounding bound."""
     rng = np.random.default_rng(77)
-    for (m, n, k, tb) in ((64, 1000, 4128, 0), (64, 1000, 4128, 1), (16, 2000, 4096, 1)):
+    for (m, n, k, tb) in ((64, 1000, 4128, 0), (64, 1000, 4128, 1), (16, 2000, 4096, 1),
+                          (16, 2000, 4096, 0)):
         a = rng.standard_normal(m * k).astype(np.float32)
         b = rng.standard_normal(n * k).astype(np.float32)
         ldb = k if tb else n
