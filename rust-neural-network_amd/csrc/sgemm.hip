@@ -766,15 +766,14 @@ extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k
     // fewer than two tiles per CU (else 4); the B range of a workgroup stays
     // under 2 GiB
     // m <= 16 with B as stored ([k, n]) and at least 256 columns: the skinny
-    // NN kernel, 32 columns per workgroup, 8 waves while there are fewer than
-    // two workgroups per CU (else 4); B's whole range stays under 2 GiB
+    // NN kernel, 32 columns per workgroup over 4 waves (measured, B rotated
+    // past the MALL: 16 x 11008 x 4096 52.5 us against 54.0 with 8 waves and
+    // 54.2 / 57.6 with 2 / 8 steps in flight; 16 x 4096 x 11008 60.9 against
+    // 63.3 with 8 waves); B's whole range stays under 2 GiB
     if (fast && !transa && !transb && m <= 16 && n >= 256 && k >= 16 &&
         ((k - 1) * ldb + n) * 4 < (int64_t(1) << 31) && (16 * ldb) * 4 < (int64_t(1) << 31)) {
-        const int64_t blocks = ceil_div(n, 32);
-        if (blocks >= 2 * cus)
-            sgemm_skinny_nn_kernel<4><<<(unsigned)blocks, 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
-        else
-            sgemm_skinny_nn_kernel<8><<<(unsigned)blocks, 512, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k, alpha, beta);
+        sgemm_skinny_nn_kernel<4><<<(unsigned)ceil_div(n, 32), 256, 0, st>>>(a, lda, b, ldb, c, ldc, (int)m, n, k,
+                                                                        alpha, beta);
         return check_launch(name);
     }
     if (fast && !transa && transb && m <= 16 && n >= 256 && k >= 32 &&

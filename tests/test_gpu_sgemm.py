@@ -69,8 +69,8 @@ def test_sgemm_reference_cases(dev, hip, case):
     (5, 4100, 1056, -1.0, 0.0, 4),       # transb: skinny, padded strides, a ragged last tile
     (3, 8200, 64, 2.0, 1.0, 0),          # transb: skinny, 2 tiles per workgroup, 2 of 4 waves idle
     (7, 260, 4096, 0.5, 0.0, 0),         # transb: skinny, 32 steps per wave (the steady loop)
-    (16, 8200, 2056, 1.0, 0.5, 0),       # B as stored: skinny NN, 4 waves, K tail, ragged last block
-    (9, 300, 100, 2.0, 0.0, 8),          # B as stored: skinny NN, 8 waves, short K, padded strides
+    (16, 8200, 2056, 1.0, 0.5, 0),       # B as stored: skinny NN, K tail, ragged last block
+    (9, 300, 100, 2.0, 0.0, 8),          # B as stored: skinny NN, short K, padded strides
 ])
 def test_sgemm_shapes(dev, hip, ta, tb, m, n, k, alpha, beta, pad):
     rng = np.random.default_rng(m * 7 + n * 3 + k + 11 * ta + 13 * tb)
