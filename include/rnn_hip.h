@@ -250,9 +250,11 @@ int rnn_rotorquant_dequantize(const int8_t *codes, const float *scales,
  * choosing, so results agree with the reference within the usual GEMM
  * rounding bound (|err| <= ~k * 2^-24 * (|alpha| |A||B| + |beta C|)), not bit
  * for bit -- as the reference's own blocked and small-matrix paths do with
- * each other. Shapes with fewer 128 x 128 tiles of C than CUs split K into up
- * to 16 ranges whose partial products (in stream-ordered scratch) are added
- * in a fixed order: the same inputs give the same bits on every call. */
+ * each other. m <= 16 with n >= 256 (decode shapes, either B layout) runs a
+ * kernel that reads B once and sums K in a fixed order; other shapes with
+ * fewer 128 x 128 tiles of C than CUs split K into up to 16 ranges whose
+ * partial products (in stream-ordered scratch) are added in a fixed order:
+ * the same inputs give the same bits on every call. */
 int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k,
               float alpha, const float *a, int64_t lda, const float *b,
               int64_t ldb, float beta, float *c, int64_t ldc, void *stream);
