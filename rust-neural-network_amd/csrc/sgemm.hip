@@ -674,6 +674,36 @@ __global__ __launch_bounds__(64 * NW) void sgemm_skinny_nn_kernel(const float *_
     }
 }
 
+// B [K, N] (row stride ldb) -> Bt [N, K] (contiguous), 64 x 64 tiles through
+// LDS: thread t loads float4 (k row t / 16 + 16 i, columns 4 (t % 16) ..),
+// writes float4 (n row t / 16 + 16 i, k 4 (t % 16) ..). K and N are
+// multiples of 4, so a float4 is wholly inside or outside.
+__global__ __launch_bounds__(256) void sgemm_transpose_kernel(const float *__restrict__ B, int64_t ldb,
+                                                              float *__restrict__ Bt, int64_t K,
+                                                              int64_t N, int tiles_n) {
+    __shared__ float t[64][65];
+    const int tid = threadIdx.x;
+    const int64_t n0 = (int64_t)(blockIdx.x % (unsigned)tiles_n) * 64, k0 = (int64_t)(blockIdx.x / (unsigned)tiles_n) * 64;
+    const int c = 4 * (tid & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int kr = (tid >> 4) + 16 * i;
+        f4 v = {0.f, 0.f, 0.f, 0.f};
+        if (k0 + kr < K && n0 + c < N) v = *reinterpret_cast<const f4 *>(B + (k0 + kr) * ldb + n0 + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[kr][c + e] = v[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int nr = (tid >> 4) + 16 * i;
+        if (n0 + nr < N && k0 + c < K) {
+            const f4 v = {t[c][nr], t[c + 1][nr], t[c + 2][nr], t[c + 3][nr]};
+            *reinterpret_cast<f4 *>(Bt + (n0 + nr) * K + k0 + c) = v;
+        }
+    }
+}
+
 // Split K: C = alpha * (P_0 + P_1 + ... + P_{S-1}) + beta * C, the partial
 // products P_s ([M, N], N contiguous, P_s at P + s * pstride) added in order.
 constexpr int64_t kSplitMinK = 64;
@@ -794,6 +824,26 @@ extern "C" int rnn_sgemm(int transa, int transb, int64_t m, int64_t n, int64_t k
     const int64_t tm = ceil_div(m, kSgBM), tn = ceil_div(n, kSgBN);
     RNN_REQUIRE(tm * tn <= 0x7fffffffLL && tm < 0x7fffffffLL, "%s: too many tiles", name);
     const unsigned grid = (unsigned)(tm * tn);
+    // C = A B with B as stored and at least 2048 rows of A: B is transposed
+    // into stream-ordered scratch and the product runs on the both-K-
+    // contiguous kernel (the K-major B tile's loads cost the NN kernel about
+    // 7%, the transpose reads and writes K N floats once; measured at 4096^3:
+    // 1071 us NN against 993 NT + the transpose)
+    if (!transa && !transb && m >= 2048 && grid >= (unsigned)cus && k % kSgBK == 0 &&
+        k < (int64_t(1) << 22) && lda < (int64_t(1) << 22) && n * k < (int64_t(1) << 31)) {
+        float *bt = nullptr;
+        RNN_TRY(check_hip(hipMallocAsync(reinterpret_cast<void **>(&bt), sizeof(float) * n * k, st), name));
+        const int64_t ttn = ceil_div(n, 64), ttk = ceil_div(k, 64);
+        sgemm_transpose_kernel<<<(unsigned)(ttn * ttk), 256, 0, st>>>(b, ldb, bt, k, n, (int)ttn);
+        int rc = check_launch(name);
+        if (rc == RNN_OK) {
+            sgemm_mfma2_kernel<false, true><<<grid, 256, 0, st>>>(a, lda, bt, k, c, ldc, m, n, k, alpha, beta,
+                                                                 (int)tm, (int)grid, k, 0);
+            rc = check_launch(name);
+        }
+        const int rf = check_hip(hipFreeAsync(bt, st), name);
+        return rc != RNN_OK ? rc : rf;
+    }
     // Fewer tiles than CUs: K is split into S ranges of whole 32-k stages
     // (the last one takes the rest; at least kSplitMinK each, S <= 16), each
     // range's tiles go to stream-ordered scratch, and sgemm_split_sum_kernel

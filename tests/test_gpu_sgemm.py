@@ -143,3 +143,18 @@ def test_sgemm_split_and_skinny_repeatable(dev, hip):
         runs = [run(dev, hip, 0, tb, m, n, k, 1.0, a, k, b, ldb, 0.0, c0, n) for _ in range(3)]
         assert all(np.array_equal(runs[0].view(np.uint32), r.view(np.uint32)) for r in runs[1:])
         check(runs[0], 0, tb, m, n, k, 1.0, a, k, b, ldb, 0.0, c0, n)
+
+
+def test_sgemm_nn_through_transposed_b(dev, hip):
+    """C = A B with B as stored and at least 2048 rows: B is transposed into
+    scratch (64 x 64 tiles, ragged here in both N and K) and the product runs
+    on the both-K-contiguous kernel; padded strides, alpha and beta, within
+    the rounding bound, padding columns of C untouched."""
+    rng = np.random.default_rng(2052)
+    m, n, k, pad = 2048, 2052, 1056, 4
+    lda, ldb, ldc = k + pad, n + pad, n + pad
+    a = rng.standard_normal(m * lda).astype(np.float32)
+    b = rng.standard_normal(k * ldb).astype(np.float32)
+    c0 = rng.standard_normal(m * ldc).astype(np.float32)
+    got = run(dev, hip, 0, 0, m, n, k, 0.75, a, lda, b, ldb, -0.5, c0, ldc)
+    check(got, 0, 0, m, n, k, 0.75, a, lda, b, ldb, -0.5, c0, ldc)
