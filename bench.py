@@ -788,8 +788,8 @@ def bench_sgemm(H, dev, steps):
     return {"m": m, "n": n, "k": k, "trans": "nn", "us": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
             "frac_fp32_mfma_peak": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4),
             "torch_matmul_TFLOP/s": round(tflops_lib, 1), "traffic": traffic_for("f32_sgemm"),
-            "kernel": "sgemm_mfma2_kernel<false,false> (v_mfma_f32_16x16x4f32, 128x128 tiles, "
-                      "both operands as 4-k quads in LDS)",
+            "kernel": "sgemm_transpose_kernel (B [k, n] -> [n, k] in scratch) + sgemm_mfma2_kernel<false,true> "
+                      "(v_mfma_f32_16x16x4f32, 128x128 tiles, both operands as 4-k quads in LDS)",
             "nt": {"us": round(ms_nt * 1e3, 1), "TFLOP/s": round(nt, 1),
                    "frac_fp32_mfma_peak": round(nt / PEAK_FP32_MFMA_TFLOPS, 4),
                    "torch_matmul_TFLOP/s": round(nt_lib, 1),
