@@ -251,7 +251,9 @@ int rnn_rotorquant_dequantize(const int8_t *codes, const float *scales,
  * rounding bound (|err| <= ~k * 2^-24 * (|alpha| |A||B| + |beta C|)), not bit
  * for bit -- as the reference's own blocked and small-matrix paths do with
  * each other. m <= 16 with n >= 256 (decode shapes, either B layout) runs a
- * kernel that reads B once and sums K in a fixed order; other shapes with
+ * kernel that reads B once and sums K in a fixed order; C = A B with B as
+ * stored and m >= 2048 first transposes B into stream-ordered scratch and
+ * runs the kernel for B stored [n, k]; other shapes with
  * fewer 128 x 128 tiles of C than CUs split K into up to 16 ranges whose
  * partial products (in stream-ordered scratch) are added in a fixed order:
  * the same inputs give the same bits on every call. */
