@@ -452,7 +452,7 @@ class QuantizedLinear(Module):
     def __init__(self, weight, bias, in_features, out_features):
         self.weight, self.bias = weight, bias
         self.in_features, self.out_features = in_features, out_features
-        self._workspace = None  # the bf16 MFMA GEMV's split x, made on first use
+        self._workspace = None  # the bf16 MFMA GEMV's split-K partial sums and counters, made on first use
 
     @classmethod
     def from_linear(cls, weight, bias, fmt, group_size):
